@@ -1,0 +1,100 @@
+/*
+ * kushkash_amd.h — C ABI of the MI355X (gfx950) compressed-KV hot path: quantize-and-pack on
+ * write and fused dequant decode attention over int4 / int8 page records.
+ *
+ * Library: kushkash_amd/libkushhip.so (hipcc, --offload-arch=gfx950). These entry points replace
+ * the reference's kernel dispatch (kushkash/_cuda.py:60-103 Kernel(grid, block, *args) launching
+ * Mojo PTX, and kushkash/_ops.py:42-213 Ops). Each argument keeps the meaning of the reference
+ * kernel parameter it replaces; the reference's per-config specialisation (GpuConfig(head_dim,
+ * bits, group, dtype), _build.py:112-149) becomes the leading head_dim / bits / group / dtype
+ * arguments.
+ *
+ * Conventions (reference: _ops.py:6-15, gpu.mojo:1-12):
+ *   - The caller owns every buffer; pointers are device addresses. No entry point allocates,
+ *     synchronizes or checks index values: launches are asynchronous on `stream` (a hipStream_t,
+ *     NULL = default stream) and safe to record into a HIP graph.
+ *   - cache: record of (block b, kv head h) at cache + b*block_stride + h*head_stride (bytes);
+ *     records, block_stride and head_stride must be 16-byte aligned.
+ *   - Record layout [kq 32*DC | vq 32*DC | ks D fp16 | kb D fp16 | vs 32 fp16 | vb 32 fp16],
+ *     DC = D (int8) or D/2 (int4); record bytes = 64*DC + 4*D + 128.
+ *   - tail_k: [slots][hkv][32][D] in dtype, exact K of each sequence's partial page; sequence s
+ *     uses slot tail_idx[s].
+ *   - k, v rows: row r, kv head h at base + r*row_stride + h*D (elements); q, out contiguous
+ *     [n_seqs][hkv*group][D] (q head = kv_head*group + g).
+ *   - block_table: int32 [n_seqs][bt_row_stride]; seq_lens int32 [n_seqs].
+ *   - dtype codes: 0 fp32, 1 fp16, 2 bf16 (for q, k, v, out and tail_k).
+ *   - head_dim 64, 128 or 256; bits 4 or 8; any group >= 1.
+ *
+ * Return values: 0 success; KUSH_EUNSUPPORTED for a head_dim / bits / dtype outside the
+ * supported set (the reference's -1 -> ValueError, _cpu.py:38-40); KUSH_EINVAL for a rejected
+ * argument; KUSH_EHIP for a launch error (the reference's RuntimeError with the driver string,
+ * _cuda.py:39-43). kush_last_error() returns the message of the last failure on this thread.
+ */
+#ifndef KUSHKASH_AMD_H
+#define KUSHKASH_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KUSH_OK 0
+#define KUSH_EUNSUPPORTED (-1)
+#define KUSH_EINVAL (-2)
+#define KUSH_EHIP (-3)
+
+#define KUSH_DTYPE_F32 0
+#define KUSH_DTYPE_F16 1
+#define KUSH_DTYPE_BF16 2
+
+/* One new token per sequence (decode step): row s of k / v goes to position
+ * seq_lens[s] + pos_offset; negative positions (padding rows) are skipped. K goes to the exact
+ * tail and its page is quantized when the token fills it; V is quantized straight into its
+ * record row. advance != 0 stores pos + 1 back into seq_lens[s].
+ * Replaces kush_append (gpu.mojo:207-238) as launched by Ops.append (_ops.py:66-80). */
+int kush_append(int head_dim, int bits, int dtype, const void* k, const void* v, int64_t k_row_stride,
+                int64_t v_row_stride, int32_t* seq_lens, int32_t pos_offset, int32_t advance,
+                const int32_t* tail_idx, void* cache, int64_t block_stride, int64_t head_stride, void* tail_k,
+                const int32_t* block_table, int64_t bt_row_stride, int32_t hkv, int32_t n_seqs, void* stream);
+
+/* Ragged multi-token write, one launch per mode: sequence s owns rows
+ * [query_start_loc[s], query_start_loc[s+1]) at positions ending at seq_lens[s] (already
+ * counting them); job j covers logical page job_page[j] of sequence job_seq[j]. mode 0 writes V
+ * rows and quantizes pages the chunk completes; mode 1 stashes the K rows of still-partial pages
+ * in the tail. Call mode 0 for all jobs, then mode 1, on the same stream.
+ * Replaces kush_write (gpu.mojo:241-276) as launched by Ops.write (_ops.py:82-101). */
+int kush_write(int head_dim, int bits, int dtype, const void* k, const void* v, int64_t k_row_stride,
+               int64_t v_row_stride, const int32_t* query_start_loc, const int32_t* seq_lens,
+               const int32_t* tail_idx, const int32_t* job_seq, const int32_t* job_page, int32_t n_jobs,
+               int32_t mode, void* cache, int64_t block_stride, int64_t head_stride, void* tail_k,
+               const int32_t* block_table, int64_t bt_row_stride, int32_t hkv, void* stream);
+
+/* Decode attention of one query per sequence over its seq_lens[s] cached tokens, softmax scale
+ * `scale`. n_splits == 1 writes out; n_splits > 1 writes per-split partials instead:
+ * part_ml fp32 [n_seqs*hkv*n_splits*group][2] (running max in log2 units, sum) and part_o fp32
+ * [n_seqs*hkv*n_splits*group][head_dim] (unnormalized), to be merged by kush_combine.
+ * Replaces kush_decode_tc / kush_decode (gpu.mojo:566-807, :840-1040) as launched by Ops.decode
+ * (_ops.py:191-211); the partial layout is the reference's `work` layout (_ops.py:204-208). */
+int kush_decode(int head_dim, int bits, int group, int dtype, const void* q, void* out, const void* cache,
+                int64_t block_stride, int64_t head_stride, const void* tail_k, const int32_t* tail_idx,
+                const int32_t* block_table, const int32_t* seq_lens, int64_t bt_row_stride, int32_t hkv,
+                float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t n_seqs, void* stream);
+
+/* Merge kush_decode's split partials into out [n_seqs][hkv*group][head_dim].
+ * Replaces kush_combine (gpu.mojo:469-491) as launched by Ops.decode (_ops.py:212-213). */
+int kush_combine(int head_dim, int group, int dtype, void* out, const float* part_ml, const float* part_o,
+                 int32_t n_splits, int32_t hkv, int32_t n_seqs, void* stream);
+
+/* Message of the last failing call on this thread ("" if none). No reference counterpart: the
+ * reference raises the driver's error string directly (_cuda.py:39-43). */
+const char* kush_last_error(void);
+
+/* ABI revision of this header (1). No reference counterpart. */
+int kush_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KUSHKASH_AMD_H */

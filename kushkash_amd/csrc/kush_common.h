@@ -1,0 +1,137 @@
+// Shared definitions for the gfx950 kernels of the compressed-KV hot path: the page-record
+// format (kushkash/kush/quant.mojo:16-87), the quantization arithmetic (quant.mojo:25-50), input
+// dtype conversions and wave64 reductions.
+//
+// Page record of one (block, kv head), D channels, BITS in {4, 8}, DC = row bytes:
+//   [ kq: 32*DC | vq: 32*DC | ks: D fp16 | kb: D fp16 | vs: 32 fp16 | vb: 32 fp16 ]
+// int4 row byte j holds the code of dim j (low nibble) and of dim j + D/2 (high nibble).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "kushkash_amd.h"   // the C ABI these sources implement
+
+// Error reporting shared by the C entry points (kush_capi.hip): records a message for
+// kush_last_error() and returns code.
+int kush_fail(int code, const char* fmt, ...);
+int kush_check_launch(const char* what);
+
+namespace kush {
+
+constexpr int PAGE = 32;
+constexpr int WAVE = 64;
+
+template <int D, int BITS>
+struct Fmt {
+    static_assert(D == 64 || D == 128 || D == 256, "head_dim must be 64, 128 or 256");
+    static_assert(BITS == 4 || BITS == 8, "bits must be 4 or 8");
+    static constexpr int DC = BITS == 8 ? D : D / 2;   // bytes per token row
+    static constexpr int OFF_VQ = PAGE * DC;
+    static constexpr int OFF_KS = 2 * PAGE * DC;
+    static constexpr int OFF_KB = OFF_KS + 2 * D;
+    static constexpr int OFF_VS = OFF_KS + 4 * D;
+    static constexpr int OFF_VB = OFF_VS + 2 * PAGE;
+    static constexpr int REC = OFF_VB + 2 * PAGE;       // record bytes, a multiple of 16
+    static constexpr int HALF = 1 << (BITS - 1);
+    static_assert(REC % 16 == 0, "records must stay 16-byte aligned");
+};
+
+// ------------------------------------------------------------------ input element types
+// The kernels take q, k, v, out and the exact K tail in one of three dtypes.
+struct bf16_t {
+    uint16_t u;
+};
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(_Float16 x) { return (float)x; }
+__device__ __forceinline__ float to_f32(bf16_t x) { return __uint_as_float((uint32_t)x.u << 16); }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x);
+template <>
+__device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ _Float16 from_f32<_Float16>(float x) { return (_Float16)x; }   // RNE
+template <>
+__device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return bf16_t{(uint16_t)((u >> 16) | 0x40u)};   // quiet NaN
+    u += 0x7fffu + ((u >> 16) & 1u);                                                     // RNE
+    return bf16_t{(uint16_t)(u >> 16)};
+}
+
+__device__ __forceinline__ uint16_t f16_bits(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+__device__ __forceinline__ float f16_val(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
+
+// ------------------------------------------------------------------ quantization (quant.mojo:25-50)
+// These must round exactly like the reference CPU path: IEEE fp32 division (the library is built
+// with -fhip-fp32-correctly-rounded-divide-sqrt and without fast-math), RNE to fp16, codes
+// against the fp16-rounded scale and bias, round half to even.
+#pragma clang fp contract(off)
+
+template <int BITS>
+__device__ __forceinline__ void qparams(float mn, float mx, float& s, float& b, float& inv) {
+    constexpr float LEVELS = float((1 << BITS) - 1);
+    constexpr float HALF = float(1 << (BITS - 1));
+    s = (float)(_Float16)((mx - mn) / LEVELS);
+    b = (float)(_Float16)(mn + s * HALF);
+    inv = s > 0.0f ? 1.0f / s : 0.0f;
+}
+
+template <int BITS>
+__device__ __forceinline__ int qcode(float x, float b, float inv) {
+    constexpr float HALF = float(1 << (BITS - 1));
+    float r = __builtin_rintf((x - b) * inv);
+    r = __builtin_fminf(__builtin_fmaxf(r, -HALF), HALF - 1.0f);
+    return (int)r;
+}
+
+__device__ __forceinline__ uint8_t pack4(int lo, int hi) { return (uint8_t)((lo & 0xF) | ((hi & 0xF) << 4)); }
+
+#pragma clang fp contract(on)
+
+// ------------------------------------------------------------------ wave64 reductions
+__device__ __forceinline__ float wave_min(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x = __builtin_fminf(x, __shfl_xor(x, o, WAVE));
+    return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x = __builtin_fmaxf(x, __shfl_xor(x, o, WAVE));
+    return x;
+}
+
+// ------------------------------------------------------------------ shape dispatch
+template <int V>
+using ic = std::integral_constant<int, V>;
+
+template <typename Fn>
+static inline int dispatch_shape(int D, int bits, int dtype, const char* what, Fn&& fn) {
+    auto by_dtype = [&](auto dd, auto bb) -> int {
+        switch (dtype) {
+            case 0: return fn(dd, bb, float{});
+            case 1: return fn(dd, bb, _Float16{});
+            case 2: return fn(dd, bb, bf16_t{});
+        }
+        return kush_fail(-1, "%s: unsupported dtype code %d (0 fp32, 1 fp16, 2 bf16)", what, dtype);
+    };
+    auto by_bits = [&](auto dd) -> int {
+        if (bits == 4) return by_dtype(dd, ic<4>{});
+        if (bits == 8) return by_dtype(dd, ic<8>{});
+        return kush_fail(-1, "%s: unsupported bits %d (4 or 8)", what, bits);
+    };
+    switch (D) {
+        case 64: return by_bits(ic<64>{});
+        case 128: return by_bits(ic<128>{});
+        case 256: return by_bits(ic<256>{});
+    }
+    return kush_fail(-1, "%s: unsupported head_dim %d (64, 128 or 256)", what, D);
+}
+
+}  // namespace kush
+

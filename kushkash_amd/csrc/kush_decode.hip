@@ -1,0 +1,473 @@
+// Fused dequant decode attention over int4/int8 page records for gfx950 (CDNA4), with split-K
+// partials and a log-sum-exp combine. Contract: kushkash/kush/gpu.mojo:566-807 (decode),
+// :418-491 (split ranges, merge, combine), kushkash/_ops.py:182-213 (launch), arithmetic of the
+// reference CPU path kushkash/kush/cpu.mojo:320-451.
+//
+// Mapping onto CDNA4. One workgroup = NW waves for one (sequence, kv head, split, 16-head
+// chunk); its waves take the split's pages round-robin, each keeping its own online-softmax
+// state, and merge through LDS at the end. Per page a wave:
+//   1. loads its K code slice straight into registers (lane (t, q): row t of a 16-token tile,
+//      bytes [q*DC/4, (q+1)*DC/4): the 64 lanes read 16 contiguous rows) and copies the V codes
+//      and the page's scales / biases into a wave-private LDS stage with 16-byte loads;
+//   2. turns codes into exact fp16 with v_perm (byte under the fp16 exponent of 1024) and one
+//      packed subtract, and computes S^T = K . Q'^T on MFMA 16x16x32 f16, where
+//      Q' = fp16(q * sm * log2 e) * k_scale (fp16) and the K bias dot stays fp32 (v_dot2 on a
+//      hi/lo fp16 split of q);
+//   3. runs a page-granular online softmax in base 2 (wave shuffles over the 4 lane groups);
+//   4. reads V codes column-wise from LDS (8 tokens per lane) into V^T operands and
+//      accumulates O^T += V^T . P'^T on MFMA, with P' = e * v_scale in fp16 and the V bias
+//      folded into one scalar per head.
+// The partial last page takes K from the exact tail (fp32 dot products) and V rows from its
+// record, masked beyond the tail length.
+//
+// MFMA 16x16x32 f16 operand layout used throughout (lane l, r = l % 16, q = l / 16):
+//   A: row r, 8 contraction slots of lane group q;  B: column r, the same 8 slots;
+//   C: rows 4q .. 4q+3 of column r.
+// Which physical dim or token a slot stands for is chosen here (kdim, tok), identically for A
+// and B, so only the C layout is relied upon.
+#include "kush_common.h"
+
+namespace kush {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr float LOG2E = 1.4426950408889634f;
+
+__device__ __forceinline__ h2 as_h2(uint32_t x) { return __builtin_bit_cast(h2, x); }
+
+// Four two's-complement nibble codes per byte pair of w -> exact fp16. Slots 0-3: low nibbles of
+// bytes 0-3, slots 4-7: high nibbles. n ^ 8 = c + 8 for a signed nibble c; placed under the fp16
+// exponent of 1024 it reads 1024 + c + 8, and one packed subtract leaves c.
+__device__ __forceinline__ h8 int4_codes(uint32_t w) {
+    const uint32_t x = w ^ 0x88888888u;
+    const uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
+    const h2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    const h2 a = as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u)) + off;
+    const h2 b = as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u)) + off;
+    const h2 c = as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u)) + off;
+    const h2 d = as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u)) + off;
+    return h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// Eight signed int8 codes (two words) -> exact fp16 (c + 128 under the exponent of 1024).
+__device__ __forceinline__ h8 int8_codes(uint32_t w0, uint32_t w1) {
+    const uint32_t x0 = w0 ^ 0x80808080u, x1 = w1 ^ 0x80808080u;
+    const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const h2 a = as_h2(__builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u)) + off;
+    const h2 b = as_h2(__builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u)) + off;
+    const h2 c = as_h2(__builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u)) + off;
+    const h2 d = as_h2(__builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u)) + off;
+    return h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+__device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+
+// Physical dim of contraction slot j of lane group q in K-step kk (QK^T). int4: the lane's 16-byte
+// slice of a row holds dims [q D/8, (q+1) D/8) in low nibbles and the same + D/2 in high nibbles;
+// K-step kk takes bytes 4kk..4kk+3 of it. int8: dims q D/4 + 8 kk + j.
+template <int D, int BITS>
+__device__ __forceinline__ int kdim(int kk, int q, int j) {
+    if constexpr (BITS == 4)
+        return (j < 4 ? 0 : D / 2) + q * (D / 8) + 4 * kk + (j & 3);
+    else
+        return q * (D / 4) + 8 * kk + j;
+}
+
+// Token of slot j of lane group q in the PV contraction: the token the QK^T accumulators of lane
+// group q hold in register j % 4 of tile j / 4.
+__device__ __forceinline__ int tok(int q, int j) { return 16 * (j >> 2) + 4 * q + (j & 3); }
+
+template <int D, int BITS>
+struct Stage {                                     // wave-private LDS copy of a record's tail part
+    using F = Fmt<D, BITS>;
+    static constexpr int BYTES = F::REC - F::OFF_VQ;   // V codes + ks + kb + vs + vb
+    static constexpr int CHUNKS = BYTES / 16;
+    static constexpr int KS = F::OFF_KS - F::OFF_VQ;
+    static constexpr int KB = F::OFF_KB - F::OFF_VQ;
+    static constexpr int VS = F::OFF_VS - F::OFF_VQ;
+    static constexpr int VB = F::OFF_VB - F::OFF_VQ;
+};
+
+template <int D, int BITS>
+__device__ __forceinline__ void stage_record(const uint8_t* __restrict__ rec, uint8_t* st, int lane) {
+    using F = Fmt<D, BITS>;
+    using S = Stage<D, BITS>;
+    const uint4* src = reinterpret_cast<const uint4*>(rec + F::OFF_VQ);
+    uint4* dst = reinterpret_cast<uint4*>(st);
+#pragma unroll
+    for (int i = 0; i < (S::CHUNKS + WAVE - 1) / WAVE; ++i) {
+        const int c = lane + WAVE * i;
+        if (c < S::CHUNKS) dst[c] = src[c];
+    }
+}
+
+// Softmax update of one page (scores x in log2 units, tokens tok(q, j); tokens >= valid masked)
+// and its PV accumulation from the staged V codes.
+template <int D, int BITS>
+__device__ __forceinline__ void consume_page(const uint8_t* st, f4 (&o)[D / 16], const float (&x)[8], int valid,
+                                             float& m_run, float& l_run, float& vb_run, int r16, int q) {
+    using F = Fmt<D, BITS>;
+    using S = Stage<D, BITS>;
+    float pm = x[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) pm = __builtin_fmaxf(pm, x[j]);
+    pm = __builtin_fmaxf(pm, __shfl_xor(pm, 16, WAVE));
+    pm = __builtin_fmaxf(pm, __shfl_xor(pm, 32, WAVE));
+    const float m_new = __builtin_fmaxf(m_run, pm);
+    const float corr = __builtin_amdgcn_exp2f(m_run - m_new);   // first page: exp2(-inf) = 0
+
+    const h4v vs0 = *reinterpret_cast<const h4v*>(st + S::VS + 8 * q);
+    const h4v vs1 = *reinterpret_cast<const h4v*>(st + S::VS + 32 + 8 * q);
+    const h4v vb0 = *reinterpret_cast<const h4v*>(st + S::VB + 8 * q);
+    const h4v vb1 = *reinterpret_cast<const h4v*>(st + S::VB + 32 + 8 * q);
+    float lsum = 0.0f, vbsum = 0.0f;
+    h8 pw;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const bool ok = tok(q, j) < valid;
+        const float vsj = (float)(j < 4 ? vs0[j] : vs1[j - 4]);
+        const float vbj = (float)(j < 4 ? vb0[j] : vb1[j - 4]);
+        const float e = ok ? __builtin_amdgcn_exp2f(x[j] - m_new) : 0.0f;
+        lsum += e;
+        vbsum += ok ? e * vbj : 0.0f;
+        pw[j] = (_Float16)(ok ? e * vsj : 0.0f);
+    }
+    l_run = l_run * corr + lsum;
+    vb_run = vb_run * corr + vbsum;
+    m_run = m_new;
+    if (corr != 1.0f) {
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) o[dt] *= corr;
+    }
+
+    // V^T operands: byte column c of the 8 tokens of this lane group
+    constexpr int NCOL = BITS == 4 ? D / 32 : D / 16;
+#pragma unroll
+    for (int ct = 0; ct < NCOL; ++ct) {
+        const uint8_t* col = st + 16 * ct + r16;
+        uint32_t P[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            P[k] = (uint32_t)col[tok(q, 2 * k) * F::DC] | ((uint32_t)col[tok(q, 2 * k + 1) * F::DC] << 16);
+        if constexpr (BITS == 4) {
+            const h2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+            h8 lo, hi;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t xx = P[k] ^ 0x00880088u;
+                const h2 l2 = as_h2((xx & 0x000F000Fu) | 0x64006400u) + off;
+                const h2 u2 = as_h2(((xx >> 4) & 0x000F000Fu) | 0x64006400u) + off;
+                lo[2 * k] = l2[0];
+                lo[2 * k + 1] = l2[1];
+                hi[2 * k] = u2[0];
+                hi[2 * k + 1] = u2[1];
+            }
+            o[ct] = mfma16(lo, pw, o[ct]);
+            o[ct + D / 32] = mfma16(hi, pw, o[ct + D / 32]);
+        } else {
+            const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+            h8 vv;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const h2 v2 = as_h2((P[k] ^ 0x00800080u) | 0x64006400u) + off;
+                vv[2 * k] = v2[0];
+                vv[2 * k + 1] = v2[1];
+            }
+            o[ct] = mfma16(vv, pw, o[ct]);
+        }
+    }
+}
+
+// grid (S, Hkv, n_splits * ceil(G / 16)), block NW * 64.
+template <int D, int BITS, typename IN, int NW>
+__global__ __launch_bounds__(NW * WAVE) void decode_kernel(
+    const IN* __restrict__ qg, IN* __restrict__ out, const uint8_t* __restrict__ cache, int64_t bs, int64_t hs,
+    const IN* __restrict__ tail_k, const int32_t* __restrict__ tail_idx, const int32_t* __restrict__ block_table,
+    const int32_t* __restrict__ seq_lens, int64_t bt_stride, int H, int G, float sm_log2, int NS,
+    float* __restrict__ part_ml, float* __restrict__ part_o) {
+    using F = Fmt<D, BITS>;
+    using S = Stage<D, BITS>;
+    constexpr int KSTEPS = D / 32;
+    constexpr int DT = D / 16;
+    constexpr int KBYTES = F::DC / 4;                // K code bytes per lane per 16-token tile
+    constexpr int KW = KBYTES / 4;
+    constexpr int STAGE = (S::BYTES + 15) / 16 * 16;
+
+    __shared__ __align__(16) uint8_t stage_all[NW * STAGE];
+    __shared__ __align__(16) float qs_l[16 * D];     // q * sm * log2e for the exact-K tail; then merge buffer
+    __shared__ float sc_l[16 * PAGE];                // tail scores
+    __shared__ float m_l[NW * 16], l_l[NW * 16];
+
+    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+    const int r16 = lane & 15, q = lane >> 4;
+    const int s = blockIdx.x, h = blockIdx.y;
+    const int z = blockIdx.z % NS, g0 = (blockIdx.z / NS) * 16;
+    const int Gc = min(16, G - g0);
+
+    const int n = seq_lens[s];
+    const int full = n / PAGE, tail_n = n % PAGE;
+    const int pps = (full + NS - 1) / NS;
+    const int p0 = min(full, z * pps), p1 = min(full, p0 + pps);
+    const int32_t* bt = block_table + (int64_t)s * bt_stride;
+    const uint8_t* head_base = cache + (int64_t)h * hs;
+    const int64_t qbase = ((int64_t)s * H + h) * G * D + (int64_t)g0 * D;
+    uint8_t* st = stage_all + w * STAGE;
+
+    // this lane's q head (B column r16) over its contraction dims, as an fp16 hi / lo pair
+    const bool gv = r16 < Gc;
+    h8 qh[KSTEPS], ql[KSTEPS];
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float xq = gv ? to_f32(qg[qbase + (int64_t)r16 * D + kdim<D, BITS>(kk, q, j)]) * sm_log2 : 0.0f;
+            const _Float16 hi = (_Float16)xq;
+            qh[kk][j] = hi;
+            ql[kk][j] = (_Float16)(xq - (float)hi);
+        }
+
+    f4 o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -__builtin_inff(), l_run = 0.0f, vb_run = 0.0f;
+
+    for (int p = p0 + w; p < p1; p += NW) {
+        const uint8_t* rec = head_base + (int64_t)bt[p] * bs;
+        uint32_t kw[2][KW];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const uint8_t* src = rec + (16 * tt + r16) * F::DC + q * KBYTES;
+            if constexpr (KBYTES == 8) {
+                const uint2 v2 = *reinterpret_cast<const uint2*>(src);
+                kw[tt][0] = v2.x;
+                kw[tt][1] = v2.y;
+            } else {
+#pragma unroll
+                for (int c = 0; c < KBYTES / 16; ++c) {
+                    const uint4 v4 = reinterpret_cast<const uint4*>(src)[c];
+                    kw[tt][4 * c + 0] = v4.x;
+                    kw[tt][4 * c + 1] = v4.y;
+                    kw[tt][4 * c + 2] = v4.z;
+                    kw[tt][4 * c + 3] = v4.w;
+                }
+            }
+        }
+        stage_record<D, BITS>(rec, st, lane);
+
+        f4 sacc[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};
+        float kbs = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < KSTEPS; ++kk) {
+            h8 ks8, kb8;
+            if constexpr (BITS == 4) {
+                const int d0 = q * (D / 8) + 4 * kk;
+                const h4v a = *reinterpret_cast<const h4v*>(st + S::KS + 2 * d0);
+                const h4v b = *reinterpret_cast<const h4v*>(st + S::KS + 2 * (d0 + D / 2));
+                const h4v c = *reinterpret_cast<const h4v*>(st + S::KB + 2 * d0);
+                const h4v d = *reinterpret_cast<const h4v*>(st + S::KB + 2 * (d0 + D / 2));
+                ks8 = h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+                kb8 = h8{c[0], c[1], c[2], c[3], d[0], d[1], d[2], d[3]};
+            } else {
+                const int d0 = q * (D / 4) + 8 * kk;
+                ks8 = *reinterpret_cast<const h8*>(st + S::KS + 2 * d0);
+                kb8 = *reinterpret_cast<const h8*>(st + S::KB + 2 * d0);
+            }
+            const h8 qp = qh[kk] * ks8;                       // fp16 multiply, as the reference TC path
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const h2 kb2 = {kb8[2 * e], kb8[2 * e + 1]};
+                kbs = __builtin_amdgcn_fdot2(h2{qh[kk][2 * e], qh[kk][2 * e + 1]}, kb2, kbs, false);
+                kbs = __builtin_amdgcn_fdot2(h2{ql[kk][2 * e], ql[kk][2 * e + 1]}, kb2, kbs, false);
+            }
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                h8 a;
+                if constexpr (BITS == 4)
+                    a = int4_codes(kw[tt][kk]);
+                else
+                    a = int8_codes(kw[tt][2 * kk], kw[tt][2 * kk + 1]);
+                sacc[tt] = mfma16(a, qp, sacc[tt]);
+            }
+        }
+        kbs += __shfl_xor(kbs, 16, WAVE);
+        kbs += __shfl_xor(kbs, 32, WAVE);
+        float x[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = sacc[j >> 2][j & 3] + kbs;
+        consume_page<D, BITS>(st, o, x, PAGE, m_run, l_run, vb_run, r16, q);
+    }
+
+    // partial last page: exact K from the tail, V rows from its record (last split only)
+    if (tail_n > 0 && z == NS - 1) {
+        for (int i = threadIdx.x; i < 16 * D; i += NW * WAVE) {
+            const int gg = i / D;
+            qs_l[i] = gg < Gc ? to_f32(qg[qbase + i]) * sm_log2 : 0.0f;
+        }
+        __syncthreads();
+        if (w == (p1 - p0) % NW) {
+            const IN* tk = tail_k + ((int64_t)tail_idx[s] * H + h) * PAGE * D;
+            const int t = lane & 31, hf = lane >> 5;
+            float acc[16];
+#pragma unroll
+            for (int g = 0; g < 16; ++g) acc[g] = 0.0f;
+            if (t < tail_n) {
+                for (int d = hf * (D / 2); d < (hf + 1) * (D / 2); d += 4) {
+                    const float k0 = to_f32(tk[t * D + d]), k1 = to_f32(tk[t * D + d + 1]);
+                    const float k2 = to_f32(tk[t * D + d + 2]), k3 = to_f32(tk[t * D + d + 3]);
+#pragma unroll
+                    for (int g = 0; g < 16; ++g) {
+                        const float4 q4 = *reinterpret_cast<const float4*>(&qs_l[g * D + d]);
+                        acc[g] += q4.x * k0 + q4.y * k1 + q4.z * k2 + q4.w * k3;
+                    }
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < 16; ++g) {
+                acc[g] += __shfl_xor(acc[g], 32, WAVE);
+                if (hf == 0) sc_l[g * PAGE + t] = t < tail_n ? acc[g] : -__builtin_inff();
+            }
+            stage_record<D, BITS>(head_base + (int64_t)bt[full] * bs, st, lane);
+            float x[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = sc_l[r16 * PAGE + tok(q, j)];
+            consume_page<D, BITS>(st, o, x, tail_n, m_run, l_run, vb_run, r16, q);
+        }
+    }
+
+    // merge the waves: every wave rescales to the workgroup max and adds into LDS in turn
+    l_run += __shfl_xor(l_run, 16, WAVE);
+    l_run += __shfl_xor(l_run, 32, WAVE);
+    vb_run += __shfl_xor(vb_run, 16, WAVE);
+    vb_run += __shfl_xor(vb_run, 32, WAVE);
+    __syncthreads();
+    if (q == 0) {
+        m_l[w * 16 + r16] = m_run;
+        l_l[w * 16 + r16] = l_run;
+    }
+    __syncthreads();
+    float M = -__builtin_inff();
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) M = __builtin_fmaxf(M, m_l[ww * 16 + r16]);
+    const float f = m_run == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m_run - M);
+    float* mbuf = qs_l;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) {
+        if (w == ww) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int idx = r16 * D + 16 * dt + 4 * q + i;
+                    const float val = (o[dt][i] + vb_run) * f;
+                    mbuf[idx] = ww == 0 ? val : mbuf[idx] + val;
+                }
+        }
+        __syncthreads();
+    }
+    for (int i = threadIdx.x; i < Gc * D; i += NW * WAVE) {
+        const int g = i / D, d = i % D;
+        float Mg = -__builtin_inff();
+#pragma unroll
+        for (int ww = 0; ww < NW; ++ww) Mg = __builtin_fmaxf(Mg, m_l[ww * 16 + g]);
+        float L = 0.0f;
+        if (Mg > -__builtin_inff()) {
+#pragma unroll
+            for (int ww = 0; ww < NW; ++ww) {
+                const float mw = m_l[ww * 16 + g];
+                if (mw > -__builtin_inff()) L += l_l[ww * 16 + g] * __builtin_amdgcn_exp2f(mw - Mg);
+            }
+        }
+        const float val = mbuf[g * D + d];
+        if (NS == 1) {
+            out[qbase + i] = from_f32<IN>(L > 0.0f ? val / L : 0.0f);
+        } else {
+            const int64_t pb = (((int64_t)s * H + h) * NS + z) * G + g0 + g;
+            part_o[pb * D + d] = val;
+            if (d == 0) {
+                part_ml[2 * pb] = Mg;
+                part_ml[2 * pb + 1] = L;
+            }
+        }
+    }
+}
+
+// grid (S, Hkv), block 256: merge split-K partials (M, L, unnormalized O) into the output.
+// M is in log2 units. Splits with no tokens (M = -inf) are skipped (gpu.mojo:469-491).
+template <typename IN>
+__global__ __launch_bounds__(256) void combine_kernel(IN* __restrict__ out, const float* __restrict__ part_ml,
+                                                      const float* __restrict__ part_o, int NS, int H, int G, int D) {
+    const int s = blockIdx.x, h = blockIdx.y;
+    const int64_t base = ((int64_t)s * H + h) * NS;
+    for (int i = threadIdx.x; i < G * D; i += 256) {
+        const int g = i / D, d = i % D;
+        float M = -__builtin_inff();
+        for (int z = 0; z < NS; ++z) M = __builtin_fmaxf(M, part_ml[2 * ((base + z) * G + g)]);
+        float L = 0.0f, o = 0.0f;
+        if (M > -__builtin_inff()) {
+            for (int z = 0; z < NS; ++z) {
+                const int64_t pb = (base + z) * G + g;
+                const float mz = part_ml[2 * pb];
+                if (mz > -__builtin_inff()) {
+                    const float fz = __builtin_amdgcn_exp2f(mz - M);
+                    L += part_ml[2 * pb + 1] * fz;
+                    o += fz * part_o[pb * D + d];
+                }
+            }
+        }
+        out[((int64_t)s * H + h) * G * D + i] = from_f32<IN>(L > 0.0f ? o / L : 0.0f);
+    }
+}
+
+constexpr int DECODE_WAVES = 4;
+
+}  // namespace kush
+
+using namespace kush;
+
+extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const void* q, void* out, const void* cache,
+                           int64_t block_stride, int64_t head_stride, const void* tail_k, const int32_t* tail_idx,
+                           const int32_t* block_table, const int32_t* seq_lens, int64_t bt_stride, int32_t hkv,
+                           float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t n_seqs,
+                           void* stream) {
+    if (n_seqs < 0 || hkv <= 0 || group <= 0 || n_splits <= 0)
+        return kush_fail(-2, "kush_decode: bad n_seqs %d / hkv %d / group %d / n_splits %d", n_seqs, hkv, group,
+                         n_splits);
+    if (n_splits > 1 && (part_ml == nullptr || part_o == nullptr))
+        return kush_fail(-2, "kush_decode: n_splits %d needs the partial buffers", n_splits);
+    if (((uintptr_t)cache | (uint64_t)block_stride | (uint64_t)head_stride) & 15)
+        return kush_fail(-2, "kush_decode: cache records must be 16-byte aligned");
+    const int n_gc = (group + 15) / 16;
+    if ((int64_t)n_splits * n_gc > 65535) return kush_fail(-2, "kush_decode: n_splits %d too large", n_splits);
+    const float sm_log2 = (float)((double)scale * 1.4426950408889634);
+    return dispatch_shape(head_dim, bits, dtype, "kush_decode", [&](auto dd, auto bb, auto in) -> int {
+        constexpr int D = decltype(dd)::value, BITS = decltype(bb)::value;
+        using IN = decltype(in);
+        if (n_seqs == 0) return 0;
+        decode_kernel<D, BITS, IN, DECODE_WAVES>
+            <<<dim3(n_seqs, hkv, n_splits * n_gc), dim3(DECODE_WAVES * WAVE), 0, (hipStream_t)stream>>>(
+                (const IN*)q, (IN*)out, (const uint8_t*)cache, block_stride, head_stride, (const IN*)tail_k, tail_idx,
+                block_table, seq_lens, bt_stride, hkv, group, sm_log2, n_splits, part_ml, part_o);
+        return kush_check_launch("kush_decode");
+    });
+}
+
+extern "C" int kush_combine(int head_dim, int group, int dtype, void* out, const float* part_ml, const float* part_o,
+                            int32_t n_splits, int32_t hkv, int32_t n_seqs, void* stream) {
+    if (n_seqs < 0 || hkv <= 0 || group <= 0 || n_splits <= 0)
+        return kush_fail(-2, "kush_combine: bad arguments");
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+        return kush_fail(-1, "kush_combine: unsupported head_dim %d", head_dim);
+    if (n_seqs == 0) return 0;
+    const dim3 grid(n_seqs, hkv);
+    hipStream_t st = (hipStream_t)stream;
+    switch (dtype) {
+        case 0: combine_kernel<float><<<grid, 256, 0, st>>>((float*)out, part_ml, part_o, n_splits, hkv, group, head_dim); break;
+        case 1: combine_kernel<_Float16><<<grid, 256, 0, st>>>((_Float16*)out, part_ml, part_o, n_splits, hkv, group, head_dim); break;
+        case 2: combine_kernel<bf16_t><<<grid, 256, 0, st>>>((bf16_t*)out, part_ml, part_o, n_splits, hkv, group, head_dim); break;
+        default: return kush_fail(-1, "kush_combine: unsupported dtype code %d", dtype);
+    }
+    return kush_check_launch("kush_combine");
+}

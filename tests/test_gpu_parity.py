@@ -1,0 +1,143 @@
+"""GPU parity against the CPU oracle (needs an MI355X): packed records and K tails bit-exact, decode
+outputs within tolerance. Mirrors the reference's tests/test_gpu.py (test_pages_match_cpu,
+test_decode_matches_reference, test_split_k_long_context) with the oracle as the CPU side."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+import kushkash_amd as kk
+from _harness import oracle_cache, out_tol
+from kushkash_amd._ops import PAGE
+from oracle.cpu_ops import OracleOps
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _fill(c, K, V, bulk: int) -> None:
+    """Bulk write of the first `bulk` tokens, then one append per token (the reference's pattern)."""
+    T = K.shape[2]
+    if bulk:
+        c.write(0, K[:, :, :bulk], V[:, :, :bulk])
+    for t in range(bulk, T):
+        c.write(0, K[:, :, t:t + 1], V[:, :, t:t + 1])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_pages_match_oracle(D, bits, dtype):
+    """Record bytes and K tails of bulk writes + token appends are identical to the oracle's
+    (reference: tests/test_gpu.py:14-33); K channel 1 carries a +50 offset."""
+    torch.manual_seed(D + bits)
+    B, H, T = 2, 2, 3 * PAGE + 5
+    K, V = torch.randn(B, H, T, D) * 2, torch.randn(B, H, T, D)
+    K[..., 1] += 50
+    K, V = K.to(dtype), V.to(dtype)
+    g = kk.KushCache(1, H, H, D, batch_size=B, bits=bits, device=DEV, dtype=dtype, rotate=False)
+    _fill(g, K.to(DEV), V.to(DEV), 40)
+    c = oracle_cache(1, H, H, D, batch_size=B, bits=bits, rotate=False)
+    _fill(c, K.float(), V.float(), 40)
+    n = -(-T // PAGE) * B
+    x, y = g.pool[0, :n].cpu(), c.pool[0, :n]
+    assert torch.equal(x, y), f"{(x != y).float().mean():.2e} of record bytes differ"
+    r = T % PAGE
+    assert torch.equal(g.tail_k[0, :, :, :r].float().cpu(), c.tail_k[0, :, :, :r])
+    assert torch.equal(g.seq_lens.cpu(), c.seq_lens)
+
+
+def oracle_decode(c: kk.KushCache, layer: int, q: torch.Tensor) -> torch.Tensor:
+    """The oracle's decode over the GPU cache's own records (copied to the CPU), fp32."""
+    ops = OracleOps("cpu", c.D, c.bits, c.G)
+    out = torch.empty(q.shape, dtype=torch.float32)
+    ops.decode(q.float().cpu().contiguous(), out, c.pool[layer].cpu(), c.block_table.cpu(),
+               c.seq_lens[layer].cpu(), c.tail_idx.cpu(), c.tail_k[layer].float().cpu(), c.scale)
+    return out
+
+
+CASES = [  # (D, bits, G, dtype, B, N): the reference's CASES (tests/test_gpu.py:36-43)
+    (128, 4, 4, torch.float16, 4, 1000), (128, 8, 4, torch.bfloat16, 2, 777),
+    (128, 4, 7, torch.bfloat16, 1, 8192), (128, 4, 8, torch.float16, 3, 300),
+    (128, 4, 12, torch.float16, 2, 500),
+    (64, 4, 4, torch.bfloat16, 2, 2000), (64, 8, 2, torch.float16, 1, 70),
+    (256, 4, 2, torch.float16, 2, 1500), (256, 8, 8, torch.bfloat16, 1, 4100),
+    (128, 4, 4, torch.float32, 1, 33), (128, 4, 4, torch.float16, 1, 31),
+    (128, 8, 20, torch.bfloat16, 2, 200),                                      # G > 16: two head chunks
+]
+
+
+@pytest.mark.parametrize("D,bits,G,dtype,B,N", CASES)
+def test_decode_matches_oracle(D, bits, G, dtype, B, N):
+    """Decode after every one of the last 8 appends: against the oracle on the same records
+    (max-abs 2e-3 + output rounding) and against SDPA over the dequantized cache (rel-norm, the
+    reference's tolerances, tests/test_gpu.py:61)."""
+    torch.manual_seed(N)
+    H = 2
+    c = kk.KushCache(2, H, H * G, D, batch_size=B, bits=bits, device=DEV, dtype=dtype, rotate=False)
+    K = torch.randn(B, H, N, D, device=DEV, dtype=dtype)
+    V = torch.randn(B, H, N, D, device=DEV, dtype=dtype)
+    if N > 8:
+        c.write(1, K[:, :, :N - 8], V[:, :, :N - 8])
+    for t in range(max(0, N - 8), N):
+        c.write(1, K[:, :, t:t + 1], V[:, :, t:t + 1])
+        q = torch.randn(B, H * G, D, device=DEV, dtype=dtype)
+        out = c.attend(1, q).float().cpu()
+        want = oracle_decode(c, 1, q)
+        err = (out - want).abs().max().item()
+        assert err <= out_tol(want, dtype), (t, err)
+        hk, hv = c.dequantize(1)
+        ref = F.scaled_dot_product_attention(q[:, :, None].float(), hk.float(), hv.float(),
+                                             enable_gqa=G > 1)[:, :, 0].cpu()
+        rel = ((out - ref).norm() / ref.norm()).item()
+        assert rel < (2e-2 if dtype == torch.bfloat16 else 3e-3), (t, rel)
+
+
+@pytest.mark.parametrize("ns", [1, 2, 8, 64, 256])
+def test_split_k_matches_oracle(ns):
+    """Forced split-K factors incl. splits with no pages (ns > pages) and the LSE combine
+    (reference: tests/test_gpu.py:100-111)."""
+    torch.manual_seed(ns)
+    B, H, G, D, N = 2, 8, 4, 128, 32 * 100 + 7
+    c = kk.KushCache(1, H, H * G, D, batch_size=B, bits=4, device=DEV, dtype=torch.bfloat16, rotate=False)
+    K = torch.randn(B, H, N, D, device=DEV, dtype=torch.bfloat16)
+    c.write(0, K, K.flip(2))
+    q = torch.randn(B, H * G, D, device=DEV, dtype=torch.bfloat16)
+    out = torch.empty_like(q)
+    work = torch.empty(B * H * ns * G * (D + 2), dtype=torch.float32, device=DEV)
+    c.ops.decode(q, out, c.pool[0], c.block_table, c.seq_lens[0], c.tail_idx, c.tail_k[0], c.scale, ns, work)
+    want = oracle_decode(c, 0, q)
+    err = (out.float().cpu() - want).abs().max().item()
+    assert err <= out_tol(want, torch.bfloat16), err
+
+
+def test_empty_and_short_sequences():
+    """Sequences of 0, 1, 31, 32 and 33 tokens in one batch (ragged lengths through the raw Ops):
+    an empty sequence decodes to zeros, as the reference's l = 0 branch."""
+    torch.manual_seed(3)
+    lens = [0, 1, 31, 32, 33]
+    S, H, G, D, bits, dtype = len(lens), 2, 3, 128, 4, torch.bfloat16
+    ops = kk.Ops(torch.device(DEV), D, bits, G, dtype)
+    pages = 2
+    cache = torch.zeros(S * pages, H, kk.record_bytes(D, bits), dtype=torch.uint8, device=DEV)
+    bt = torch.randperm(S * pages, dtype=torch.int32).view(S, pages).to(DEV)
+    tail_k = torch.zeros(S, H, PAGE, D, dtype=dtype, device=DEV)
+    tail_idx = torch.arange(S, dtype=torch.int32, device=DEV)
+    T = max(lens)
+    k = torch.randn(S * T, H, D, dtype=dtype, device=DEV)
+    v = torch.randn(S * T, H, D, dtype=dtype, device=DEV)
+    qsl = torch.tensor([0] + [sum(lens[:i + 1]) for i in range(S)], dtype=torch.int32, device=DEV)
+    seq_lens = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    jobs = [(s, p) for s in range(S) for p in range(-(-lens[s] // PAGE))]
+    js = torch.tensor([j[0] for j in jobs], dtype=torch.int32, device=DEV)
+    jp = torch.tensor([j[1] for j in jobs], dtype=torch.int32, device=DEV)
+    ops.write(k, v, qsl, seq_lens, tail_idx, js, jp, cache, bt, tail_k)
+    q = torch.randn(S, H * G, D, dtype=dtype, device=DEV)
+    out = torch.empty_like(q)
+    ops.decode(q, out, cache, bt, seq_lens, tail_idx, tail_k, D ** -0.5)
+    o = OracleOps("cpu", D, bits, G)
+    want = torch.empty(q.shape)
+    o.decode(q.float().cpu(), want, cache.cpu(), bt.cpu(), seq_lens.cpu(), tail_idx.cpu(), tail_k.float().cpu(),
+             D ** -0.5)
+    got = out.float().cpu()
+    assert torch.equal(got[0], torch.zeros_like(got[0]))
+    assert (got - want).abs().max().item() <= out_tol(want, dtype)
