@@ -1,0 +1,275 @@
+"""Decode-attention benchmark of the compressed-KV hot path on one MI355X.
+
+Headline workload ("C2"): Qwen2.5-7B-shaped layer, 28 q heads / 4 kv
+heads (GQA 7), head_dim 128, int4 records, page 32, batch 64 x exactly 4096 cached tokens, bf16 q
+and output. One step = one decode-attention pass of that layer (decode kernel + split-K combine),
+replayed from HIP graphs with the inputs resident in HBM.
+
+Synthetic data (seed 0, generated on the GPU in this order): per pool, K = N(0,1) with a per-channel
+bias ~ N(0, 6^2) (sigma 6) on a seeded 10% of the channels of each kv head (13 of 128), V = N(0,1),
+written through the product's own quantize-and-pack kernel (Ops.write) into pages placed by a
+seeded random permutation of the physical blocks; q = N(0,1).
+
+The 155 MB of records of one pool fit in the 256 MB Infinity Cache, so steps rotate over
+--pools independent KV pools (default 4, 621 MB) and every step reads records that left the
+cache.
+
+Prints one JSON line (the driver's contract) with "roofline" (decode kernel: algorithmic bytes /
+its mean duration, from HIP events around graph replays of the decode kernel alone) and
+"cpu_baseline" (the C restatement of the reference CPU path, oracle/, on the host cores).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E, vendor figure (8 TB/s)
+PAGE = 32
+
+
+def parse_args(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200, help="timed steps (graph replays)")
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--ctx", type=int, default=4096)
+    ap.add_argument("--hq", type=int, default=28)
+    ap.add_argument("--hkv", type=int, default=4)
+    ap.add_argument("--dim", type=int, default=128)
+    ap.add_argument("--bits", type=int, default=4)
+    ap.add_argument("--pools", type=int, default=4, help="independent KV pools rotated across steps")
+    ap.add_argument("--splits", type=int, default=0, help="split-K factor (0: Ops.splits policy)")
+    ap.add_argument("--sweep-splits", default="", help="comma list of split factors to time (extra lines on stderr)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline")
+    return ap.parse_args(argv)
+
+
+def make_workload(a, dev):
+    """Pools of records written by the product's write kernel, per-pool block tables, q."""
+    import kushkash_amd as kk
+    from kushkash_amd._ops import Ops, record_bytes
+    B, N, Hkv, G, D, bits = a.batch, a.ctx, a.hkv, a.hq // a.hkv, a.dim, a.bits
+    dtype = torch.bfloat16
+    pages = -(-N // PAGE)
+    RB = record_bytes(D, bits)
+    ops = Ops(torch.device(dev), D, bits, G, dtype)
+    nblk = a.pools * B * pages
+    cache = torch.zeros(nblk, Hkv, RB, dtype=torch.uint8, device=dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    perm = torch.randperm(nblk, generator=gen, device=dev).to(torch.int32)
+    tables = [perm[i * B * pages:(i + 1) * B * pages].view(B, pages).contiguous() for i in range(a.pools)]
+    tail_k = torch.zeros(B, Hkv, PAGE, D, dtype=dtype, device=dev)
+    tail_idx = torch.arange(B, dtype=torch.int32, device=dev)
+    seq_lens = torch.full((B,), N, dtype=torch.int32, device=dev)
+    n_bias = max(1, round(0.10 * D))
+    chunk = max(1, (1 << 27) // (Hkv * N * D * 2))          # sequences per write call (~128 MB of K)
+    for i in range(a.pools):
+        bias = torch.zeros(Hkv, D, device=dev)
+        for h in range(Hkv):
+            ch = torch.randperm(D, generator=gen, device=dev)[:n_bias]
+            bias[h, ch] = 6.0 * torch.randn(n_bias, generator=gen, device=dev)
+        for s0 in range(0, B, chunk):
+            s1 = min(B, s0 + chunk)
+            n = s1 - s0
+            k = (torch.randn(n * N, Hkv, D, generator=gen, device=dev) + bias).to(dtype)
+            v = torch.randn(n * N, Hkv, D, generator=gen, device=dev).to(dtype)
+            qsl = torch.arange(n + 1, dtype=torch.int32, device=dev) * N
+            js = torch.arange(n, dtype=torch.int32, device=dev).repeat_interleave(pages)
+            jp = torch.arange(pages, dtype=torch.int32, device=dev).repeat(n)
+            ops.write(k, v, qsl, seq_lens[s0:s1], tail_idx[s0:s1], js, jp, cache, tables[i][s0:s1].contiguous(),
+                      tail_k)
+            del k, v
+    q = torch.randn(B, a.hq, D, generator=gen, device=dev).to(dtype)
+    torch.cuda.synchronize()
+    return dict(ops=ops, cache=cache, tables=tables, tail_k=tail_k, tail_idx=tail_idx, seq_lens=seq_lens, q=q,
+                B=B, N=N, Hkv=Hkv, G=G, D=D, bits=bits, RB=RB, pages=pages, kk=kk)
+
+
+def algorithmic_bytes(w) -> int:
+    """Bytes the step must move at minimum (the reference's quantized_bytes / time, cache.py:242,
+    bench_decode.py:129, plus q, out, block table and seq_lens): split-K scratch excluded."""
+    B, Hkv, G, D = w["B"], w["Hkv"], w["G"], w["D"]
+    full, tail = w["N"] // PAGE, w["N"] % PAGE
+    rec = B * Hkv * (full + (1 if tail else 0)) * w["RB"]
+    tail_b = B * Hkv * tail * D * 2
+    qo = 2 * B * Hkv * G * D * 2
+    return rec + tail_b + qo + B * w["pages"] * 4 + B * 4
+
+
+def graphs_for(w, ns: int, decode_only: bool):
+    """One HIP graph per pool: the decode step (decode + combine) or the decode kernel alone."""
+    ops, B, Hkv, G, D = w["ops"], w["B"], w["Hkv"], w["G"], w["D"]
+    out = torch.empty_like(w["q"])
+    work = torch.empty(max(1, B * Hkv * ns * G * (D + 2)), dtype=torch.float32, device=w["q"].device)
+    lib = ops._lib
+    bs, hs = w["cache"].stride(0), w["cache"].stride(1)
+    sm = 1.0 / math.sqrt(D)
+
+    def step(i):
+        if decode_only:
+            nml = B * Hkv * ns * G * 2
+            pm, po = (work.data_ptr(), work.data_ptr() + nml * 4) if ns > 1 else (None, None)
+            lib.call("kush_decode", D, w["bits"], G, 2, w["q"].data_ptr(), out.data_ptr(), w["cache"].data_ptr(), bs,
+                     hs, w["tail_k"].data_ptr(), w["tail_idx"].data_ptr(), w["tables"][i].data_ptr(),
+                     w["seq_lens"].data_ptr(), w["tables"][i].stride(0), Hkv, sm, ns, pm, po, B,
+                     torch.cuda.current_stream().cuda_stream)
+        else:
+            ops.decode(w["q"], out, w["cache"], w["tables"][i], w["seq_lens"], w["tail_idx"], w["tail_k"], sm, ns,
+                       work)
+
+    graphs = []
+    for i in range(len(w["tables"])):
+        step(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step(i)
+        graphs.append(g)
+    torch.cuda.synchronize()
+    return graphs, out
+
+
+def time_graphs(graphs, steps: int, warmup: int) -> float:
+    """Mean ms per replay, HIP events on the replay stream, pools rotated every step."""
+    P = len(graphs)
+    for i in range(warmup):
+        graphs[i % P].replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(steps):
+        graphs[i % P].replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def cpu_baseline(w, budget_s: float):
+    """The oracle's decode (C restatement of the reference CPU path, fp32, one task per (sequence,
+    kv head)) on the host cores, over a bounded sample of the same workload: the first S_cpu
+    sequences of pool 0 (records copied to host memory). Median of runs after one warm-up."""
+    from oracle import cpu_ops
+    B, Hkv, G, D = w["B"], w["Hkv"], w["G"], w["D"]
+    ncores = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():         # the box's CPU share for this GPU
+        ncores = min(ncores, int(os.environ["OMP_NUM_THREADS"]))
+    cpu_ops.set_threads(ncores)
+    ops = cpu_ops.OracleOps("cpu", D, w["bits"], G)
+    table = w["tables"][0].cpu()
+    S = B
+    # size the sample: one sequence timed first, then as many as fit in the budget
+    cache = w["cache"].cpu()
+    tail_k = w["tail_k"].float().cpu()
+    q = w["q"].float().cpu()
+    sl = w["seq_lens"].cpu()
+    ti = w["tail_idx"].cpu()
+
+    def run(n):
+        out = torch.empty(n, Hkv * G, D)
+        t0 = time.perf_counter()
+        ops.decode(q[:n].contiguous(), out, cache, table[:n].contiguous(), sl[:n].contiguous(), ti[:n].contiguous(),
+                   tail_k, 1.0 / math.sqrt(D))
+        return time.perf_counter() - t0
+
+    t1 = run(min(S, max(1, ncores)))
+    per_seq = t1 / min(S, max(1, ncores))
+    n = int(min(S, max(1, budget_s / 4 / max(per_seq, 1e-6))))
+    run(n)                                                       # warm-up
+    reps = max(1, min(20, int(budget_s / max(per_seq * n, 1e-6))))
+    times = sorted(run(n) for _ in range(reps))
+    med = times[len(times) // 2]
+    frac = n / S
+    cpu_ops.set_threads(1)                                        # single-core figure on one sequence
+    t_one = min(run(1) for _ in range(2))
+    cpu_ops.set_threads(ncores)
+    bytes_ = algorithmic_bytes(w) * frac
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(bytes_ / med / 1e9, 3), "unit": "GB/s", "cores": ncores, "kind": "port",
+            "sample": f"{n} of {S} sequences of the same C2 workload (all {Hkv} kv heads, {w['N']} tokens each), "
+                      f"median of {reps} runs after 1 warm-up; {med * 1e6 / n:.0f} us per sequence on {ncores} "
+                      f"threads, {t_one * 1e6:.0f} us per sequence on 1 thread; host CPU: {cpu_model}",
+            "us_per_step_extrapolated": round(med / frac * 1e6, 1)}
+
+
+def main(argv=None):
+    a = parse_args(argv)
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (every box here has one GPU); "
+              "run with --gpus 1", file=sys.stderr)
+        raise SystemExit(2)
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a GPU")
+    dev = "cuda:0"
+    w = make_workload(a, dev)
+    ns = a.splits or w["ops"].splits(w["B"], w["Hkv"], w["N"] // PAGE)
+    alg = algorithmic_bytes(w)
+
+    for extra in [int(x) for x in a.sweep_splits.split(",") if x.strip()]:
+        g, _ = graphs_for(w, extra, decode_only=False)
+        ms = time_graphs(g, a.steps, a.warmup)
+        gd, _ = graphs_for(w, extra, decode_only=True)
+        msd = time_graphs(gd, a.steps, a.warmup)
+        print(f"splits {extra:4d}: step {ms * 1e3:8.2f} us ({alg / ms / 1e6:7.1f} GB/s)  decode kernel "
+              f"{msd * 1e3:8.2f} us ({alg / msd / 1e6:7.1f} GB/s)", file=sys.stderr, flush=True)
+        del g, gd
+
+    graphs, out = graphs_for(w, ns, decode_only=False)
+    ms = time_graphs(graphs, a.steps, a.warmup)
+    dgraphs, _ = graphs_for(w, ns, decode_only=True)
+    ms_dec = time_graphs(dgraphs, a.steps, a.warmup)
+    gbs = alg / ms / 1e6
+    gbs_dec = alg / ms_dec / 1e6
+    res = {
+        "metric": "decode-attn us/step + achieved HBM GB/s (% peak), int4, bs64 x 4k ctx",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_step": round(ms * 1e3, 2),
+        "pct_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 1),
+        "tokens_per_s": round(w["B"] / (ms / 1e3), 1),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4 records, f16 MFMA, f32 accumulate, bf16 q/out",
+        "data": "synthetic (seeded; K bias sigma 6 on 10% of channels; random page placement; "
+                f"{a.pools} rotated pools)",
+        "config": {"workload": f"C2 Qwen2.5-7B decode layer: {a.hq} q / {a.hkv} kv heads, D {a.dim}, int{a.bits}, "
+                               f"page 32, batch {a.batch} x {a.ctx} tokens", "global_batch": a.batch,
+                   "seq_len": a.ctx, "parallelism": "single GPU", "split_k": ns, "pools": a.pools},
+        "roofline": {"bound": "hbm", "achieved": round(gbs_dec, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs_dec / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "decode_kernel<128,4,bf16,4>", "kernel_us": round(ms_dec * 1e3, 2),
+                     "algorithmic_bytes": alg},
+        "cpu_baseline": None,
+    }
+    del graphs, dgraphs
+    if not a.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(w, a.cpu_seconds)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()
