@@ -50,7 +50,8 @@ def parse_args(argv=None):
     ap.add_argument("--bits", type=int, default=4)
     ap.add_argument("--pools", type=int, default=4, help="independent KV pools rotated across steps")
     ap.add_argument("--splits", type=int, default=0, help="split-K factor (0: Ops.splits policy)")
-    ap.add_argument("--sweep-splits", default="", help="comma list of split factors to time (extra lines on stderr)")
+    ap.add_argument("--waves", type=int, default=0, help="waves per decode workgroup (0: Ops.waves policy)")
+    ap.add_argument("--sweep", default="", help="comma list of splits:waves pairs to time (extra lines on stderr)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline")
     return ap.parse_args(argv)
@@ -109,26 +110,17 @@ def algorithmic_bytes(w) -> int:
     return rec + tail_b + qo + B * w["pages"] * 4 + B * 4
 
 
-def graphs_for(w, ns: int, decode_only: bool):
-    """One HIP graph per pool: the decode step (decode + combine) or the decode kernel alone."""
+def graphs_for(w, ns: int, waves: int):
+    """One HIP graph per pool holding one decode step (a single kernel: split-K partials are merged
+    inside it by the last workgroup of each (sequence, kv head))."""
     ops, B, Hkv, G, D = w["ops"], w["B"], w["Hkv"], w["G"], w["D"]
     out = torch.empty_like(w["q"])
     work = torch.empty(max(1, B * Hkv * ns * G * (D + 2)), dtype=torch.float32, device=w["q"].device)
-    lib = ops._lib
-    bs, hs = w["cache"].stride(0), w["cache"].stride(1)
     sm = 1.0 / math.sqrt(D)
 
     def step(i):
-        if decode_only:
-            nml = B * Hkv * ns * G * 2
-            pm, po = (work.data_ptr(), work.data_ptr() + nml * 4) if ns > 1 else (None, None)
-            lib.call("kush_decode", D, w["bits"], G, 2, w["q"].data_ptr(), out.data_ptr(), w["cache"].data_ptr(), bs,
-                     hs, w["tail_k"].data_ptr(), w["tail_idx"].data_ptr(), w["tables"][i].data_ptr(),
-                     w["seq_lens"].data_ptr(), w["tables"][i].stride(0), Hkv, sm, ns, pm, po, B,
-                     torch.cuda.current_stream().cuda_stream)
-        else:
-            ops.decode(w["q"], out, w["cache"], w["tables"][i], w["seq_lens"], w["tail_idx"], w["tail_k"], sm, ns,
-                       work)
+        ops.decode(w["q"], out, w["cache"], w["tables"][i], w["seq_lens"], w["tail_idx"], w["tail_k"], sm, ns, work,
+                   waves=waves)
 
     graphs = []
     for i in range(len(w["tables"])):
@@ -224,19 +216,18 @@ def main(argv=None):
     ns = a.splits or w["ops"].splits(w["B"], w["Hkv"], w["N"] // PAGE)
     alg = algorithmic_bytes(w)
 
-    for extra in [int(x) for x in a.sweep_splits.split(",") if x.strip()]:
-        g, _ = graphs_for(w, extra, decode_only=False)
-        ms = time_graphs(g, a.steps, a.warmup)
-        gd, _ = graphs_for(w, extra, decode_only=True)
-        msd = time_graphs(gd, a.steps, a.warmup)
-        print(f"splits {extra:4d}: step {ms * 1e3:8.2f} us ({alg / ms / 1e6:7.1f} GB/s)  decode kernel "
-              f"{msd * 1e3:8.2f} us ({alg / msd / 1e6:7.1f} GB/s)", file=sys.stderr, flush=True)
-        del g, gd
+    for item in [x for x in a.sweep.split(",") if x.strip()]:
+        sns, swv = (int(v) for v in item.split(":"))
+        g, _ = graphs_for(w, sns, swv)
+        msx = time_graphs(g, a.steps, a.warmup)
+        print(f"splits {sns:4d} waves {swv:3d}: {msx * 1e3:8.2f} us/step  {alg / msx / 1e6:7.1f} GB/s "
+              f"({100 * alg / msx / 1e6 / PEAK_HBM_GBS:5.1f}% of peak)", file=sys.stderr, flush=True)
+        del g
 
-    graphs, out = graphs_for(w, ns, decode_only=False)
+    wv = a.waves or w["ops"].waves(w["B"], w["Hkv"], ns)
+    graphs, out = graphs_for(w, ns, wv)
     ms = time_graphs(graphs, a.steps, a.warmup)
-    dgraphs, _ = graphs_for(w, ns, decode_only=True)
-    ms_dec = time_graphs(dgraphs, a.steps, a.warmup)
+    ms_dec = ms                                   # one kernel per step: the decode kernel is the step
     gbs = alg / ms / 1e6
     gbs_dec = alg / ms_dec / 1e6
     res = {
@@ -258,14 +249,14 @@ def main(argv=None):
                 f"{a.pools} rotated pools)",
         "config": {"workload": f"C2 Qwen2.5-7B decode layer: {a.hq} q / {a.hkv} kv heads, D {a.dim}, int{a.bits}, "
                                f"page 32, batch {a.batch} x {a.ctx} tokens", "global_batch": a.batch,
-                   "seq_len": a.ctx, "parallelism": "single GPU", "split_k": ns, "pools": a.pools},
+                   "seq_len": a.ctx, "parallelism": "single GPU", "split_k": ns, "waves": wv, "pools": a.pools},
         "roofline": {"bound": "hbm", "achieved": round(gbs_dec, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs_dec / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "decode_kernel<128,4,bf16,4>", "kernel_us": round(ms_dec * 1e3, 2),
+                     "kernel": f"decode_kernel<{a.dim},{a.bits},bf16,{wv}>", "kernel_us": round(ms_dec * 1e3, 2),
                      "algorithmic_bytes": alg},
         "cpu_baseline": None,
     }
-    del graphs, dgraphs
+    del graphs
     if not a.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(w, a.cpu_seconds)
     print(json.dumps(res), flush=True)

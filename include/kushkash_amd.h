@@ -71,15 +71,22 @@ int kush_write(int head_dim, int bits, int dtype, const void* k, const void* v, 
                const int32_t* block_table, int64_t bt_row_stride, int32_t hkv, void* stream);
 
 /* Decode attention of one query per sequence over its seq_lens[s] cached tokens, softmax scale
- * `scale`. n_splits == 1 writes out; n_splits > 1 writes per-split partials instead:
- * part_ml fp32 [n_seqs*hkv*n_splits*group][2] (running max in log2 units, sum) and part_o fp32
- * [n_seqs*hkv*n_splits*group][head_dim] (unnormalized), to be merged by kush_combine.
- * Replaces kush_decode_tc / kush_decode (gpu.mojo:566-807, :840-1040) as launched by Ops.decode
- * (_ops.py:191-211); the partial layout is the reference's `work` layout (_ops.py:204-208). */
+ * `scale`. n_splits == 1 writes out. n_splits > 1 splits every sequence's pages into n_splits
+ * contiguous ranges and writes per-split partials: part_ml fp32
+ * [n_seqs*hkv*n_splits*group][2] (running max in log2 units, sum) and part_o fp32
+ * [n_seqs*hkv*n_splits*group][head_dim] (unnormalized), the reference's `work` layout
+ * (_ops.py:204-208). With split_sync (int32 [n_seqs*hkv*ceil(group/16)], zero before the first
+ * call) the last workgroup of each (sequence, kv head) merges the splits into out itself and
+ * resets its counter, so the buffer stays zero between calls; calls that share split_sync must
+ * not overlap. Without it (NULL), run kush_combine afterwards. waves: 4, 8 or 16 waves per
+ * workgroup (0 = 4).
+ * Replaces kush_decode_tc / kush_decode (gpu.mojo:566-807, :840-1040) and, with split_sync, the
+ * kush_combine launch (gpu.mojo:469-491) as issued by Ops.decode (_ops.py:191-213). */
 int kush_decode(int head_dim, int bits, int group, int dtype, const void* q, void* out, const void* cache,
                 int64_t block_stride, int64_t head_stride, const void* tail_k, const int32_t* tail_idx,
                 const int32_t* block_table, const int32_t* seq_lens, int64_t bt_row_stride, int32_t hkv,
-                float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t n_seqs, void* stream);
+                float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t* split_sync, int32_t waves,
+                int32_t n_seqs, void* stream);
 
 /* Merge kush_decode's split partials into out [n_seqs][hkv*group][head_dim].
  * Replaces kush_combine (gpu.mojo:469-491) as launched by Ops.decode (_ops.py:212-213). */
@@ -90,7 +97,7 @@ int kush_combine(int head_dim, int group, int dtype, void* out, const float* par
  * reference raises the driver's error string directly (_cuda.py:39-43). */
 const char* kush_last_error(void);
 
-/* ABI revision of this header (1). No reference counterpart. */
+/* ABI revision of this header (2). No reference counterpart. */
 int kush_abi_version(void);
 
 #ifdef __cplusplus

@@ -104,19 +104,46 @@ __device__ __forceinline__ void stage_record(const uint8_t* __restrict__ rec, ui
     }
 }
 
+// max / sum over the 4 lanes l, l ^ 16, l ^ 32, l ^ 48 (one q head's lane groups), on the VALU
+__device__ __forceinline__ float rows_max(float x) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __builtin_fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __builtin_fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float rows_sum(float x) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i lds_v2i;
+
+// V^T operand gather: within each 16-lane group, ds_read_b64_tr_b8 hands output lane i byte
+// (i % 8) of the 8-byte rows supplied by lanes 2k + (i % 16) / 8, k = 0..7. Lane (2k + half) of
+// group q supplies token tok(q, k) at byte column 16 ct + 8 half, so lane r of the group receives
+// byte column 16 ct + r of its 8 tokens, in PV slot order.
+__device__ __forceinline__ v2i gather_vt(const uint8_t* st, int dc, int ct, int lane) {
+    const int s16 = lane & 15, q = lane >> 4;
+    const uint8_t* src = st + tok(q, s16 >> 1) * dc + 16 * ct + 8 * (s16 & 1);
+    return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(src));
+}
+
 // Softmax update of one page (scores x in log2 units, tokens tok(q, j); tokens >= valid masked)
 // and its PV accumulation from the staged V codes.
 template <int D, int BITS>
 __device__ __forceinline__ void consume_page(const uint8_t* st, f4 (&o)[D / 16], const float (&x)[8], int valid,
-                                             float& m_run, float& l_run, float& vb_run, int r16, int q) {
+                                             float& m_run, float& l_run, float& vb_run, int lane) {
     using F = Fmt<D, BITS>;
     using S = Stage<D, BITS>;
+    const int q = lane >> 4;
     float pm = x[0];
 #pragma unroll
     for (int j = 1; j < 8; ++j) pm = __builtin_fmaxf(pm, x[j]);
-    pm = __builtin_fmaxf(pm, __shfl_xor(pm, 16, WAVE));
-    pm = __builtin_fmaxf(pm, __shfl_xor(pm, 32, WAVE));
-    const float m_new = __builtin_fmaxf(m_run, pm);
+    const float m_new = __builtin_fmaxf(m_run, rows_max(pm));
     const float corr = __builtin_amdgcn_exp2f(m_run - m_new);   // first page: exp2(-inf) = 0
 
     const h4v vs0 = *reinterpret_cast<const h4v*>(st + S::VS + 8 * q);
@@ -143,68 +170,62 @@ __device__ __forceinline__ void consume_page(const uint8_t* st, f4 (&o)[D / 16],
         for (int dt = 0; dt < D / 16; ++dt) o[dt] *= corr;
     }
 
-    // V^T operands: byte column c of the 8 tokens of this lane group
     constexpr int NCOL = BITS == 4 ? D / 32 : D / 16;
 #pragma unroll
     for (int ct = 0; ct < NCOL; ++ct) {
-        const uint8_t* col = st + 16 * ct + r16;
-        uint32_t P[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            P[k] = (uint32_t)col[tok(q, 2 * k) * F::DC] | ((uint32_t)col[tok(q, 2 * k + 1) * F::DC] << 16);
+        const v2i w = gather_vt(st, F::DC, ct, lane);
         if constexpr (BITS == 4) {
+            const uint32_t x0 = (uint32_t)w[0] ^ 0x88888888u, x1 = (uint32_t)w[1] ^ 0x88888888u;
+            const uint32_t l0 = x0 & 0x0F0F0F0Fu, l1 = x1 & 0x0F0F0F0Fu;
+            const uint32_t u0 = (x0 >> 4) & 0x0F0F0F0Fu, u1 = (x1 >> 4) & 0x0F0F0F0Fu;
             const h2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-            h8 lo, hi;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint32_t xx = P[k] ^ 0x00880088u;
-                const h2 l2 = as_h2((xx & 0x000F000Fu) | 0x64006400u) + off;
-                const h2 u2 = as_h2(((xx >> 4) & 0x000F000Fu) | 0x64006400u) + off;
-                lo[2 * k] = l2[0];
-                lo[2 * k + 1] = l2[1];
-                hi[2 * k] = u2[0];
-                hi[2 * k + 1] = u2[1];
-            }
-            o[ct] = mfma16(lo, pw, o[ct]);
-            o[ct + D / 32] = mfma16(hi, pw, o[ct + D / 32]);
+            const h2 a = as_h2(__builtin_amdgcn_perm(0x64646464u, l0, 0x04010400u)) + off;
+            const h2 b = as_h2(__builtin_amdgcn_perm(0x64646464u, l0, 0x04030402u)) + off;
+            const h2 c = as_h2(__builtin_amdgcn_perm(0x64646464u, l1, 0x04010400u)) + off;
+            const h2 d = as_h2(__builtin_amdgcn_perm(0x64646464u, l1, 0x04030402u)) + off;
+            const h2 e = as_h2(__builtin_amdgcn_perm(0x64646464u, u0, 0x04010400u)) + off;
+            const h2 f = as_h2(__builtin_amdgcn_perm(0x64646464u, u0, 0x04030402u)) + off;
+            const h2 g = as_h2(__builtin_amdgcn_perm(0x64646464u, u1, 0x04010400u)) + off;
+            const h2 hh = as_h2(__builtin_amdgcn_perm(0x64646464u, u1, 0x04030402u)) + off;
+            o[ct] = mfma16(h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]}, pw, o[ct]);
+            o[ct + D / 32] = mfma16(h8{e[0], e[1], f[0], f[1], g[0], g[1], hh[0], hh[1]}, pw, o[ct + D / 32]);
         } else {
-            const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-            h8 vv;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const h2 v2 = as_h2((P[k] ^ 0x00800080u) | 0x64006400u) + off;
-                vv[2 * k] = v2[0];
-                vv[2 * k + 1] = v2[1];
-            }
-            o[ct] = mfma16(vv, pw, o[ct]);
+            o[ct] = mfma16(int8_codes((uint32_t)w[0], (uint32_t)w[1]), pw, o[ct]);
         }
     }
 }
 
 // grid (S, Hkv, n_splits * ceil(G / 16)), block NW * 64.
+// NS > 1: each workgroup writes its split's partials; with `sync` (one zeroed int32 per
+// (sequence, kv head, head chunk)), the last workgroup of a (sequence, kv head, head chunk) to
+// finish merges all splits into `out` and resets its counter, so no second launch is needed.
 template <int D, int BITS, typename IN, int NW>
 __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     const IN* __restrict__ qg, IN* __restrict__ out, const uint8_t* __restrict__ cache, int64_t bs, int64_t hs,
     const IN* __restrict__ tail_k, const int32_t* __restrict__ tail_idx, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ seq_lens, int64_t bt_stride, int H, int G, float sm_log2, int NS,
-    float* __restrict__ part_ml, float* __restrict__ part_o) {
+    float* __restrict__ part_ml, float* __restrict__ part_o, int32_t* __restrict__ sync) {
     using F = Fmt<D, BITS>;
     using S = Stage<D, BITS>;
     constexpr int KSTEPS = D / 32;
     constexpr int DT = D / 16;
     constexpr int KBYTES = F::DC / 4;                // K code bytes per lane per 16-token tile
     constexpr int KW = KBYTES / 4;
-    constexpr int STAGE = (S::BYTES + 15) / 16 * 16;
+    constexpr int STAGE = S::BYTES;
+    constexpr int VCPL = (S::CHUNKS + WAVE - 1) / WAVE;
 
     __shared__ __align__(16) uint8_t stage_all[NW * STAGE];
-    __shared__ __align__(16) float qs_l[16 * D];     // q * sm * log2e for the exact-K tail; then merge buffer
+    __shared__ __align__(16) h8 qhl[KSTEPS * WAVE];   // fp16(q sm log2e) in each lane's contraction order
+    __shared__ __align__(16) h8 qll[KSTEPS * WAVE];   // fp16 remainder: hi + lo carries q to ~2^-22
+    __shared__ __align__(16) float qs_l[16 * D];     // fp32 q sm log2e for the exact-K tail; then merge buffer
     __shared__ float sc_l[16 * PAGE];                // tail scores
     __shared__ float m_l[NW * 16], l_l[NW * 16];
+    __shared__ int last_flag;
 
     const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
     const int r16 = lane & 15, q = lane >> 4;
     const int s = blockIdx.x, h = blockIdx.y;
-    const int z = blockIdx.z % NS, g0 = (blockIdx.z / NS) * 16;
+    const int z = blockIdx.z % NS, gc = blockIdx.z / NS, g0 = gc * 16;
     const int Gc = min(16, G - g0);
 
     const int n = seq_lens[s];
@@ -214,51 +235,76 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     const int32_t* bt = block_table + (int64_t)s * bt_stride;
     const uint8_t* head_base = cache + (int64_t)h * hs;
     const int64_t qbase = ((int64_t)s * H + h) * G * D + (int64_t)g0 * D;
+    const bool has_tail = tail_n > 0 && z == NS - 1;
     uint8_t* st = stage_all + w * STAGE;
 
-    // this lane's q head (B column r16) over its contraction dims, as an fp16 hi / lo pair
-    const bool gv = r16 < Gc;
-    h8 qh[KSTEPS], ql[KSTEPS];
-#pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float xq = gv ? to_f32(qg[qbase + (int64_t)r16 * D + kdim<D, BITS>(kk, q, j)]) * sm_log2 : 0.0f;
-            const _Float16 hi = (_Float16)xq;
-            qh[kk][j] = hi;
-            ql[kk][j] = (_Float16)(xq - (float)hi);
-        }
+    for (int i = threadIdx.x; i < KSTEPS * WAVE * 8; i += NW * WAVE) {
+        const int kk = i / (WAVE * 8), l = (i / 8) % WAVE, j = i % 8;
+        const int g = l & 15;
+        const float xq = g < Gc ? to_f32(qg[qbase + (int64_t)g * D + kdim<D, BITS>(kk, l >> 4, j)]) * sm_log2 : 0.0f;
+        const _Float16 hi = (_Float16)xq;
+        reinterpret_cast<_Float16*>(&qhl[kk * WAVE + l])[j] = hi;
+        reinterpret_cast<_Float16*>(&qll[kk * WAVE + l])[j] = (_Float16)(xq - (float)hi);
+    }
+    if (has_tail) {
+        for (int i = threadIdx.x; i < 16 * D; i += NW * WAVE)
+            qs_l[i] = i / D < Gc ? to_f32(qg[qbase + i]) * sm_log2 : 0.0f;
+    }
+    __syncthreads();
 
     f4 o[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     float m_run = -__builtin_inff(), l_run = 0.0f, vb_run = 0.0f;
 
-    for (int p = p0 + w; p < p1; p += NW) {
+    // one page in flight per wave: K code slice in registers, V codes + scales staged through registers
+    uint32_t kwn[2][KW];
+    uint4 vn[VCPL];
+    auto issue = [&](int p) {
         const uint8_t* rec = head_base + (int64_t)bt[p] * bs;
-        uint32_t kw[2][KW];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
             const uint8_t* src = rec + (16 * tt + r16) * F::DC + q * KBYTES;
             if constexpr (KBYTES == 8) {
                 const uint2 v2 = *reinterpret_cast<const uint2*>(src);
-                kw[tt][0] = v2.x;
-                kw[tt][1] = v2.y;
+                kwn[tt][0] = v2.x;
+                kwn[tt][1] = v2.y;
             } else {
 #pragma unroll
                 for (int c = 0; c < KBYTES / 16; ++c) {
                     const uint4 v4 = reinterpret_cast<const uint4*>(src)[c];
-                    kw[tt][4 * c + 0] = v4.x;
-                    kw[tt][4 * c + 1] = v4.y;
-                    kw[tt][4 * c + 2] = v4.z;
-                    kw[tt][4 * c + 3] = v4.w;
+                    kwn[tt][4 * c + 0] = v4.x;
+                    kwn[tt][4 * c + 1] = v4.y;
+                    kwn[tt][4 * c + 2] = v4.z;
+                    kwn[tt][4 * c + 3] = v4.w;
                 }
             }
         }
-        stage_record<D, BITS>(rec, st, lane);
+        const uint4* vsrc = reinterpret_cast<const uint4*>(rec + F::OFF_VQ);
+#pragma unroll
+        for (int i = 0; i < VCPL; ++i) {
+            const int c = lane + WAVE * i;
+            if (c < S::CHUNKS) vn[i] = vsrc[c];
+        }
+    };
+
+    int p = p0 + w;
+    if (p < p1) issue(p);
+    for (; p < p1; p += NW) {
+        uint32_t kw[2][KW];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int i = 0; i < KW; ++i) kw[tt][i] = kwn[tt][i];
+#pragma unroll
+        for (int i = 0; i < VCPL; ++i) {
+            const int c = lane + WAVE * i;
+            if (c < S::CHUNKS) reinterpret_cast<uint4*>(st)[c] = vn[i];
+        }
+        if (p + NW < p1) issue(p + NW);
 
         f4 sacc[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};
-        float kbs = 0.0f;
+        f4 kacc = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int kk = 0; kk < KSTEPS; ++kk) {
             h8 ks8, kb8;
@@ -275,13 +321,13 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
                 ks8 = *reinterpret_cast<const h8*>(st + S::KS + 2 * d0);
                 kb8 = *reinterpret_cast<const h8*>(st + S::KB + 2 * d0);
             }
-            const h8 qp = qh[kk] * ks8;                       // fp16 multiply, as the reference TC path
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const h2 kb2 = {kb8[2 * e], kb8[2 * e + 1]};
-                kbs = __builtin_amdgcn_fdot2(h2{qh[kk][2 * e], qh[kk][2 * e + 1]}, kb2, kbs, false);
-                kbs = __builtin_amdgcn_fdot2(h2{ql[kk][2 * e], ql[kk][2 * e + 1]}, kb2, kbs, false);
-            }
+            const h8 qh = qhl[kk * WAVE + lane];
+            const h8 ql = qll[kk * WAVE + lane];
+            // K bias dot: every row of A is this lane group's k_bias slice, so every output row is
+            // sum_d kb[d] q[g][d]: all four accumulators of lane (q, g) hold it, no reduction needed
+            kacc = mfma16(kb8, qh, kacc);
+            kacc = mfma16(kb8, ql, kacc);
+            const h8 qp = qh * ks8;                           // fp16 multiply, as the reference TC path
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
                 h8 a;
@@ -292,56 +338,50 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
                 sacc[tt] = mfma16(a, qp, sacc[tt]);
             }
         }
-        kbs += __shfl_xor(kbs, 16, WAVE);
-        kbs += __shfl_xor(kbs, 32, WAVE);
         float x[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = sacc[j >> 2][j & 3] + kbs;
-        consume_page<D, BITS>(st, o, x, PAGE, m_run, l_run, vb_run, r16, q);
+        for (int j = 0; j < 8; ++j) x[j] = sacc[j >> 2][j & 3] + kacc[0];
+        consume_page<D, BITS>(st, o, x, PAGE, m_run, l_run, vb_run, lane);
     }
 
     // partial last page: exact K from the tail, V rows from its record (last split only)
-    if (tail_n > 0 && z == NS - 1) {
-        for (int i = threadIdx.x; i < 16 * D; i += NW * WAVE) {
-            const int gg = i / D;
-            qs_l[i] = gg < Gc ? to_f32(qg[qbase + i]) * sm_log2 : 0.0f;
-        }
-        __syncthreads();
-        if (w == (p1 - p0) % NW) {
-            const IN* tk = tail_k + ((int64_t)tail_idx[s] * H + h) * PAGE * D;
-            const int t = lane & 31, hf = lane >> 5;
-            float acc[16];
+    if (has_tail && w == (p1 - p0) % NW) {
+        const IN* tk = tail_k + ((int64_t)tail_idx[s] * H + h) * PAGE * D;
+        const int t = lane & 31, hf = lane >> 5;
+        float acc[16];
 #pragma unroll
-            for (int g = 0; g < 16; ++g) acc[g] = 0.0f;
-            if (t < tail_n) {
-                for (int d = hf * (D / 2); d < (hf + 1) * (D / 2); d += 4) {
-                    const float k0 = to_f32(tk[t * D + d]), k1 = to_f32(tk[t * D + d + 1]);
-                    const float k2 = to_f32(tk[t * D + d + 2]), k3 = to_f32(tk[t * D + d + 3]);
+        for (int g = 0; g < 16; ++g) acc[g] = 0.0f;
+        if (t < tail_n) {
+            for (int d = hf * (D / 2); d < (hf + 1) * (D / 2); d += 4) {
+                const float k0 = to_f32(tk[t * D + d]), k1 = to_f32(tk[t * D + d + 1]);
+                const float k2 = to_f32(tk[t * D + d + 2]), k3 = to_f32(tk[t * D + d + 3]);
 #pragma unroll
-                    for (int g = 0; g < 16; ++g) {
-                        const float4 q4 = *reinterpret_cast<const float4*>(&qs_l[g * D + d]);
-                        acc[g] += q4.x * k0 + q4.y * k1 + q4.z * k2 + q4.w * k3;
-                    }
+                for (int g = 0; g < 16; ++g) {
+                    const float4 q4 = *reinterpret_cast<const float4*>(&qs_l[g * D + d]);
+                    acc[g] += q4.x * k0 + q4.y * k1 + q4.z * k2 + q4.w * k3;
                 }
             }
-#pragma unroll
-            for (int g = 0; g < 16; ++g) {
-                acc[g] += __shfl_xor(acc[g], 32, WAVE);
-                if (hf == 0) sc_l[g * PAGE + t] = t < tail_n ? acc[g] : -__builtin_inff();
-            }
-            stage_record<D, BITS>(head_base + (int64_t)bt[full] * bs, st, lane);
-            float x[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) x[j] = sc_l[r16 * PAGE + tok(q, j)];
-            consume_page<D, BITS>(st, o, x, tail_n, m_run, l_run, vb_run, r16, q);
         }
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+            acc[g] += __shfl_xor(acc[g], 32, WAVE);
+            if (hf == 0) sc_l[g * PAGE + t] = t < tail_n ? acc[g] : -__builtin_inff();
+        }
+        const uint4* vsrc = reinterpret_cast<const uint4*>(head_base + (int64_t)bt[full] * bs + F::OFF_VQ);
+#pragma unroll
+        for (int i = 0; i < VCPL; ++i) {
+            const int c = lane + WAVE * i;
+            if (c < S::CHUNKS) reinterpret_cast<uint4*>(st)[c] = vsrc[c];
+        }
+        float x[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = sc_l[r16 * PAGE + tok(q, j)];
+        consume_page<D, BITS>(st, o, x, tail_n, m_run, l_run, vb_run, lane);
     }
 
     // merge the waves: every wave rescales to the workgroup max and adds into LDS in turn
-    l_run += __shfl_xor(l_run, 16, WAVE);
-    l_run += __shfl_xor(l_run, 32, WAVE);
-    vb_run += __shfl_xor(vb_run, 16, WAVE);
-    vb_run += __shfl_xor(vb_run, 32, WAVE);
+    l_run = rows_sum(l_run);
+    vb_run = rows_sum(vb_run);
     __syncthreads();
     if (q == 0) {
         m_l[w * 16 + r16] = m_run;
@@ -353,7 +393,7 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     for (int ww = 0; ww < NW; ++ww) M = __builtin_fmaxf(M, m_l[ww * 16 + r16]);
     const float f = m_run == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m_run - M);
     float* mbuf = qs_l;
-#pragma unroll
+#pragma unroll 1
     for (int ww = 0; ww < NW; ++ww) {
         if (w == ww) {
 #pragma unroll
@@ -392,6 +432,40 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
             }
         }
     }
+    if (NS == 1 || sync == nullptr) return;
+
+    // split-K: the last workgroup of this (sequence, kv head, head chunk) merges every split
+    __threadfence();                                        // this thread's partials, visible device-wide
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int n_gc = gridDim.z / NS;
+        int32_t* ctr = sync + ((int64_t)s * H + h) * n_gc + gc;
+        const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        last_flag = prev == NS - 1;
+        if (prev == NS - 1) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last_flag) return;
+    __threadfence();                                        // acquire: see every split's partials
+    const int64_t base = ((int64_t)s * H + h) * NS;
+    for (int i = threadIdx.x; i < Gc * D; i += NW * WAVE) {
+        const int g = g0 + i / D, d = i % D;
+        float Mg = -__builtin_inff();
+        for (int zz = 0; zz < NS; ++zz) Mg = __builtin_fmaxf(Mg, part_ml[2 * ((base + zz) * G + g)]);
+        float L = 0.0f, acc = 0.0f;
+        if (Mg > -__builtin_inff()) {
+            for (int zz = 0; zz < NS; ++zz) {
+                const int64_t pb = (base + zz) * G + g;
+                const float mz = part_ml[2 * pb];
+                if (mz > -__builtin_inff()) {
+                    const float fz = __builtin_amdgcn_exp2f(mz - Mg);
+                    L += part_ml[2 * pb + 1] * fz;
+                    acc += fz * part_o[pb * D + d];
+                }
+            }
+        }
+        out[qbase + i] = from_f32<IN>(L > 0.0f ? acc / L : 0.0f);
+    }
 }
 
 // grid (S, Hkv), block 256: merge split-K partials (M, L, unnormalized O) into the output.
@@ -421,7 +495,22 @@ __global__ __launch_bounds__(256) void combine_kernel(IN* __restrict__ out, cons
     }
 }
 
-constexpr int DECODE_WAVES = 4;
+// Static LDS of one decode workgroup (must stay within the 160 KB of a gfx950 CU).
+template <int D, int BITS, int NW>
+constexpr int decode_lds_bytes() {
+    return NW * Stage<D, BITS>::BYTES + 2 * (D / 32) * WAVE * 16 + 16 * D * 4 + 16 * PAGE * 4 + 2 * NW * 16 * 4 + 16;
+}
+
+template <int D, int BITS, typename IN, int NW>
+static int launch_decode(dim3 grid, hipStream_t stream, const void* q, void* out, const void* cache, int64_t bs,
+                         int64_t hs, const void* tail_k, const int32_t* tail_idx, const int32_t* block_table,
+                         const int32_t* seq_lens, int64_t bt_stride, int hkv, int group, float sm_log2, int n_splits,
+                         float* part_ml, float* part_o, int32_t* sync) {
+    decode_kernel<D, BITS, IN, NW><<<grid, dim3(NW * WAVE), 0, stream>>>(
+        (const IN*)q, (IN*)out, (const uint8_t*)cache, bs, hs, (const IN*)tail_k, tail_idx, block_table, seq_lens,
+        bt_stride, hkv, group, sm_log2, n_splits, part_ml, part_o, sync);
+    return kush_check_launch("kush_decode");
+}
 
 }  // namespace kush
 
@@ -430,8 +519,8 @@ using namespace kush;
 extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const void* q, void* out, const void* cache,
                            int64_t block_stride, int64_t head_stride, const void* tail_k, const int32_t* tail_idx,
                            const int32_t* block_table, const int32_t* seq_lens, int64_t bt_stride, int32_t hkv,
-                           float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t n_seqs,
-                           void* stream) {
+                           float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t* split_sync,
+                           int32_t waves, int32_t n_seqs, void* stream) {
     if (n_seqs < 0 || hkv <= 0 || group <= 0 || n_splits <= 0)
         return kush_fail(-2, "kush_decode: bad n_seqs %d / hkv %d / group %d / n_splits %d", n_seqs, hkv, group,
                          n_splits);
@@ -439,18 +528,28 @@ extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const v
         return kush_fail(-2, "kush_decode: n_splits %d needs the partial buffers", n_splits);
     if (((uintptr_t)cache | (uint64_t)block_stride | (uint64_t)head_stride) & 15)
         return kush_fail(-2, "kush_decode: cache records must be 16-byte aligned");
+    if (waves == 0) waves = 4;
+    if (waves != 4 && waves != 8 && waves != 16) return kush_fail(-2, "kush_decode: waves must be 0, 4, 8 or 16");
     const int n_gc = (group + 15) / 16;
     if ((int64_t)n_splits * n_gc > 65535) return kush_fail(-2, "kush_decode: n_splits %d too large", n_splits);
     const float sm_log2 = (float)((double)scale * 1.4426950408889634);
+    const dim3 grid(n_seqs, hkv, n_splits * n_gc);
+    hipStream_t st = (hipStream_t)stream;
     return dispatch_shape(head_dim, bits, dtype, "kush_decode", [&](auto dd, auto bb, auto in) -> int {
         constexpr int D = decltype(dd)::value, BITS = decltype(bb)::value;
         using IN = decltype(in);
         if (n_seqs == 0) return 0;
-        decode_kernel<D, BITS, IN, DECODE_WAVES>
-            <<<dim3(n_seqs, hkv, n_splits * n_gc), dim3(DECODE_WAVES * WAVE), 0, (hipStream_t)stream>>>(
-                (const IN*)q, (IN*)out, (const uint8_t*)cache, block_stride, head_stride, (const IN*)tail_k, tail_idx,
-                block_table, seq_lens, bt_stride, hkv, group, sm_log2, n_splits, part_ml, part_o);
-        return kush_check_launch("kush_decode");
+#define KUSH_DECODE_ARGS grid, st, q, out, cache, block_stride, head_stride, tail_k, tail_idx, block_table, seq_lens, \
+                         bt_stride, hkv, group, sm_log2, n_splits, part_ml, part_o, split_sync
+        if (waves == 16) {
+            if constexpr (decode_lds_bytes<D, BITS, 16>() <= 160 * 1024)
+                return launch_decode<D, BITS, IN, 16>(KUSH_DECODE_ARGS);
+            else
+                return launch_decode<D, BITS, IN, 8>(KUSH_DECODE_ARGS);
+        }
+        if (waves == 8) return launch_decode<D, BITS, IN, 8>(KUSH_DECODE_ARGS);
+        return launch_decode<D, BITS, IN, 4>(KUSH_DECODE_ARGS);
+#undef KUSH_DECODE_ARGS
     });
 }
 

@@ -92,22 +92,32 @@ def test_decode_matches_oracle(D, bits, G, dtype, B, N):
         assert rel < (2e-2 if dtype == torch.bfloat16 else 3e-3), (t, rel)
 
 
+@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("waves", [4, 8, 16])
 @pytest.mark.parametrize("ns", [1, 2, 8, 64, 256])
-def test_split_k_matches_oracle(ns):
-    """Forced split-K factors incl. splits with no pages (ns > pages) and the LSE combine
-    (reference: tests/test_gpu.py:100-111)."""
+def test_split_k_matches_oracle(ns, waves, fused, monkeypatch):
+    """Forced split-K factors incl. splits with no pages (ns > pages), merged inside the decode launch
+    (fused: the last workgroup of each sequence / kv head) or by the combine kernel, for every
+    waves-per-workgroup variant (reference: tests/test_gpu.py:100-111). Two calls in a row check
+    that the merge counters reset themselves."""
+    import kushkash_amd._ops as ops_mod
+    if not fused:
+        monkeypatch.setattr(ops_mod, "SYNC_SLOTS", 0)
     torch.manual_seed(ns)
     B, H, G, D, N = 2, 8, 4, 128, 32 * 100 + 7
     c = kk.KushCache(1, H, H * G, D, batch_size=B, bits=4, device=DEV, dtype=torch.bfloat16, rotate=False)
     K = torch.randn(B, H, N, D, device=DEV, dtype=torch.bfloat16)
     c.write(0, K, K.flip(2))
-    q = torch.randn(B, H * G, D, device=DEV, dtype=torch.bfloat16)
-    out = torch.empty_like(q)
     work = torch.empty(B * H * ns * G * (D + 2), dtype=torch.float32, device=DEV)
-    c.ops.decode(q, out, c.pool[0], c.block_table, c.seq_lens[0], c.tail_idx, c.tail_k[0], c.scale, ns, work)
-    want = oracle_decode(c, 0, q)
-    err = (out.float().cpu() - want).abs().max().item()
-    assert err <= out_tol(want, torch.bfloat16), err
+    for call in range(2):
+        q = torch.randn(B, H * G, D, device=DEV, dtype=torch.bfloat16)
+        out = torch.empty_like(q)
+        c.ops.decode(q, out, c.pool[0], c.block_table, c.seq_lens[0], c.tail_idx, c.tail_k[0], c.scale, ns, work,
+                     waves=waves)
+        want = oracle_decode(c, 0, q)
+        err = (out.float().cpu() - want).abs().max().item()
+        assert err <= out_tol(want, torch.bfloat16), (call, err)
+    assert int(c.ops._sync.abs().sum()) == 0
 
 
 def test_empty_and_short_sequences():
