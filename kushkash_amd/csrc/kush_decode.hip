@@ -33,6 +33,8 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
 constexpr float LOG2E = 1.4426950408889634f;
 
@@ -259,37 +261,35 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
 
     // one page in flight per wave: K code slice in registers, V codes + scales staged through registers
     uint32_t kwn[2][KW];
-    uint4 vn[VCPL];
-    auto issue = [&](int p) {
-        const uint8_t* rec = head_base + (int64_t)bt[p] * bs;
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            const uint8_t* src = rec + (16 * tt + r16) * F::DC + q * KBYTES;
-            if constexpr (KBYTES == 8) {
-                const uint2 v2 = *reinterpret_cast<const uint2*>(src);
-                kwn[tt][0] = v2.x;
-                kwn[tt][1] = v2.y;
-            } else {
-#pragma unroll
-                for (int c = 0; c < KBYTES / 16; ++c) {
-                    const uint4 v4 = reinterpret_cast<const uint4*>(src)[c];
-                    kwn[tt][4 * c + 0] = v4.x;
-                    kwn[tt][4 * c + 1] = v4.y;
-                    kwn[tt][4 * c + 2] = v4.z;
-                    kwn[tt][4 * c + 3] = v4.w;
-                }
-            }
-        }
-        const uint4* vsrc = reinterpret_cast<const uint4*>(rec + F::OFF_VQ);
-#pragma unroll
-        for (int i = 0; i < VCPL; ++i) {
-            const int c = lane + WAVE * i;
-            if (c < S::CHUNKS) vn[i] = vsrc[c];
-        }
-    };
+    u4 vn[VCPL];
+#define KUSH_ISSUE(P_)                                                                                   \
+    do {                                                                                                 \
+        const uint8_t* rec_ = head_base + (int64_t)bt[(P_)] * bs;                                        \
+        _Pragma("unroll") for (int tt = 0; tt < 2; ++tt) {                                               \
+            const uint8_t* src_ = rec_ + (16 * tt + r16) * F::DC + q * KBYTES;                           \
+            if constexpr (KBYTES == 8) {                                                                 \
+                const u2 v2_ = *reinterpret_cast<const u2*>(src_);                                       \
+                kwn[tt][0] = v2_[0];                                                                     \
+                kwn[tt][1] = v2_[1];                                                                     \
+            } else {                                                                                     \
+                _Pragma("unroll") for (int c = 0; c < KBYTES / 16; ++c) {                                \
+                    const u4 v4_ = reinterpret_cast<const u4*>(src_)[c];                                 \
+                    kwn[tt][4 * c + 0] = v4_[0];                                                         \
+                    kwn[tt][4 * c + 1] = v4_[1];                                                         \
+                    kwn[tt][4 * c + 2] = v4_[2];                                                         \
+                    kwn[tt][4 * c + 3] = v4_[3];                                                         \
+                }                                                                                        \
+            }                                                                                            \
+        }                                                                                                \
+        const u4* vsrc_ = reinterpret_cast<const u4*>(rec_ + F::OFF_VQ);                                 \
+        _Pragma("unroll") for (int i = 0; i < VCPL; ++i) {                                               \
+            const int c = lane + WAVE * i;                                                               \
+            vn[i] = c < S::CHUNKS ? vsrc_[c < S::CHUNKS ? c : 0] : u4{0u, 0u, 0u, 0u};                   \
+        }                                                                                                \
+    } while (0)
 
     int p = p0 + w;
-    if (p < p1) issue(p);
+    if (p < p1) KUSH_ISSUE(p);
     for (; p < p1; p += NW) {
         uint32_t kw[2][KW];
 #pragma unroll
@@ -299,9 +299,10 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
 #pragma unroll
         for (int i = 0; i < VCPL; ++i) {
             const int c = lane + WAVE * i;
-            if (c < S::CHUNKS) reinterpret_cast<uint4*>(st)[c] = vn[i];
+            if (c < S::CHUNKS) reinterpret_cast<u4*>(st)[c] = vn[i];
         }
-        if (p + NW < p1) issue(p + NW);
+        if (p + NW < p1) KUSH_ISSUE(p + NW);
+#undef KUSH_ISSUE
 
         f4 sacc[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};
         f4 kacc = f4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -367,11 +368,11 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
             acc[g] += __shfl_xor(acc[g], 32, WAVE);
             if (hf == 0) sc_l[g * PAGE + t] = t < tail_n ? acc[g] : -__builtin_inff();
         }
-        const uint4* vsrc = reinterpret_cast<const uint4*>(head_base + (int64_t)bt[full] * bs + F::OFF_VQ);
+        const u4* vsrc = reinterpret_cast<const u4*>(head_base + (int64_t)bt[full] * bs + F::OFF_VQ);
 #pragma unroll
         for (int i = 0; i < VCPL; ++i) {
             const int c = lane + WAVE * i;
-            if (c < S::CHUNKS) reinterpret_cast<uint4*>(st)[c] = vsrc[c];
+            if (c < S::CHUNKS) reinterpret_cast<u4*>(st)[c] = vsrc[c];
         }
         float x[8];
 #pragma unroll
