@@ -224,7 +224,8 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     __shared__ float m_l[NW * 16], l_l[NW * 16];
     __shared__ int last_flag;
 
-    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);   // wave-uniform: scalar page loop
     const int r16 = lane & 15, q = lane >> 4;
     const int s = blockIdx.x, h = blockIdx.y;
     const int z = blockIdx.z % NS, gc = blockIdx.z / NS, g0 = gc * 16;
@@ -262,9 +263,9 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     // one page in flight per wave: K code slice in registers, V codes + scales staged through registers
     uint32_t kwn[2][KW];
     u4 vn[VCPL];
-#define KUSH_ISSUE(P_)                                                                                   \
+#define KUSH_ISSUE(BLK_)                                                                                 \
     do {                                                                                                 \
-        const uint8_t* rec_ = head_base + (int64_t)bt[(P_)] * bs;                                        \
+        const uint8_t* rec_ = head_base + (int64_t)(BLK_) * bs;                                          \
         _Pragma("unroll") for (int tt = 0; tt < 2; ++tt) {                                               \
             const uint8_t* src_ = rec_ + (16 * tt + r16) * F::DC + q * KBYTES;                           \
             if constexpr (KBYTES == 8) {                                                                 \
@@ -288,8 +289,10 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
         }                                                                                                \
     } while (0)
 
+    // block ids run one page ahead of the data loads, so no iteration waits on a table read
     int p = p0 + w;
-    if (p < p1) KUSH_ISSUE(p);
+    int32_t blk_next = p + NW < p1 ? bt[p + NW] : 0;
+    if (p < p1) KUSH_ISSUE(bt[p]);
     for (; p < p1; p += NW) {
         uint32_t kw[2][KW];
 #pragma unroll
@@ -301,7 +304,10 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
             const int c = lane + WAVE * i;
             if (c < S::CHUNKS) reinterpret_cast<u4*>(st)[c] = vn[i];
         }
-        if (p + NW < p1) KUSH_ISSUE(p + NW);
+        if (p + NW < p1) {
+            KUSH_ISSUE(blk_next);
+            blk_next = p + 2 * NW < p1 ? bt[p + 2 * NW] : 0;
+        }
 #undef KUSH_ISSUE
 
         f4 sacc[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};
@@ -435,8 +441,10 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     }
     if (NS == 1 || sync == nullptr) return;
 
-    // split-K: the last workgroup of this (sequence, kv head, head chunk) merges every split
-    __threadfence();                                        // this thread's partials, visible device-wide
+    // split-K: the last workgroup of this (sequence, kv head, head chunk) merges every split. The
+    // barrier completes every wave's partial stores; one agent-scope release (L2 writeback) by thread
+    // 0 then publishes them before the counter moves, and the last workgroup's thread 0 acquires
+    // (L2 invalidate) before its waves read the other splits.
     __syncthreads();
     if (threadIdx.x == 0) {
         const int n_gc = gridDim.z / NS;
@@ -447,7 +455,6 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     }
     __syncthreads();
     if (!last_flag) return;
-    __threadfence();                                        // acquire: see every split's partials
     const int64_t base = ((int64_t)s * H + h) * NS;
     for (int i = threadIdx.x; i < Gc * D; i += NW * WAVE) {
         const int g = g0 + i / D, d = i % D;
