@@ -201,7 +201,7 @@ __device__ __forceinline__ void consume_page(const uint8_t* st, f4 (&o)[D / 16],
 // NS > 1: each workgroup writes its split's partials; with `sync` (one zeroed int32 per
 // (sequence, kv head, head chunk)), the last workgroup of a (sequence, kv head, head chunk) to
 // finish merges all splits into `out` and resets its counter, so no second launch is needed.
-template <int D, int BITS, typename IN, int NW>
+template <int D, int BITS, typename IN, int NW, int PF>
 __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     const IN* __restrict__ qg, IN* __restrict__ out, const uint8_t* __restrict__ cache, int64_t bs, int64_t hs,
     const IN* __restrict__ tail_k, const int32_t* __restrict__ tail_idx, const int32_t* __restrict__ block_table,
@@ -241,6 +241,45 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     const bool has_tail = tail_n > 0 && z == NS - 1;
     uint8_t* st = stage_all + w * STAGE;
 
+    // PF pages in flight per wave: K code slices in registers, V codes + scales staged through
+    // registers, one ring slot per page; the loop is unrolled over the ring so slots stay in VGPRs.
+    uint32_t kwn[PF][2][KW];
+    u4 vn[PF][VCPL];
+#define KUSH_ISSUE(SLOT_, BLK_)                                                                          \
+    do {                                                                                                 \
+        const uint8_t* rec_ = head_base + (int64_t)(BLK_) * bs;                                          \
+        _Pragma("unroll") for (int tt = 0; tt < 2; ++tt) {                                               \
+            const uint8_t* src_ = rec_ + (16 * tt + r16) * F::DC + q * KBYTES;                           \
+            if constexpr (KBYTES == 8) {                                                                 \
+                const u2 v2_ = *reinterpret_cast<const u2*>(src_);                                       \
+                kwn[SLOT_][tt][0] = v2_[0];                                                              \
+                kwn[SLOT_][tt][1] = v2_[1];                                                              \
+            } else {                                                                                     \
+                _Pragma("unroll") for (int c = 0; c < KBYTES / 16; ++c) {                                \
+                    const u4 v4_ = reinterpret_cast<const u4*>(src_)[c];                                 \
+                    kwn[SLOT_][tt][4 * c + 0] = v4_[0];                                                  \
+                    kwn[SLOT_][tt][4 * c + 1] = v4_[1];                                                  \
+                    kwn[SLOT_][tt][4 * c + 2] = v4_[2];                                                  \
+                    kwn[SLOT_][tt][4 * c + 3] = v4_[3];                                                  \
+                }                                                                                        \
+            }                                                                                            \
+        }                                                                                                \
+        const u4* vsrc_ = reinterpret_cast<const u4*>(rec_ + F::OFF_VQ);                                 \
+        _Pragma("unroll") for (int i = 0; i < VCPL; ++i) {                                               \
+            const int c = lane + WAVE * i;                                                               \
+            vn[SLOT_][i] = c < S::CHUNKS ? vsrc_[c < S::CHUNKS ? c : 0] : u4{0u, 0u, 0u, 0u};            \
+        }                                                                                                \
+    } while (0)
+
+    // the first pages are requested before the q prologue so their latency overlaps it
+    int32_t bnext[PF];                       // block ids of the round after the one in flight
+#pragma unroll
+    for (int slot = 0; slot < PF; ++slot) {
+        const int pp = p0 + w + slot * NW, pn = pp + PF * NW;
+        if (pp < p1) KUSH_ISSUE(slot, bt[pp]);
+        bnext[slot] = pn < p1 ? bt[pn] : 0;
+    }
+
     for (int i = threadIdx.x; i < KSTEPS * WAVE * 8; i += NW * WAVE) {
         const int kk = i / (WAVE * 8), l = (i / 8) % WAVE, j = i % 8;
         const int g = l & 15;
@@ -260,96 +299,70 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     for (int dt = 0; dt < DT; ++dt) o[dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     float m_run = -__builtin_inff(), l_run = 0.0f, vb_run = 0.0f;
 
-    // one page in flight per wave: K code slice in registers, V codes + scales staged through registers
-    uint32_t kwn[2][KW];
-    u4 vn[VCPL];
-#define KUSH_ISSUE(BLK_)                                                                                 \
-    do {                                                                                                 \
-        const uint8_t* rec_ = head_base + (int64_t)(BLK_) * bs;                                          \
-        _Pragma("unroll") for (int tt = 0; tt < 2; ++tt) {                                               \
-            const uint8_t* src_ = rec_ + (16 * tt + r16) * F::DC + q * KBYTES;                           \
-            if constexpr (KBYTES == 8) {                                                                 \
-                const u2 v2_ = *reinterpret_cast<const u2*>(src_);                                       \
-                kwn[tt][0] = v2_[0];                                                                     \
-                kwn[tt][1] = v2_[1];                                                                     \
-            } else {                                                                                     \
-                _Pragma("unroll") for (int c = 0; c < KBYTES / 16; ++c) {                                \
-                    const u4 v4_ = reinterpret_cast<const u4*>(src_)[c];                                 \
-                    kwn[tt][4 * c + 0] = v4_[0];                                                         \
-                    kwn[tt][4 * c + 1] = v4_[1];                                                         \
-                    kwn[tt][4 * c + 2] = v4_[2];                                                         \
-                    kwn[tt][4 * c + 3] = v4_[3];                                                         \
-                }                                                                                        \
-            }                                                                                            \
-        }                                                                                                \
-        const u4* vsrc_ = reinterpret_cast<const u4*>(rec_ + F::OFF_VQ);                                 \
-        _Pragma("unroll") for (int i = 0; i < VCPL; ++i) {                                               \
-            const int c = lane + WAVE * i;                                                               \
-            vn[i] = c < S::CHUNKS ? vsrc_[c < S::CHUNKS ? c : 0] : u4{0u, 0u, 0u, 0u};                   \
-        }                                                                                                \
-    } while (0)
-
-    // block ids run one page ahead of the data loads, so no iteration waits on a table read
-    int p = p0 + w;
-    int32_t blk_next = p + NW < p1 ? bt[p + NW] : 0;
-    if (p < p1) KUSH_ISSUE(bt[p]);
-    for (; p < p1; p += NW) {
-        uint32_t kw[2][KW];
+    for (int pb = p0 + w; pb < p1; pb += PF * NW) {
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
+        for (int slot = 0; slot < PF; ++slot) {
+            const int p = pb + slot * NW;
+            if (p >= p1) break;
+            uint32_t kw[2][KW];
 #pragma unroll
-            for (int i = 0; i < KW; ++i) kw[tt][i] = kwn[tt][i];
+            for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int i = 0; i < VCPL; ++i) {
-            const int c = lane + WAVE * i;
-            if (c < S::CHUNKS) reinterpret_cast<u4*>(st)[c] = vn[i];
-        }
-        if (p + NW < p1) {
-            KUSH_ISSUE(blk_next);
-            blk_next = p + 2 * NW < p1 ? bt[p + 2 * NW] : 0;
-        }
-#undef KUSH_ISSUE
-
-        f4 sacc[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};
-        f4 kacc = f4{0.0f, 0.0f, 0.0f, 0.0f};
+                for (int i = 0; i < KW; ++i) kw[tt][i] = kwn[slot][tt][i];
 #pragma unroll
-        for (int kk = 0; kk < KSTEPS; ++kk) {
-            h8 ks8, kb8;
-            if constexpr (BITS == 4) {
-                const int d0 = q * (D / 8) + 4 * kk;
-                const h4v a = *reinterpret_cast<const h4v*>(st + S::KS + 2 * d0);
-                const h4v b = *reinterpret_cast<const h4v*>(st + S::KS + 2 * (d0 + D / 2));
-                const h4v c = *reinterpret_cast<const h4v*>(st + S::KB + 2 * d0);
-                const h4v d = *reinterpret_cast<const h4v*>(st + S::KB + 2 * (d0 + D / 2));
-                ks8 = h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-                kb8 = h8{c[0], c[1], c[2], c[3], d[0], d[1], d[2], d[3]};
-            } else {
-                const int d0 = q * (D / 4) + 8 * kk;
-                ks8 = *reinterpret_cast<const h8*>(st + S::KS + 2 * d0);
-                kb8 = *reinterpret_cast<const h8*>(st + S::KB + 2 * d0);
+            for (int i = 0; i < VCPL; ++i) {
+                const int c = lane + WAVE * i;
+                if (c < S::CHUNKS) reinterpret_cast<u4*>(st)[c] = vn[slot][i];
             }
-            const h8 qh = qhl[kk * WAVE + lane];
-            const h8 ql = qll[kk * WAVE + lane];
-            // K bias dot: every row of A is this lane group's k_bias slice, so every output row is
-            // sum_d kb[d] q[g][d]: all four accumulators of lane (q, g) hold it, no reduction needed
-            kacc = mfma16(kb8, qh, kacc);
-            kacc = mfma16(kb8, ql, kacc);
-            const h8 qp = qh * ks8;                           // fp16 multiply, as the reference TC path
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-                h8 a;
-                if constexpr (BITS == 4)
-                    a = int4_codes(kw[tt][kk]);
-                else
-                    a = int8_codes(kw[tt][2 * kk], kw[tt][2 * kk + 1]);
-                sacc[tt] = mfma16(a, qp, sacc[tt]);
+            const int pn = p + PF * NW;
+            if (pn < p1) {
+                KUSH_ISSUE(slot, bnext[slot]);
+                const int pnn = pn + PF * NW;
+                bnext[slot] = pnn < p1 ? bt[pnn] : 0;
             }
-        }
-        float x[8];
+
+            f4 sacc[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};
+            f4 kacc = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = sacc[j >> 2][j & 3] + kacc[0];
-        consume_page<D, BITS>(st, o, x, PAGE, m_run, l_run, vb_run, lane);
+            for (int kk = 0; kk < KSTEPS; ++kk) {
+                h8 ks8, kb8;
+                if constexpr (BITS == 4) {
+                    const int d0 = q * (D / 8) + 4 * kk;
+                    const h4v a = *reinterpret_cast<const h4v*>(st + S::KS + 2 * d0);
+                    const h4v b = *reinterpret_cast<const h4v*>(st + S::KS + 2 * (d0 + D / 2));
+                    const h4v c = *reinterpret_cast<const h4v*>(st + S::KB + 2 * d0);
+                    const h4v d = *reinterpret_cast<const h4v*>(st + S::KB + 2 * (d0 + D / 2));
+                    ks8 = h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+                    kb8 = h8{c[0], c[1], c[2], c[3], d[0], d[1], d[2], d[3]};
+                } else {
+                    const int d0 = q * (D / 4) + 8 * kk;
+                    ks8 = *reinterpret_cast<const h8*>(st + S::KS + 2 * d0);
+                    kb8 = *reinterpret_cast<const h8*>(st + S::KB + 2 * d0);
+                }
+                const h8 qh = qhl[kk * WAVE + lane];
+                const h8 ql = qll[kk * WAVE + lane];
+                // K bias dot: every row of A is this lane group's k_bias slice, so every output row is
+                // sum_d kb[d] q[g][d]: all four accumulators of lane (q, g) hold it, no reduction needed
+                kacc = mfma16(kb8, qh, kacc);
+                kacc = mfma16(kb8, ql, kacc);
+                const h8 qp = qh * ks8;                           // fp16 multiply, as the reference TC path
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    h8 a;
+                    if constexpr (BITS == 4)
+                        a = int4_codes(kw[tt][kk]);
+                    else
+                        a = int8_codes(kw[tt][2 * kk], kw[tt][2 * kk + 1]);
+                    sacc[tt] = mfma16(a, qp, sacc[tt]);
+                }
+            }
+            float x[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = sacc[j >> 2][j & 3] + kacc[0];
+            consume_page<D, BITS>(st, o, x, PAGE, m_run, l_run, vb_run, lane);
+        }
     }
+#undef KUSH_ISSUE
 
     // partial last page: exact K from the tail, V rows from its record (last split only)
     if (has_tail && w == (p1 - p0) % NW) {
@@ -509,12 +522,12 @@ constexpr int decode_lds_bytes() {
     return NW * Stage<D, BITS>::BYTES + 2 * (D / 32) * WAVE * 16 + 16 * D * 4 + 16 * PAGE * 4 + 2 * NW * 16 * 4 + 16;
 }
 
-template <int D, int BITS, typename IN, int NW>
+template <int D, int BITS, typename IN, int NW, int PF>
 static int launch_decode(dim3 grid, hipStream_t stream, const void* q, void* out, const void* cache, int64_t bs,
                          int64_t hs, const void* tail_k, const int32_t* tail_idx, const int32_t* block_table,
                          const int32_t* seq_lens, int64_t bt_stride, int hkv, int group, float sm_log2, int n_splits,
                          float* part_ml, float* part_o, int32_t* sync) {
-    decode_kernel<D, BITS, IN, NW><<<grid, dim3(NW * WAVE), 0, stream>>>(
+    decode_kernel<D, BITS, IN, NW, PF><<<grid, dim3(NW * WAVE), 0, stream>>>(
         (const IN*)q, (IN*)out, (const uint8_t*)cache, bs, hs, (const IN*)tail_k, tail_idx, block_table, seq_lens,
         bt_stride, hkv, group, sm_log2, n_splits, part_ml, part_o, sync);
     return kush_check_launch("kush_decode");
@@ -536,8 +549,13 @@ extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const v
         return kush_fail(-2, "kush_decode: n_splits %d needs the partial buffers", n_splits);
     if (((uintptr_t)cache | (uint64_t)block_stride | (uint64_t)head_stride) & 15)
         return kush_fail(-2, "kush_decode: cache records must be 16-byte aligned");
+    // waves: low byte = waves per workgroup (4, 8, 16; 0 = 4), next byte = pages in flight per wave
+    int depth = (waves >> 8) & 0xff;
+    waves &= 0xff;
     if (waves == 0) waves = 4;
+    if (depth == 0) depth = 1;
     if (waves != 4 && waves != 8 && waves != 16) return kush_fail(-2, "kush_decode: waves must be 0, 4, 8 or 16");
+    if (depth < 1 || depth > 3) return kush_fail(-2, "kush_decode: prefetch depth must be 1, 2 or 3");
     const int n_gc = (group + 15) / 16;
     if ((int64_t)n_splits * n_gc > 65535) return kush_fail(-2, "kush_decode: n_splits %d too large", n_splits);
     const float sm_log2 = (float)((double)scale * 1.4426950408889634);
@@ -551,12 +569,17 @@ extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const v
                          bt_stride, hkv, group, sm_log2, n_splits, part_ml, part_o, split_sync
         if (waves == 16) {
             if constexpr (decode_lds_bytes<D, BITS, 16>() <= 160 * 1024)
-                return launch_decode<D, BITS, IN, 16>(KUSH_DECODE_ARGS);
+                return launch_decode<D, BITS, IN, 16, 1>(KUSH_DECODE_ARGS);
             else
-                return launch_decode<D, BITS, IN, 8>(KUSH_DECODE_ARGS);
+                return launch_decode<D, BITS, IN, 8, 1>(KUSH_DECODE_ARGS);
         }
-        if (waves == 8) return launch_decode<D, BITS, IN, 8>(KUSH_DECODE_ARGS);
-        return launch_decode<D, BITS, IN, 4>(KUSH_DECODE_ARGS);
+        if (waves == 8) {
+            if (depth == 3) return launch_decode<D, BITS, IN, 8, 3>(KUSH_DECODE_ARGS);
+            if (depth == 2) return launch_decode<D, BITS, IN, 8, 2>(KUSH_DECODE_ARGS);
+            return launch_decode<D, BITS, IN, 8, 1>(KUSH_DECODE_ARGS);
+        }
+        if (depth == 2) return launch_decode<D, BITS, IN, 4, 2>(KUSH_DECODE_ARGS);
+        return launch_decode<D, BITS, IN, 4, 1>(KUSH_DECODE_ARGS);
 #undef KUSH_DECODE_ARGS
     });
 }
