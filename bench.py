@@ -52,6 +52,7 @@ def parse_args(argv=None):
     ap.add_argument("--splits", type=int, default=0, help="split-K factor (0: Ops.splits policy)")
     ap.add_argument("--waves", type=int, default=0, help="waves per decode workgroup (0: Ops.waves policy)")
     ap.add_argument("--sweep", default="", help="comma list of splits:waves[:depth] to time (extra lines on stderr)")
+    ap.add_argument("--sequential", action="store_true", help="pages in order instead of a random permutation")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline")
     return ap.parse_args(argv)
@@ -70,7 +71,8 @@ def make_workload(a, dev):
     cache = torch.zeros(nblk, Hkv, RB, dtype=torch.uint8, device=dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
-    perm = torch.randperm(nblk, generator=gen, device=dev).to(torch.int32)
+    perm = (torch.arange(nblk, device=dev) if a.sequential
+            else torch.randperm(nblk, generator=gen, device=dev)).to(torch.int32)
     tables = [perm[i * B * pages:(i + 1) * B * pages].view(B, pages).contiguous() for i in range(a.pools)]
     tail_k = torch.zeros(B, Hkv, PAGE, D, dtype=dtype, device=dev)
     tail_idx = torch.arange(B, dtype=torch.int32, device=dev)
