@@ -51,7 +51,7 @@ def parse_args(argv=None):
     ap.add_argument("--pools", type=int, default=4, help="independent KV pools rotated across steps")
     ap.add_argument("--splits", type=int, default=0, help="split-K factor (0: Ops.splits policy)")
     ap.add_argument("--waves", type=int, default=0, help="waves per decode workgroup (0: Ops.waves policy)")
-    ap.add_argument("--sweep", default="", help="comma list of splits:waves[:depth] to time (extra lines on stderr)")
+    ap.add_argument("--sweep", default="", help="comma list of splits:waves to time (extra lines on stderr)")
     ap.add_argument("--sequential", action="store_true", help="pages in order instead of a random permutation")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline")
@@ -221,11 +221,9 @@ def main(argv=None):
     for item in [x for x in a.sweep.split(",") if x.strip()]:
         parts = [int(v) for v in item.split(":")]
         sns, swv = parts[0], parts[1]
-        if len(parts) > 2:
-            swv |= parts[2] << 8                   # prefetch depth rides in the second byte of `waves`
         g, _ = graphs_for(w, sns, swv)
         msx = time_graphs(g, a.steps, a.warmup)
-        print(f"splits {sns:4d} waves {swv & 255:3d} depth {max(1, swv >> 8)}: {msx * 1e3:8.2f} us/step  {alg / msx / 1e6:7.1f} GB/s "
+        print(f"splits {sns:4d} waves {swv:3d}: {msx * 1e3:8.2f} us/step  {alg / msx / 1e6:7.1f} GB/s "
               f"({100 * alg / msx / 1e6 / PEAK_HBM_GBS:5.1f}% of peak)", file=sys.stderr, flush=True)
         del g
 

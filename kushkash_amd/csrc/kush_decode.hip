@@ -40,36 +40,11 @@ constexpr float LOG2E = 1.4426950408889634f;
 
 __device__ __forceinline__ h2 as_h2(uint32_t x) { return __builtin_bit_cast(h2, x); }
 
-// Four two's-complement nibble codes per byte pair of w -> exact fp16. Slots 0-3: low nibbles of
-// bytes 0-3, slots 4-7: high nibbles. n ^ 8 = c + 8 for a signed nibble c; placed under the fp16
-// exponent of 1024 it reads 1024 + c + 8, and one packed subtract leaves c.
-__device__ __forceinline__ h8 int4_codes(uint32_t w) {
-    const uint32_t x = w ^ 0x88888888u;
-    const uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
-    const h2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-    const h2 a = as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u)) + off;
-    const h2 b = as_h2(__builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u)) + off;
-    const h2 c = as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u)) + off;
-    const h2 d = as_h2(__builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u)) + off;
-    return h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
-}
-
-// Eight signed int8 codes (two words) -> exact fp16 (c + 128 under the exponent of 1024).
-__device__ __forceinline__ h8 int8_codes(uint32_t w0, uint32_t w1) {
-    const uint32_t x0 = w0 ^ 0x80808080u, x1 = w1 ^ 0x80808080u;
-    const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-    const h2 a = as_h2(__builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u)) + off;
-    const h2 b = as_h2(__builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u)) + off;
-    const h2 c = as_h2(__builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u)) + off;
-    const h2 d = as_h2(__builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u)) + off;
-    return h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
-}
-
 __device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
 
-// Physical dim of contraction slot j of lane group q in K-step kk (QK^T). int4: the lane's 16-byte
-// slice of a row holds dims [q D/8, (q+1) D/8) in low nibbles and the same + D/2 in high nibbles;
-// K-step kk takes bytes 4kk..4kk+3 of it. int8: dims q D/4 + 8 kk + j.
+// Physical dim of contraction slot j of lane group q in K-step kk (QK^T). int4: the lane's slice of
+// a row holds dims [q D/8, (q+1) D/8) in low nibbles and the same + D/2 in high nibbles; K-step kk
+// takes bytes 4kk..4kk+3 of it. int8: dims q D/4 + 8 kk + j.
 template <int D, int BITS>
 __device__ __forceinline__ int kdim(int kk, int q, int j) {
     if constexpr (BITS == 4)
@@ -82,28 +57,79 @@ __device__ __forceinline__ int kdim(int kk, int q, int j) {
 // group q hold in register j % 4 of tile j / 4.
 __device__ __forceinline__ int tok(int q, int j) { return 16 * (j >> 2) + 4 * q + (j & 3); }
 
+// ------------------------------------------------------------------ LDS page stage
+// A wave stages whole records in a ring of LDS slots with buffer-to-LDS DMA (64 lanes x 16 bytes per
+// instruction, lane l -> 16-byte chunk l of the instruction's 1 KB). Chunks of the 64 code rows are
+// placed XOR-swizzled within their row, chunk c of row r at position c ^ swz(r), so the column-wise
+// V gathers and the K row reads spread over the 64 LDS banks; the scales and biases stay in place.
+// The swizzle is applied on the source side: the lane that fills LDS chunk L loads record chunk
+// src_chunk(L).
 template <int D, int BITS>
-struct Stage {                                     // wave-private LDS copy of a record's tail part
+struct Ring {
     using F = Fmt<D, BITS>;
-    static constexpr int BYTES = F::REC - F::OFF_VQ;   // V codes + ks + kb + vs + vb
-    static constexpr int CHUNKS = BYTES / 16;
-    static constexpr int KS = F::OFF_KS - F::OFF_VQ;
-    static constexpr int KB = F::OFF_KB - F::OFF_VQ;
-    static constexpr int VS = F::OFF_VS - F::OFF_VQ;
-    static constexpr int VB = F::OFF_VB - F::OFF_VQ;
+    static constexpr int CPR = F::DC / 16;                  // 16-byte chunks per code row
+    static constexpr int CODE_CHUNKS = 64 * CPR;            // K rows then V rows
+    static constexpr int CHUNKS = F::REC / 16;
+    static constexpr int DMA = (CHUNKS + WAVE - 1) / WAVE;   // 1 KB instructions per page
+    static constexpr int SLOT = DMA * WAVE * 16;            // LDS bytes per ring slot
+    static constexpr int RSHIFT = F::DC >= 256 ? 0 : (F::DC == 128 ? 1 : (F::DC == 64 ? 2 : 3));
 };
 
 template <int D, int BITS>
-__device__ __forceinline__ void stage_record(const uint8_t* __restrict__ rec, uint8_t* st, int lane) {
-    using F = Fmt<D, BITS>;
-    using S = Stage<D, BITS>;
-    const uint4* src = reinterpret_cast<const uint4*>(rec + F::OFF_VQ);
-    uint4* dst = reinterpret_cast<uint4*>(st);
-#pragma unroll
-    for (int i = 0; i < (S::CHUNKS + WAVE - 1) / WAVE; ++i) {
-        const int c = lane + WAVE * i;
-        if (c < S::CHUNKS) dst[c] = src[c];
-    }
+__device__ __forceinline__ int swz(int r) {
+    using R = Ring<D, BITS>;
+    return ((r & 31) >> R::RSHIFT) & (R::CPR - 1);
+}
+
+// byte offset in a slot of record chunk c (16 bytes) of code row r (0-31 K, 32-63 V)
+template <int D, int BITS>
+__device__ __forceinline__ int slot_chunk(int r, int c) {
+    using R = Ring<D, BITS>;
+    return (r * R::CPR + (c ^ swz<D, BITS>(r))) * 16;
+}
+
+template <int D, int BITS>
+__device__ __forceinline__ uint32_t src_chunk(int L) {
+    using R = Ring<D, BITS>;
+    if (L >= R::CODE_CHUNKS) return (uint32_t)L;             // scales / biases (and padding) in place
+    const int r = L / R::CPR, j = L % R::CPR;
+    return (uint32_t)(r * R::CPR + (j ^ swz<D, BITS>(r)));
+}
+
+// s_waitcnt with only vmcnt(N) (gfx9 encoding: vmcnt [3:0] + [15:14], expcnt [6:4], lgkmcnt [11:8])
+#define KUSH_WAIT_VM(N) __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+// Subnormal fp16 codes: the bit pattern n (0..255) is the fp16 value n * 2^-24, exact, so unsigned
+// code bytes become MFMA operands with one byte shuffle and no arithmetic; the products are exact in
+// fp32 and the 2^24 is applied to the fp32 results. n = c + HALF: the HALF offset is removed through
+// the bias terms. perm(x, 0, 0x0C010C00) = bytes [x0, 0, x1, 0].
+__device__ __forceinline__ h8 sub_codes4(uint32_t lo, uint32_t hi) {    // 4 + 4 nibble values, masked
+    return h8{__builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, lo, 0x0C010C00u))[0],
+              __builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, lo, 0x0C010C00u))[1],
+              __builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, lo, 0x0C030C02u))[0],
+              __builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, lo, 0x0C030C02u))[1],
+              __builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, hi, 0x0C010C00u))[0],
+              __builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, hi, 0x0C010C00u))[1],
+              __builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, hi, 0x0C030C02u))[0],
+              __builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, hi, 0x0C030C02u))[1]};
+}
+
+// int4 word (4 bytes, two nibbles each) -> slots 0-3: low nibbles, 4-7: high nibbles, as n = c + 8
+__device__ __forceinline__ h8 int4_sub(uint32_t w) {
+    const uint32_t x = w ^ 0x88888888u;
+    return sub_codes4(x & 0x0F0F0F0Fu, (x >> 4) & 0x0F0F0F0Fu);
+}
+
+// two int4 words -> (low nibbles of both, high nibbles of both), as n = c + 8
+__device__ __forceinline__ void int4_sub2(uint32_t w0, uint32_t w1, h8& lo, h8& hi) {
+    const uint32_t x0 = w0 ^ 0x88888888u, x1 = w1 ^ 0x88888888u;
+    lo = sub_codes4(x0 & 0x0F0F0F0Fu, x1 & 0x0F0F0F0Fu);
+    hi = sub_codes4((x0 >> 4) & 0x0F0F0F0Fu, (x1 >> 4) & 0x0F0F0F0Fu);
+}
+
+// two int8 words (8 codes) -> n = c + 128
+__device__ __forceinline__ h8 int8_sub(uint32_t w0, uint32_t w1) {
+    return sub_codes4(w0 ^ 0x80808080u, w1 ^ 0x80808080u);
 }
 
 // max / sum over the 4 lanes l, l ^ 16, l ^ 32, l ^ 48 (one q head's lane groups), on the VALU
@@ -123,24 +149,27 @@ __device__ __forceinline__ float rows_sum(float x) {
 
 typedef int v2i __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) v2i lds_v2i;
+typedef __attribute__((address_space(3))) void lds_void;
 
 // V^T operand gather: within each 16-lane group, ds_read_b64_tr_b8 hands output lane i byte
 // (i % 8) of the 8-byte rows supplied by lanes 2k + (i % 16) / 8, k = 0..7. Lane (2k + half) of
-// group q supplies token tok(q, k) at byte column 16 ct + 8 half, so lane r of the group receives
+// group q supplies V token tok(q, k) at byte column 16 ct + 8 half, so lane r of the group receives
 // byte column 16 ct + r of its 8 tokens, in PV slot order.
-__device__ __forceinline__ v2i gather_vt(const uint8_t* st, int dc, int ct, int lane) {
+template <int D, int BITS>
+__device__ __forceinline__ v2i gather_vt(const uint8_t* slot, int ct, int lane) {
     const int s16 = lane & 15, q = lane >> 4;
-    const uint8_t* src = st + tok(q, s16 >> 1) * dc + 16 * ct + 8 * (s16 & 1);
+    const uint8_t* src = slot + slot_chunk<D, BITS>(32 + tok(q, s16 >> 1), ct) + 8 * (s16 & 1);
     return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(src));
 }
 
-// Softmax update of one page (scores x in log2 units, tokens tok(q, j); tokens >= valid masked)
-// and its PV accumulation from the staged V codes.
+// Softmax update of one page (scores x in log2 units, tokens tok(q, j); tokens >= valid masked) and
+// its PV accumulation from the staged V codes. o accumulates in units of 2^-24 (subnormal codes);
+// vb_run carries the V biases and the code offset: v = vs * (n - HALF) + vb = vs * n + (vb - HALF vs).
 template <int D, int BITS>
-__device__ __forceinline__ void consume_page(const uint8_t* st, f4 (&o)[D / 16], const float (&x)[8], int valid,
+__device__ __forceinline__ void consume_page(const uint8_t* slot, f4 (&o)[D / 16], const float (&x)[8], int valid,
                                              float& m_run, float& l_run, float& vb_run, int lane) {
     using F = Fmt<D, BITS>;
-    using S = Stage<D, BITS>;
+    constexpr float HALF = (float)F::HALF;
     const int q = lane >> 4;
     float pm = x[0];
 #pragma unroll
@@ -148,10 +177,10 @@ __device__ __forceinline__ void consume_page(const uint8_t* st, f4 (&o)[D / 16],
     const float m_new = __builtin_fmaxf(m_run, rows_max(pm));
     const float corr = __builtin_amdgcn_exp2f(m_run - m_new);   // first page: exp2(-inf) = 0
 
-    const h4v vs0 = *reinterpret_cast<const h4v*>(st + S::VS + 8 * q);
-    const h4v vs1 = *reinterpret_cast<const h4v*>(st + S::VS + 32 + 8 * q);
-    const h4v vb0 = *reinterpret_cast<const h4v*>(st + S::VB + 8 * q);
-    const h4v vb1 = *reinterpret_cast<const h4v*>(st + S::VB + 32 + 8 * q);
+    const h4v vs0 = *reinterpret_cast<const h4v*>(slot + F::OFF_VS + 8 * q);
+    const h4v vs1 = *reinterpret_cast<const h4v*>(slot + F::OFF_VS + 32 + 8 * q);
+    const h4v vb0 = *reinterpret_cast<const h4v*>(slot + F::OFF_VB + 8 * q);
+    const h4v vb1 = *reinterpret_cast<const h4v*>(slot + F::OFF_VB + 32 + 8 * q);
     float lsum = 0.0f, vbsum = 0.0f;
     h8 pw;
 #pragma unroll
@@ -160,9 +189,10 @@ __device__ __forceinline__ void consume_page(const uint8_t* st, f4 (&o)[D / 16],
         const float vsj = (float)(j < 4 ? vs0[j] : vs1[j - 4]);
         const float vbj = (float)(j < 4 ? vb0[j] : vb1[j - 4]);
         const float e = ok ? __builtin_amdgcn_exp2f(x[j] - m_new) : 0.0f;
+        const float ev = e * vsj;
         lsum += e;
-        vbsum += ok ? e * vbj : 0.0f;
-        pw[j] = (_Float16)(ok ? e * vsj : 0.0f);
+        vbsum += ok ? e * vbj - HALF * ev : 0.0f;
+        pw[j] = (_Float16)(ok ? ev : 0.0f);
     }
     l_run = l_run * corr + lsum;
     vb_run = vb_run * corr + vbsum;
@@ -175,50 +205,62 @@ __device__ __forceinline__ void consume_page(const uint8_t* st, f4 (&o)[D / 16],
     constexpr int NCOL = BITS == 4 ? D / 32 : D / 16;
 #pragma unroll
     for (int ct = 0; ct < NCOL; ++ct) {
-        const v2i w = gather_vt(st, F::DC, ct, lane);
+        const v2i w = gather_vt<D, BITS>(slot, ct, lane);
         if constexpr (BITS == 4) {
-            const uint32_t x0 = (uint32_t)w[0] ^ 0x88888888u, x1 = (uint32_t)w[1] ^ 0x88888888u;
-            const uint32_t l0 = x0 & 0x0F0F0F0Fu, l1 = x1 & 0x0F0F0F0Fu;
-            const uint32_t u0 = (x0 >> 4) & 0x0F0F0F0Fu, u1 = (x1 >> 4) & 0x0F0F0F0Fu;
-            const h2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-            const h2 a = as_h2(__builtin_amdgcn_perm(0x64646464u, l0, 0x04010400u)) + off;
-            const h2 b = as_h2(__builtin_amdgcn_perm(0x64646464u, l0, 0x04030402u)) + off;
-            const h2 c = as_h2(__builtin_amdgcn_perm(0x64646464u, l1, 0x04010400u)) + off;
-            const h2 d = as_h2(__builtin_amdgcn_perm(0x64646464u, l1, 0x04030402u)) + off;
-            const h2 e = as_h2(__builtin_amdgcn_perm(0x64646464u, u0, 0x04010400u)) + off;
-            const h2 f = as_h2(__builtin_amdgcn_perm(0x64646464u, u0, 0x04030402u)) + off;
-            const h2 g = as_h2(__builtin_amdgcn_perm(0x64646464u, u1, 0x04010400u)) + off;
-            const h2 hh = as_h2(__builtin_amdgcn_perm(0x64646464u, u1, 0x04030402u)) + off;
-            o[ct] = mfma16(h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]}, pw, o[ct]);
-            o[ct + D / 32] = mfma16(h8{e[0], e[1], f[0], f[1], g[0], g[1], hh[0], hh[1]}, pw, o[ct + D / 32]);
+            h8 lo, hi;
+            int4_sub2((uint32_t)w[0], (uint32_t)w[1], lo, hi);
+            o[ct] = mfma16(lo, pw, o[ct]);
+            o[ct + D / 32] = mfma16(hi, pw, o[ct + D / 32]);
         } else {
-            o[ct] = mfma16(int8_codes((uint32_t)w[0], (uint32_t)w[1]), pw, o[ct]);
+            o[ct] = mfma16(int8_sub((uint32_t)w[0], (uint32_t)w[1]), pw, o[ct]);
         }
     }
+}
+
+// Static LDS of one decode workgroup: NW rings of RING slots, q for the exact-K tail (also the merge
+// buffer), tail scores, per-wave softmax state.
+template <int D, int BITS, int NW, int RING>
+constexpr int decode_lds_bytes() {
+    return NW * RING * Ring<D, BITS>::SLOT + 16 * D * 4 + 16 * PAGE * 4 + 2 * NW * 16 * 4 + 16;
+}
+
+// Ring depth for NW waves: the deepest ring (4 at most) that keeps 8 waves per CU within its 160 KB
+// of LDS (NW = 8: one workgroup per CU; NW = 4: two; NW = 2: four). Records too large for that get
+// the whole CU at NW = 2 (occupancy then bounded by LDS); 0 if no ring of 2 fits at all.
+template <int D, int BITS, int NW>
+constexpr int ring_fit(int budget) {
+    for (int r = 4; r >= 2; --r)
+        if (decode_lds_bytes<D, BITS, NW, 4>() - (4 - r) * NW * Ring<D, BITS>::SLOT <= budget) return r;
+    return 0;
+}
+
+template <int D, int BITS, int NW>
+constexpr int ring_for() {
+    constexpr int shared = ring_fit<D, BITS, NW>(150 * 1024 * NW / 8);
+    return shared >= 2 || NW != 2 ? shared : ring_fit<D, BITS, NW>(150 * 1024);
 }
 
 // grid (S, Hkv, n_splits * ceil(G / 16)), block NW * 64.
 // NS > 1: each workgroup writes its split's partials; with `sync` (one zeroed int32 per
 // (sequence, kv head, head chunk)), the last workgroup of a (sequence, kv head, head chunk) to
 // finish merges all splits into `out` and resets its counter, so no second launch is needed.
-template <int D, int BITS, typename IN, int NW, int PF>
+template <int D, int BITS, typename IN, int NW, int RING>
 __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     const IN* __restrict__ qg, IN* __restrict__ out, const uint8_t* __restrict__ cache, int64_t bs, int64_t hs,
     const IN* __restrict__ tail_k, const int32_t* __restrict__ tail_idx, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ seq_lens, int64_t bt_stride, int H, int G, float sm_log2, int NS,
     float* __restrict__ part_ml, float* __restrict__ part_o, int32_t* __restrict__ sync) {
     using F = Fmt<D, BITS>;
-    using S = Stage<D, BITS>;
+    using R = Ring<D, BITS>;
     constexpr int KSTEPS = D / 32;
     constexpr int DT = D / 16;
     constexpr int KBYTES = F::DC / 4;                // K code bytes per lane per 16-token tile
     constexpr int KW = KBYTES / 4;
-    constexpr int STAGE = S::BYTES;
-    constexpr int VCPL = (S::CHUNKS + WAVE - 1) / WAVE;
+    constexpr float HALF = (float)F::HALF;
+    constexpr float TWO24 = 16777216.0f;
+    static_assert(RING >= 2, "a ring needs two slots");
 
-    __shared__ __align__(16) uint8_t stage_all[NW * STAGE];
-    __shared__ __align__(16) h8 qhl[KSTEPS * WAVE];   // fp16(q sm log2e) in each lane's contraction order
-    __shared__ __align__(16) h8 qll[KSTEPS * WAVE];   // fp16 remainder: hi + lo carries q to ~2^-22
+    __shared__ __align__(1024) uint8_t ring_all[NW * RING * R::SLOT];
     __shared__ __align__(16) float qs_l[16 * D];     // fp32 q sm log2e for the exact-K tail; then merge buffer
     __shared__ float sc_l[16 * PAGE];                // tail scores
     __shared__ float m_l[NW * 16], l_l[NW * 16];
@@ -239,134 +281,126 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     const uint8_t* head_base = cache + (int64_t)h * hs;
     const int64_t qbase = ((int64_t)s * H + h) * G * D + (int64_t)g0 * D;
     const bool has_tail = tail_n > 0 && z == NS - 1;
-    uint8_t* st = stage_all + w * STAGE;
+    uint8_t* ring = ring_all + w * RING * R::SLOT;
 
-    // PF pages in flight per wave: K code slices in registers, V codes + scales staged through
-    // registers, one ring slot per page; the loop is unrolled over the ring so slots stay in VGPRs.
-    uint32_t kwn[PF][2][KW];
-    u4 vn[PF][VCPL];
-#define KUSH_ISSUE(SLOT_, BLK_)                                                                          \
-    do {                                                                                                 \
-        const uint8_t* rec_ = head_base + (int64_t)(BLK_) * bs;                                          \
-        _Pragma("unroll") for (int tt = 0; tt < 2; ++tt) {                                               \
-            const uint8_t* src_ = rec_ + (16 * tt + r16) * F::DC + q * KBYTES;                           \
-            if constexpr (KBYTES == 8) {                                                                 \
-                const u2 v2_ = *reinterpret_cast<const u2*>(src_);                                       \
-                kwn[SLOT_][tt][0] = v2_[0];                                                              \
-                kwn[SLOT_][tt][1] = v2_[1];                                                              \
-            } else {                                                                                     \
-                _Pragma("unroll") for (int c = 0; c < KBYTES / 16; ++c) {                                \
-                    const u4 v4_ = reinterpret_cast<const u4*>(src_)[c];                                 \
-                    kwn[SLOT_][tt][4 * c + 0] = v4_[0];                                                  \
-                    kwn[SLOT_][tt][4 * c + 1] = v4_[1];                                                  \
-                    kwn[SLOT_][tt][4 * c + 2] = v4_[2];                                                  \
-                    kwn[SLOT_][tt][4 * c + 3] = v4_[3];                                                  \
-                }                                                                                        \
-            }                                                                                            \
-        }                                                                                                \
-        const u4* vsrc_ = reinterpret_cast<const u4*>(rec_ + F::OFF_VQ);                                 \
-        _Pragma("unroll") for (int i = 0; i < VCPL; ++i) {                                               \
-            const int c = lane + WAVE * i;                                                               \
-            vn[SLOT_][i] = c < S::CHUNKS ? vsrc_[c < S::CHUNKS ? c : 0] : u4{0u, 0u, 0u, 0u};            \
-        }                                                                                                \
-    } while (0)
-
-    // the first pages are requested before the q prologue so their latency overlaps it
-    int32_t bnext[PF];                       // block ids of the round after the one in flight
+    // per-lane DMA source offsets (swizzled code rows), fixed for every page
+    uint32_t voff[R::DMA];
 #pragma unroll
-    for (int slot = 0; slot < PF; ++slot) {
-        const int pp = p0 + w + slot * NW, pn = pp + PF * NW;
-        if (pp < p1) KUSH_ISSUE(slot, bt[pp]);
-        bnext[slot] = pn < p1 ? bt[pn] : 0;
-    }
+    for (int i = 0; i < R::DMA; ++i) voff[i] = src_chunk<D, BITS>(WAVE * i + lane) * 16u;
 
-    for (int i = threadIdx.x; i < KSTEPS * WAVE * 8; i += NW * WAVE) {
-        const int kk = i / (WAVE * 8), l = (i / 8) % WAVE, j = i % 8;
-        const int g = l & 15;
-        const float xq = g < Gc ? to_f32(qg[qbase + (int64_t)g * D + kdim<D, BITS>(kk, l >> 4, j)]) * sm_log2 : 0.0f;
-        const _Float16 hi = (_Float16)xq;
-        reinterpret_cast<_Float16*>(&qhl[kk * WAVE + l])[j] = hi;
-        reinterpret_cast<_Float16*>(&qll[kk * WAVE + l])[j] = (_Float16)(xq - (float)hi);
-    }
+    // Page j of this wave is p0 + w + j NW; it lands in slot j % RING. Every issue is R::DMA
+    // instructions, also past the end (an empty buffer range: no memory access), so vmcnt counts
+    // stay exact: before reading page j, at most (RING - 2) later pages may still be in flight.
+    const int np = p1 - p0 > w ? (p1 - p0 - w + NW - 1) / NW : 0;       // pages of this wave
+    auto issue = [&](int j) {
+        const bool valid = j < np;
+        const int blk = valid ? bt[p0 + w + j * NW] : 0;
+        const uint8_t* rec = head_base + (int64_t)blk * bs;
+        const __amdgpu_buffer_rsrc_t rsrc =
+            __builtin_amdgcn_make_buffer_rsrc((void*)rec, 0, valid ? F::REC : 0, 0x00020000);
+        uint8_t* dst = ring + (j % RING) * R::SLOT;
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < R::DMA; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(dst + i * WAVE * 16), 16, voff[i], 0, 0, 0);
+        asm volatile("" ::: "memory");
+    };
+#pragma unroll
+    for (int j = 0; j < RING - 1; ++j) issue(j);
+
+    // this lane's q head (B column r16) over its contraction dims, as an fp16 hi / lo pair
+    const bool gv = r16 < Gc;
+    h8 qh[KSTEPS], ql[KSTEPS];
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float xq = gv ? to_f32(qg[qbase + (int64_t)r16 * D + kdim<D, BITS>(kk, q, j)]) * sm_log2 : 0.0f;
+            const _Float16 hi = (_Float16)xq;
+            qh[kk][j] = hi;
+            ql[kk][j] = (_Float16)(xq - (float)hi);
+        }
     if (has_tail) {
         for (int i = threadIdx.x; i < 16 * D; i += NW * WAVE)
             qs_l[i] = i / D < Gc ? to_f32(qg[qbase + i]) * sm_log2 : 0.0f;
     }
-    __syncthreads();
+    const h8 neg_half = h8{(_Float16)-HALF, (_Float16)-HALF, (_Float16)-HALF, (_Float16)-HALF,
+                           (_Float16)-HALF, (_Float16)-HALF, (_Float16)-HALF, (_Float16)-HALF};
 
     f4 o[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     float m_run = -__builtin_inff(), l_run = 0.0f, vb_run = 0.0f;
 
-    for (int pb = p0 + w; pb < p1; pb += PF * NW) {
-#pragma unroll
-        for (int slot = 0; slot < PF; ++slot) {
-            const int p = pb + slot * NW;
-            if (p >= p1) break;
-            uint32_t kw[2][KW];
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-                for (int i = 0; i < KW; ++i) kw[tt][i] = kwn[slot][tt][i];
-#pragma unroll
-            for (int i = 0; i < VCPL; ++i) {
-                const int c = lane + WAVE * i;
-                if (c < S::CHUNKS) reinterpret_cast<u4*>(st)[c] = vn[slot][i];
-            }
-            const int pn = p + PF * NW;
-            if (pn < p1) {
-                KUSH_ISSUE(slot, bnext[slot]);
-                const int pnn = pn + PF * NW;
-                bnext[slot] = pnn < p1 ? bt[pnn] : 0;
-            }
+    for (int j = 0; j < np; ++j) {
+        KUSH_WAIT_VM(R::DMA * (RING - 2));                       // page j has landed in its slot
+        issue(j + RING - 1);                                     // refills the slot page j - 1 used
+        const uint8_t* slot = ring + (j % RING) * R::SLOT;
 
-            f4 sacc[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};
-            f4 kacc = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        f4 sacc[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};
+        f4 kacc = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int kk = 0; kk < KSTEPS; ++kk) {
-                h8 ks8, kb8;
-                if constexpr (BITS == 4) {
-                    const int d0 = q * (D / 8) + 4 * kk;
-                    const h4v a = *reinterpret_cast<const h4v*>(st + S::KS + 2 * d0);
-                    const h4v b = *reinterpret_cast<const h4v*>(st + S::KS + 2 * (d0 + D / 2));
-                    const h4v c = *reinterpret_cast<const h4v*>(st + S::KB + 2 * d0);
-                    const h4v d = *reinterpret_cast<const h4v*>(st + S::KB + 2 * (d0 + D / 2));
-                    ks8 = h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-                    kb8 = h8{c[0], c[1], c[2], c[3], d[0], d[1], d[2], d[3]};
-                } else {
-                    const int d0 = q * (D / 4) + 8 * kk;
-                    ks8 = *reinterpret_cast<const h8*>(st + S::KS + 2 * d0);
-                    kb8 = *reinterpret_cast<const h8*>(st + S::KB + 2 * d0);
-                }
-                const h8 qh = qhl[kk * WAVE + lane];
-                const h8 ql = qll[kk * WAVE + lane];
-                // K bias dot: every row of A is this lane group's k_bias slice, so every output row is
-                // sum_d kb[d] q[g][d]: all four accumulators of lane (q, g) hold it, no reduction needed
-                kacc = mfma16(kb8, qh, kacc);
-                kacc = mfma16(kb8, ql, kacc);
-                const h8 qp = qh * ks8;                           // fp16 multiply, as the reference TC path
-#pragma unroll
-                for (int tt = 0; tt < 2; ++tt) {
-                    h8 a;
-                    if constexpr (BITS == 4)
-                        a = int4_codes(kw[tt][kk]);
-                    else
-                        a = int8_codes(kw[tt][2 * kk], kw[tt][2 * kk + 1]);
-                    sacc[tt] = mfma16(a, qp, sacc[tt]);
-                }
+        for (int kk = 0; kk < KSTEPS; ++kk) {
+            h8 ks8, kb8;
+            if constexpr (BITS == 4) {
+                const int d0 = q * (D / 8) + 4 * kk;
+                const h4v a = *reinterpret_cast<const h4v*>(slot + F::OFF_KS + 2 * d0);
+                const h4v b = *reinterpret_cast<const h4v*>(slot + F::OFF_KS + 2 * (d0 + D / 2));
+                const h4v c = *reinterpret_cast<const h4v*>(slot + F::OFF_KB + 2 * d0);
+                const h4v d = *reinterpret_cast<const h4v*>(slot + F::OFF_KB + 2 * (d0 + D / 2));
+                ks8 = h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+                kb8 = h8{c[0], c[1], c[2], c[3], d[0], d[1], d[2], d[3]};
+            } else {
+                const int d0 = q * (D / 4) + 8 * kk;
+                ks8 = *reinterpret_cast<const h8*>(slot + F::OFF_KS + 2 * d0);
+                kb8 = *reinterpret_cast<const h8*>(slot + F::OFF_KB + 2 * d0);
             }
-            float x[8];
+            const h8 qp = qh[kk] * ks8;                       // fp16 multiply, as the reference TC path
+            // bias terms: every row of A is the same vector, so every output row holds the sum for
+            // head g = r16: sum_d kb[d] q[g][d] (hi + lo) - HALF sum_d Q'[g][d] (the code offset)
+            kacc = mfma16(kb8, qh[kk], kacc);
+            kacc = mfma16(kb8, ql[kk], kacc);
+            kacc = mfma16(neg_half, qp, kacc);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) x[j] = sacc[j >> 2][j & 3] + kacc[0];
-            consume_page<D, BITS>(st, o, x, PAGE, m_run, l_run, vb_run, lane);
+            for (int tt = 0; tt < 2; ++tt) {
+                // K code slice of row 16 tt + r16 for this K-step, read from the swizzled slot
+                const int row = 16 * tt + r16;
+                h8 a;
+                if constexpr (BITS == 4) {
+                    // bytes q KBYTES + 4 kk .. + 3 of the row
+                    const int byte = q * KBYTES + 4 * kk;
+                    const uint32_t wv =
+                        *reinterpret_cast<const uint32_t*>(slot + slot_chunk<D, BITS>(row, byte / 16) + byte % 16);
+                    a = int4_sub(wv);
+                } else {
+                    const int byte = q * KBYTES + 8 * kk;
+                    const u2 wv = *reinterpret_cast<const u2*>(slot + slot_chunk<D, BITS>(row, byte / 16) + byte % 16);
+                    a = int8_sub(wv[0], wv[1]);
+                }
+                sacc[tt] = mfma16(a, qp, sacc[tt]);
+            }
         }
+        float x[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) x[jj] = __builtin_fmaf(sacc[jj >> 2][jj & 3], TWO24, kacc[0]);
+        consume_page<D, BITS>(slot, o, x, PAGE, m_run, l_run, vb_run, lane);
     }
-#undef KUSH_ISSUE
+    KUSH_WAIT_VM(0);                                             // drain the trailing (empty) issues
+    __syncthreads();                                             // qs_l ready; rings idle
 
     // partial last page: exact K from the tail, V rows from its record (last split only)
     if (has_tail && w == (p1 - p0) % NW) {
         const IN* tk = tail_k + ((int64_t)tail_idx[s] * H + h) * PAGE * D;
+        uint8_t* slot = ring;
+        {
+            const uint8_t* rec = head_base + (int64_t)bt[full] * bs;
+            const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)rec, 0, F::REC, 0x00020000);
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int i = 0; i < R::DMA; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(slot + i * WAVE * 16), 16, voff[i], 0, 0, 0);
+            asm volatile("" ::: "memory");
+        }
         const int t = lane & 31, hf = lane >> 5;
         float acc[16];
 #pragma unroll
@@ -387,16 +421,11 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
             acc[g] += __shfl_xor(acc[g], 32, WAVE);
             if (hf == 0) sc_l[g * PAGE + t] = t < tail_n ? acc[g] : -__builtin_inff();
         }
-        const u4* vsrc = reinterpret_cast<const u4*>(head_base + (int64_t)bt[full] * bs + F::OFF_VQ);
-#pragma unroll
-        for (int i = 0; i < VCPL; ++i) {
-            const int c = lane + WAVE * i;
-            if (c < S::CHUNKS) reinterpret_cast<u4*>(st)[c] = vsrc[c];
-        }
         float x[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = sc_l[r16 * PAGE + tok(q, j)];
-        consume_page<D, BITS>(st, o, x, tail_n, m_run, l_run, vb_run, lane);
+        for (int jj = 0; jj < 8; ++jj) x[jj] = sc_l[r16 * PAGE + tok(q, jj)];
+        KUSH_WAIT_VM(0);
+        consume_page<D, BITS>(slot, o, x, tail_n, m_run, l_run, vb_run, lane);
     }
 
     // merge the waves: every wave rescales to the workgroup max and adds into LDS in turn
@@ -421,7 +450,7 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int idx = r16 * D + 16 * dt + 4 * q + i;
-                    const float val = (o[dt][i] + vb_run) * f;
+                    const float val = __builtin_fmaf(o[dt][i], TWO24, vb_run) * f;
                     mbuf[idx] = ww == 0 ? val : mbuf[idx] + val;
                 }
         }
@@ -516,18 +545,13 @@ __global__ __launch_bounds__(256) void combine_kernel(IN* __restrict__ out, cons
     }
 }
 
-// Static LDS of one decode workgroup (must stay within the 160 KB of a gfx950 CU).
-template <int D, int BITS, int NW>
-constexpr int decode_lds_bytes() {
-    return NW * Stage<D, BITS>::BYTES + 2 * (D / 32) * WAVE * 16 + 16 * D * 4 + 16 * PAGE * 4 + 2 * NW * 16 * 4 + 16;
-}
-
-template <int D, int BITS, typename IN, int NW, int PF>
+template <int D, int BITS, typename IN, int NW>
 static int launch_decode(dim3 grid, hipStream_t stream, const void* q, void* out, const void* cache, int64_t bs,
                          int64_t hs, const void* tail_k, const int32_t* tail_idx, const int32_t* block_table,
                          const int32_t* seq_lens, int64_t bt_stride, int hkv, int group, float sm_log2, int n_splits,
                          float* part_ml, float* part_o, int32_t* sync) {
-    decode_kernel<D, BITS, IN, NW, PF><<<grid, dim3(NW * WAVE), 0, stream>>>(
+    constexpr int RING = ring_for<D, BITS, NW>();
+    decode_kernel<D, BITS, IN, NW, RING><<<grid, dim3(NW * WAVE), 0, stream>>>(
         (const IN*)q, (IN*)out, (const uint8_t*)cache, bs, hs, (const IN*)tail_k, tail_idx, block_table, seq_lens,
         bt_stride, hkv, group, sm_log2, n_splits, part_ml, part_o, sync);
     return kush_check_launch("kush_decode");
@@ -549,13 +573,8 @@ extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const v
         return kush_fail(-2, "kush_decode: n_splits %d needs the partial buffers", n_splits);
     if (((uintptr_t)cache | (uint64_t)block_stride | (uint64_t)head_stride) & 15)
         return kush_fail(-2, "kush_decode: cache records must be 16-byte aligned");
-    // waves: low byte = waves per workgroup (4, 8, 16; 0 = 4), next byte = pages in flight per wave
-    int depth = (waves >> 8) & 0xff;
-    waves &= 0xff;
-    if (waves == 0) waves = 4;
-    if (depth == 0) depth = 1;
-    if (waves != 4 && waves != 8 && waves != 16) return kush_fail(-2, "kush_decode: waves must be 0, 4, 8 or 16");
-    if (depth < 1 || depth > 3) return kush_fail(-2, "kush_decode: prefetch depth must be 1, 2 or 3");
+    if (waves == 0) waves = 8;
+    if (waves != 2 && waves != 4 && waves != 8) return kush_fail(-2, "kush_decode: waves must be 0, 2, 4 or 8");
     const int n_gc = (group + 15) / 16;
     if ((int64_t)n_splits * n_gc > 65535) return kush_fail(-2, "kush_decode: n_splits %d too large", n_splits);
     const float sm_log2 = (float)((double)scale * 1.4426950408889634);
@@ -567,19 +586,14 @@ extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const v
         if (n_seqs == 0) return 0;
 #define KUSH_DECODE_ARGS grid, st, q, out, cache, block_stride, head_stride, tail_k, tail_idx, block_table, seq_lens, \
                          bt_stride, hkv, group, sm_log2, n_splits, part_ml, part_o, split_sync
-        if (waves == 16) {
-            if constexpr (decode_lds_bytes<D, BITS, 16>() <= 160 * 1024)
-                return launch_decode<D, BITS, IN, 16, 1>(KUSH_DECODE_ARGS);
-            else
-                return launch_decode<D, BITS, IN, 8, 1>(KUSH_DECODE_ARGS);
+        // the largest of the requested, 4 and 2 waves whose rings fit in LDS
+        if (waves >= 8) {
+            if constexpr (ring_for<D, BITS, 8>() >= 2) return launch_decode<D, BITS, IN, 8>(KUSH_DECODE_ARGS);
         }
-        if (waves == 8) {
-            if (depth == 3) return launch_decode<D, BITS, IN, 8, 3>(KUSH_DECODE_ARGS);
-            if (depth == 2) return launch_decode<D, BITS, IN, 8, 2>(KUSH_DECODE_ARGS);
-            return launch_decode<D, BITS, IN, 8, 1>(KUSH_DECODE_ARGS);
+        if (waves >= 4) {
+            if constexpr (ring_for<D, BITS, 4>() >= 2) return launch_decode<D, BITS, IN, 4>(KUSH_DECODE_ARGS);
         }
-        if (depth == 2) return launch_decode<D, BITS, IN, 4, 2>(KUSH_DECODE_ARGS);
-        return launch_decode<D, BITS, IN, 4, 1>(KUSH_DECODE_ARGS);
+        return launch_decode<D, BITS, IN, 2>(KUSH_DECODE_ARGS);
 #undef KUSH_DECODE_ARGS
     });
 }
