@@ -217,6 +217,26 @@ __device__ __forceinline__ void consume_page(const uint8_t* slot, f4 (&o)[D / 16
     }
 }
 
+// Stage page j of a wave (block bt_w[j * nw]) into ring slot j % RING: R::DMA buffer-to-LDS loads of
+// 1 KB. Past the wave's last page (j >= np) the buffer range is empty, so the loads touch no memory
+// but still count in vmcnt like a real page.
+template <int D, int BITS, int RING>
+__device__ __forceinline__ void issue_page(uint8_t* ring, int j, int np, const int32_t* __restrict__ bt_w, int nw,
+                                           const uint8_t* head_base, int64_t bs, const uint32_t* voff) {
+    using F = Fmt<D, BITS>;
+    using R = Ring<D, BITS>;
+    const bool valid = j < np;
+    const int blk = valid ? bt_w[j * nw] : 0;
+    const uint8_t* rec = head_base + (int64_t)blk * bs;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)rec, 0, valid ? F::REC : 0, 0x00020000);
+    uint8_t* dst = ring + (j % RING) * R::SLOT;
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < R::DMA; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(dst + i * WAVE * 16), 16, voff[i], 0, 0, 0);
+    asm volatile("" ::: "memory");
+}
+
 // Static LDS of one decode workgroup: NW rings of RING slots, q for the exact-K tail (also the merge
 // buffer), tail scores, per-wave softmax state.
 template <int D, int BITS, int NW, int RING>
@@ -292,21 +312,9 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     // instructions, also past the end (an empty buffer range: no memory access), so vmcnt counts
     // stay exact: before reading page j, at most (RING - 2) later pages may still be in flight.
     const int np = p1 - p0 > w ? (p1 - p0 - w + NW - 1) / NW : 0;       // pages of this wave
-    auto issue = [&](int j) {
-        const bool valid = j < np;
-        const int blk = valid ? bt[p0 + w + j * NW] : 0;
-        const uint8_t* rec = head_base + (int64_t)blk * bs;
-        const __amdgpu_buffer_rsrc_t rsrc =
-            __builtin_amdgcn_make_buffer_rsrc((void*)rec, 0, valid ? F::REC : 0, 0x00020000);
-        uint8_t* dst = ring + (j % RING) * R::SLOT;
-        asm volatile("" ::: "memory");
 #pragma unroll
-        for (int i = 0; i < R::DMA; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(dst + i * WAVE * 16), 16, voff[i], 0, 0, 0);
-        asm volatile("" ::: "memory");
-    };
-#pragma unroll
-    for (int j = 0; j < RING - 1; ++j) issue(j);
+    for (int j = 0; j < RING - 1; ++j)
+        issue_page<D, BITS, RING>(ring, j, np, bt + p0 + w, NW, head_base, bs, voff);
 
     // this lane's q head (B column r16) over its contraction dims, as an fp16 hi / lo pair
     const bool gv = r16 < Gc;
@@ -334,7 +342,7 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
 
     for (int j = 0; j < np; ++j) {
         KUSH_WAIT_VM(R::DMA * (RING - 2));                       // page j has landed in its slot
-        issue(j + RING - 1);                                     // refills the slot page j - 1 used
+        issue_page<D, BITS, RING>(ring, j + RING - 1, np, bt + p0 + w, NW, head_base, bs, voff);   // slot of page j - 1
         const uint8_t* slot = ring + (j % RING) * R::SLOT;
 
         f4 sacc[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};
@@ -391,16 +399,8 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     // partial last page: exact K from the tail, V rows from its record (last split only)
     if (has_tail && w == (p1 - p0) % NW) {
         const IN* tk = tail_k + ((int64_t)tail_idx[s] * H + h) * PAGE * D;
-        uint8_t* slot = ring;
-        {
-            const uint8_t* rec = head_base + (int64_t)bt[full] * bs;
-            const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)rec, 0, F::REC, 0x00020000);
-            asm volatile("" ::: "memory");
-#pragma unroll
-            for (int i = 0; i < R::DMA; ++i)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(slot + i * WAVE * 16), 16, voff[i], 0, 0, 0);
-            asm volatile("" ::: "memory");
-        }
+        uint8_t* slot = ring;                                    // slot 0 of this wave's ring
+        issue_page<D, BITS, RING>(ring, 0, 1, bt + full, 0, head_base, bs, voff);
         const int t = lane & 31, hf = lane >> 5;
         float acc[16];
 #pragma unroll
