@@ -2,8 +2,8 @@
 
 Headline workload ("C2"): Qwen2.5-7B-shaped layer, 28 q heads / 4 kv
 heads (GQA 7), head_dim 128, int4 records, page 32, batch 64 x exactly 4096 cached tokens, bf16 q
-and output. One step = one decode-attention pass of that layer (decode kernel + split-K combine),
-replayed from HIP graphs with the inputs resident in HBM.
+and output. One step = one decode-attention pass of that layer (one kernel: the split-K merge is
+fused), with the inputs resident in HBM; the timed steps run back to back from one HIP graph.
 
 Synthetic data (seed 0, generated on the GPU in this order): per pool, K = N(0,1) with a per-channel
 bias ~ N(0, 6^2) (sigma 6) on a seeded 10% of the channels of each kv head (13 of 128), V = N(0,1),
@@ -15,7 +15,7 @@ The 155 MB of records of one pool fit in the 256 MB Infinity Cache, so steps rot
 cache.
 
 Prints one JSON line (the driver's contract) with "roofline" (decode kernel: algorithmic bytes /
-its mean duration, from HIP events around graph replays of the decode kernel alone) and
+its mean duration, from HIP events around the graph of decode kernels) and
 "cpu_baseline" (the C restatement of the reference CPU path, oracle/, on the host cores).
 """
 from __future__ import annotations
@@ -40,7 +40,7 @@ PAGE = 32
 def parse_args(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200, help="timed steps (graph replays)")
+    ap.add_argument("--steps", type=int, default=200, help="timed steps (one graph of that many launches)")
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--ctx", type=int, default=4096)
@@ -112,40 +112,44 @@ def algorithmic_bytes(w) -> int:
     return rec + tail_b + qo + B * w["pages"] * 4 + B * 4
 
 
-def graphs_for(w, ns: int, waves: int):
-    """One HIP graph per pool holding one decode step (a single kernel: split-K partials are merged
-    inside it by the last workgroup of each (sequence, kv head))."""
+def graph_of(w, ns: int, waves: int, n_steps: int):
+    """One HIP graph holding n_steps decode steps back to back, step i on pool i % pools (as a model's
+    decode graph holds one attention launch per layer): graph launch cost is paid once per replay, not
+    once per step. Each step is a single kernel (split-K partials are merged inside it by the last
+    workgroup of each (sequence, kv head))."""
     ops, B, Hkv, G, D = w["ops"], w["B"], w["Hkv"], w["G"], w["D"]
     out = torch.empty_like(w["q"])
     work = torch.empty(max(1, B * Hkv * ns * G * (D + 2)), dtype=torch.float32, device=w["q"].device)
     sm = 1.0 / math.sqrt(D)
+    P = len(w["tables"])
 
     def step(i):
-        ops.decode(w["q"], out, w["cache"], w["tables"][i], w["seq_lens"], w["tail_idx"], w["tail_k"], sm, ns, work,
-                   waves=waves)
+        ops.decode(w["q"], out, w["cache"], w["tables"][i % P], w["seq_lens"], w["tail_idx"], w["tail_k"], sm, ns,
+                   work, waves=waves)
 
-    graphs = []
-    for i in range(len(w["tables"])):
+    for i in range(P):                     # eager first call per pool (lazy init outside the capture)
         step(i)
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            step(i)
-        graphs.append(g)
     torch.cuda.synchronize()
-    return graphs, out
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n_steps):
+            step(i)
+    torch.cuda.synchronize()
+    return g, out
 
 
-def time_graphs(graphs, steps: int, warmup: int) -> float:
-    """Mean ms per replay, HIP events on the replay stream, pools rotated every step."""
-    P = len(graphs)
-    for i in range(warmup):
-        graphs[i % P].replay()
+def time_steps(w, ns: int, waves: int, steps: int, warmup: int) -> float:
+    """Mean ms per step: `warmup` untimed steps (a graph of their own), then exactly `steps` steps in
+    one graph replay bracketed by synchronizations and HIP events on the replay stream."""
+    if warmup:
+        gw, _ = graph_of(w, ns, waves, warmup)
+        gw.replay()
+        del gw
+    g, _ = graph_of(w, ns, waves, steps)
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
-    for i in range(steps):
-        graphs[i % P].replay()
+    g.replay()
     b.record()
     torch.cuda.synchronize()
     return a.elapsed_time(b) / steps
@@ -221,15 +225,12 @@ def main(argv=None):
     for item in [x for x in a.sweep.split(",") if x.strip()]:
         parts = [int(v) for v in item.split(":")]
         sns, swv = parts[0], parts[1]
-        g, _ = graphs_for(w, sns, swv)
-        msx = time_graphs(g, a.steps, a.warmup)
+        msx = time_steps(w, sns, swv, a.steps, a.warmup)
         print(f"splits {sns:4d} waves {swv:3d}: {msx * 1e3:8.2f} us/step  {alg / msx / 1e6:7.1f} GB/s "
               f"({100 * alg / msx / 1e6 / PEAK_HBM_GBS:5.1f}% of peak)", file=sys.stderr, flush=True)
-        del g
 
     wv = a.waves or w["ops"].waves(w["B"], w["Hkv"], ns)
-    graphs, out = graphs_for(w, ns, wv)
-    ms = time_graphs(graphs, a.steps, a.warmup)
+    ms = time_steps(w, ns, wv, a.steps, a.warmup)
     ms_dec = ms                                   # one kernel per step: the decode kernel is the step
     gbs = alg / ms / 1e6
     gbs_dec = alg / ms_dec / 1e6
@@ -259,7 +260,6 @@ def main(argv=None):
                      "algorithmic_bytes": alg},
         "cpu_baseline": None,
     }
-    del graphs
     if not a.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(w, a.cpu_seconds)
     print(json.dumps(res), flush=True)

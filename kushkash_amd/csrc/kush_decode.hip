@@ -42,15 +42,41 @@ __device__ __forceinline__ h2 as_h2(uint32_t x) { return __builtin_bit_cast(h2, 
 
 __device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
 
-// Physical dim of contraction slot j of lane group q in K-step kk (QK^T). int4: the lane's slice of
-// a row holds dims [q D/8, (q+1) D/8) in low nibbles and the same + D/2 in high nibbles; K-step kk
-// takes bytes 4kk..4kk+3 of it. int8: dims q D/4 + 8 kk + j.
+// Physical dim of contraction slot j of lane group q in K-step kk (QK^T). The lane owns bytes
+// [q KB, (q+1) KB) of each code row (KB = DC / 4). int4: K-steps come in pairs over 8 of those
+// bytes, 2 pr and 2 pr + 1 taking their low and high nibbles, so the 8 dims of a K-step are
+// consecutive and its scales and biases are one 16-byte read. int8: dims q D/4 + 8 kk + j.
 template <int D, int BITS>
 __device__ __forceinline__ int kdim(int kk, int q, int j) {
     if constexpr (BITS == 4)
-        return (j < 4 ? 0 : D / 2) + q * (D / 8) + 4 * kk + (j & 3);
+        return (kk & 1) * (D / 2) + q * (D / 8) + 8 * (kk >> 1) + j;
     else
         return q * (D / 4) + 8 * kk + j;
+}
+
+// 8 consecutive elements as fp32, one or two 16-byte loads (p 16-byte aligned)
+__device__ __forceinline__ void load8(const float* p, float (&x)[8]) {
+    const f4 a = *reinterpret_cast<const f4*>(p), b = *reinterpret_cast<const f4*>(p + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        x[j] = a[j];
+        x[j + 4] = b[j];
+    }
+}
+
+__device__ __forceinline__ void load8(const _Float16* p, float (&x)[8]) {
+    const h8 v = *reinterpret_cast<const h8*>(p);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = (float)v[j];
+}
+
+__device__ __forceinline__ void load8(const bf16_t* p, float (&x)[8]) {
+    const u4 v = *reinterpret_cast<const u4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        x[2 * i] = __uint_as_float(v[i] << 16);
+        x[2 * i + 1] = __uint_as_float(v[i] & 0xFFFF0000u);
+    }
 }
 
 // Token of slot j of lane group q in the PV contraction: the token the QK^T accumulators of lane
@@ -75,10 +101,18 @@ struct Ring {
     static constexpr int RSHIFT = F::DC >= 256 ? 0 : (F::DC == 128 ? 1 : (F::DC == 64 ? 2 : 3));
 };
 
+// Swizzle of code row r (0-31 K, 32-63 V). K rows are read row-wise (16 rows by 16 lanes):
+// rows r and r + 4 (DC = 64) must land on different banks, so the swizzle takes the row bits
+// above those that already select the bank. V rows are gathered column-wise, 16 tokens per half
+// wave, t = 16 a + 4 q + b (b < 4, q the lane group, a the tile); u = b | (q & 1) << 2 | a << 3
+// indexes them, and the swizzle takes the bits of u that the row address leaves on one bank.
 template <int D, int BITS>
 __device__ __forceinline__ int swz(int r) {
     using R = Ring<D, BITS>;
-    return ((r & 31) >> R::RSHIFT) & (R::CPR - 1);
+    if (r < 32) return (r >> R::RSHIFT) & (R::CPR - 1);
+    const int t = r - 32;
+    const int u = (t & 3) | (((t >> 2) & 1) << 2) | (((t >> 4) & 1) << 3);
+    return (u >> R::RSHIFT) & (R::CPR - 1);
 }
 
 // byte offset in a slot of record chunk c (16 bytes) of code row r (0-31 K, 32-63 V)
@@ -104,20 +138,8 @@ __device__ __forceinline__ uint32_t src_chunk(int L) {
 // fp32 and the 2^24 is applied to the fp32 results. n = c + HALF: the HALF offset is removed through
 // the bias terms. perm(x, 0, 0x0C010C00) = bytes [x0, 0, x1, 0].
 __device__ __forceinline__ h8 sub_codes4(uint32_t lo, uint32_t hi) {    // 4 + 4 nibble values, masked
-    return h8{__builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, lo, 0x0C010C00u))[0],
-              __builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, lo, 0x0C010C00u))[1],
-              __builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, lo, 0x0C030C02u))[0],
-              __builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, lo, 0x0C030C02u))[1],
-              __builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, hi, 0x0C010C00u))[0],
-              __builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, hi, 0x0C010C00u))[1],
-              __builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, hi, 0x0C030C02u))[0],
-              __builtin_bit_cast(h2, __builtin_amdgcn_perm(0u, hi, 0x0C030C02u))[1]};
-}
-
-// int4 word (4 bytes, two nibbles each) -> slots 0-3: low nibbles, 4-7: high nibbles, as n = c + 8
-__device__ __forceinline__ h8 int4_sub(uint32_t w) {
-    const uint32_t x = w ^ 0x88888888u;
-    return sub_codes4(x & 0x0F0F0F0Fu, (x >> 4) & 0x0F0F0F0Fu);
+    return __builtin_bit_cast(h8, u4{__builtin_amdgcn_perm(0u, lo, 0x0C010C00u), __builtin_amdgcn_perm(0u, lo, 0x0C030C02u),
+                                     __builtin_amdgcn_perm(0u, hi, 0x0C010C00u), __builtin_amdgcn_perm(0u, hi, 0x0C030C02u)});
 }
 
 // two int4 words -> (low nibbles of both, high nibbles of both), as n = c + 8
@@ -174,7 +196,10 @@ __device__ __forceinline__ void consume_page(const uint8_t* slot, f4 (&o)[D / 16
     float pm = x[0];
 #pragma unroll
     for (int j = 1; j < 8; ++j) pm = __builtin_fmaxf(pm, x[j]);
-    const float m_new = __builtin_fmaxf(m_run, rows_max(pm));
+    // the reference point of the exponentials moves only when the page max exceeds it by more than
+    // 2^3: weights stay <= 8 (P' = e vs stays far from fp16 overflow) and most pages skip the O rescale
+    pm = rows_max(pm);
+    const float m_new = pm > m_run + 3.0f ? pm : m_run;
     const float corr = __builtin_amdgcn_exp2f(m_run - m_new);   // first page: exp2(-inf) = 0
 
     const h4v vs0 = *reinterpret_cast<const h4v*>(slot + F::OFF_VS + 8 * q);
@@ -217,24 +242,75 @@ __device__ __forceinline__ void consume_page(const uint8_t* slot, f4 (&o)[D / 16
     }
 }
 
-// Stage page j of a wave (block bt_w[j * nw]) into ring slot j % RING: R::DMA buffer-to-LDS loads of
-// 1 KB. Past the wave's last page (j >= np) the buffer range is empty, so the loads touch no memory
-// but still count in vmcnt like a real page.
-template <int D, int BITS, int RING>
-__device__ __forceinline__ void issue_page(uint8_t* ring, int j, int np, const int32_t* __restrict__ bt_w, int nw,
-                                           const uint8_t* head_base, int64_t bs, const uint32_t* voff) {
+// Stage the record of block blk into LDS at dst: R::DMA buffer-to-LDS loads of 1 KB. An invalid
+// page (past the wave's last) gets an empty buffer range: the loads touch no memory but still count
+// in vmcnt like a real page.
+template <int D, int BITS>
+__device__ __forceinline__ void issue_page(uint8_t* dst, bool valid, int blk, const uint8_t* head_base, int64_t bs,
+                                           const uint32_t* voff) {
     using F = Fmt<D, BITS>;
     using R = Ring<D, BITS>;
-    const bool valid = j < np;
-    const int blk = valid ? bt_w[j * nw] : 0;
     const uint8_t* rec = head_base + (int64_t)blk * bs;
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)rec, 0, valid ? F::REC : 0, 0x00020000);
-    uint8_t* dst = ring + (j % RING) * R::SLOT;
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int i = 0; i < R::DMA; ++i)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(dst + i * WAVE * 16), 16, voff[i], 0, 0, 0);
     asm volatile("" ::: "memory");
+}
+
+// Scores of the 32 tokens of a staged page in log2 units: x[j] for token tok(q, j), head r16.
+// S^T = K . Q'^T on codes n = c + HALF as subnormal fp16 (units of 2^-24); the bias
+// sum_d kb[d] q[d] and the offset -HALF sum_d Q'[d] come from MFMAs whose A rows are all equal.
+template <int D, int BITS>
+__device__ __forceinline__ void page_scores(const uint8_t* slot, const h8 (&qh)[D / 32], const h8 (&ql)[D / 32],
+                                            float (&x)[8], int lane) {
+    using F = Fmt<D, BITS>;
+    constexpr int KSTEPS = D / 32;
+    constexpr int KBYTES = F::DC / 4;                // K code bytes per lane per 16-token tile
+    constexpr _Float16 NH = (_Float16)(-(float)F::HALF);
+    constexpr float TWO24 = 16777216.0f;
+    const int r16 = lane & 15, q = lane >> 4;
+    const h8 neg_half = h8{NH, NH, NH, NH, NH, NH, NH, NH};
+    f4 sacc[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};
+    f4 kacc = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+        h8 a[2];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            // code bytes of row 16 tt + r16 for this K-step, from the swizzled slot
+            const int row = 16 * tt + r16;
+            const int byte = q * KBYTES + 8 * (BITS == 4 ? kk >> 1 : kk);
+            const u2 wv = *reinterpret_cast<const u2*>(slot + slot_chunk<D, BITS>(row, byte / 16) + byte % 16);
+            if constexpr (BITS == 4) {
+                const uint32_t x0 = wv[0] ^ 0x88888888u, x1 = wv[1] ^ 0x88888888u;
+                a[tt] = (kk & 1) ? sub_codes4((x0 >> 4) & 0x0F0F0F0Fu, (x1 >> 4) & 0x0F0F0F0Fu)
+                                 : sub_codes4(x0 & 0x0F0F0F0Fu, x1 & 0x0F0F0F0Fu);
+            } else {
+                a[tt] = int8_sub(wv[0], wv[1]);
+            }
+        }
+        const int d0 = kdim<D, BITS>(kk, q, 0);
+        const h8 ks8 = *reinterpret_cast<const h8*>(slot + F::OFF_KS + 2 * d0);
+        const h8 kb8 = *reinterpret_cast<const h8*>(slot + F::OFF_KB + 2 * d0);
+        const h8 qp = qh[kk] * ks8;                       // fp16 multiply, as the reference TC path
+        kacc = mfma16(kb8, qh[kk], kacc);
+        kacc = mfma16(kb8, ql[kk], kacc);
+        kacc = mfma16(neg_half, qp, kacc);
+        sacc[0] = mfma16(a[0], qp, sacc[0]);
+        sacc[1] = mfma16(a[1], qp, sacc[1]);
+    }
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) x[jj] = __builtin_fmaf(sacc[jj >> 2][jj & 3], TWO24, kacc[0]);
+}
+
+template <int K>
+__device__ __forceinline__ uint8_t* pick_slot(uint8_t* s0, uint8_t* s1, uint8_t* s2, uint8_t* s3) {
+    if constexpr (K == 0) return s0;
+    else if constexpr (K == 1) return s1;
+    else if constexpr (K == 2) return s2;
+    else return s3;
 }
 
 // Static LDS of one decode workgroup: NW rings of RING slots, q for the exact-K tail (also the merge
@@ -274,13 +350,16 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     using R = Ring<D, BITS>;
     constexpr int KSTEPS = D / 32;
     constexpr int DT = D / 16;
-    constexpr int KBYTES = F::DC / 4;                // K code bytes per lane per 16-token tile
-    constexpr int KW = KBYTES / 4;
-    constexpr float HALF = (float)F::HALF;
     constexpr float TWO24 = 16777216.0f;
     static_assert(RING >= 2, "a ring needs two slots");
+    static_assert(NW == 2 || NW == 4 || NW == 8, "the tail splits 16 heads over 2 NW lane halves");
 
-    __shared__ __align__(1024) uint8_t ring_all[NW * RING * R::SLOT];
+    // one array per ring slot (wave w at offset w R::SLOT): the compiler then tells the slots apart
+    // and leaves the DMA waits to the explicit vmcnt below
+    __shared__ __align__(1024) uint8_t ring0[NW * R::SLOT];
+    __shared__ __align__(1024) uint8_t ring1[NW * R::SLOT];
+    __shared__ __align__(1024) uint8_t ring2[RING > 2 ? NW * R::SLOT : 16];
+    __shared__ __align__(1024) uint8_t ring3[RING > 3 ? NW * R::SLOT : 16];
     __shared__ __align__(16) float qs_l[16 * D];     // fp32 q sm log2e for the exact-K tail; then merge buffer
     __shared__ float sc_l[16 * PAGE];                // tail scores
     __shared__ float m_l[NW * 16], l_l[NW * 16];
@@ -301,185 +380,193 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     const uint8_t* head_base = cache + (int64_t)h * hs;
     const int64_t qbase = ((int64_t)s * H + h) * G * D + (int64_t)g0 * D;
     const bool has_tail = tail_n > 0 && z == NS - 1;
-    uint8_t* ring = ring_all + w * RING * R::SLOT;
+    uint8_t* const sl0 = ring0 + w * R::SLOT;
+    uint8_t* const sl1 = ring1 + w * R::SLOT;
+    uint8_t* const sl2 = ring2 + (RING > 2 ? w * R::SLOT : 0);
+    uint8_t* const sl3 = ring3 + (RING > 3 ? w * R::SLOT : 0);
 
     // per-lane DMA source offsets (swizzled code rows), fixed for every page
     uint32_t voff[R::DMA];
 #pragma unroll
     for (int i = 0; i < R::DMA; ++i) voff[i] = src_chunk<D, BITS>(WAVE * i + lane) * 16u;
 
-    // Page j of this wave is p0 + w + j NW; it lands in slot j % RING. Every issue is R::DMA
-    // instructions, also past the end (an empty buffer range: no memory access), so vmcnt counts
-    // stay exact: before reading page j, at most (RING - 2) later pages may still be in flight.
+    // Page j of this wave is p0 + w + j NW. The wave walks its pages in chunks of 64, whose block ids
+    // sit in one VGPR (lane i: page c0 + i) and reach the scalar unit by v_readlane; page c0 + j of
+    // a chunk lands in ring slot j % RING. Every issue is R::DMA instructions, also past the chunk's
+    // end (an empty buffer range: no memory access), so vmcnt counts stay exact: before reading
+    // page j, at most (RING - 2) later pages may still be in flight.
     const int np = p1 - p0 > w ? (p1 - p0 - w + NW - 1) / NW : 0;       // pages of this wave
-#pragma unroll
-    for (int j = 0; j < RING - 1; ++j)
-        issue_page<D, BITS, RING>(ring, j, np, bt + p0 + w, NW, head_base, bs, voff);
+    const int32_t* bt_w = bt + p0 + w;
+    int c0, nc = min(np, 64);                                            // chunk start, pages in it
+    int ids = lane < nc ? bt_w[lane * NW] : 0;
 
-    // this lane's q head (B column r16) over its contraction dims, as an fp16 hi / lo pair
+    // this lane's q head (B column r16) over its contraction dims (8 consecutive dims per K-step),
+    // loaded after the block ids and before the first DMAs, so that each wait covers only what it
+    // needs. Lanes of heads past the chunk read the chunk's last head and zero it.
     const bool gv = r16 < Gc;
+    float qv[KSTEPS][8];
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) load8(qg + qbase + (int64_t)min(r16, Gc - 1) * D + kdim<D, BITS>(kk, q, 0), qv[kk]);
+
+#define KUSH_ISSUE(SLOT, J) \
+    issue_page<D, BITS>(SLOT, (J) < nc, (J) < nc ? __builtin_amdgcn_readlane(ids, (J) & 63) : 0, head_base, bs, voff)
+#define KUSH_PROLOGUE()                                  \
+    KUSH_ISSUE(sl0, 0);                                  \
+    if constexpr (RING > 2) KUSH_ISSUE(sl1, 1);          \
+    if constexpr (RING > 3) KUSH_ISSUE(sl2, 2);
+    KUSH_PROLOGUE()
+
     h8 qh[KSTEPS], ql[KSTEPS];
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float xq = gv ? to_f32(qg[qbase + (int64_t)r16 * D + kdim<D, BITS>(kk, q, j)]) * sm_log2 : 0.0f;
+            const float xq = gv ? qv[kk][j] * sm_log2 : 0.0f;
             const _Float16 hi = (_Float16)xq;
             qh[kk][j] = hi;
             ql[kk][j] = (_Float16)(xq - (float)hi);
         }
-    if (has_tail) {
-        for (int i = threadIdx.x; i < 16 * D; i += NW * WAVE)
-            qs_l[i] = i / D < Gc ? to_f32(qg[qbase + i]) * sm_log2 : 0.0f;
+    if (has_tail && w == 0) {                         // wave 0 holds q of all 16 heads over all dims
+#pragma unroll
+        for (int kk = 0; kk < KSTEPS; ++kk)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) qs_l[r16 * D + kdim<D, BITS>(kk, q, j)] = gv ? qv[kk][j] * sm_log2 : 0.0f;
     }
-    const h8 neg_half = h8{(_Float16)-HALF, (_Float16)-HALF, (_Float16)-HALF, (_Float16)-HALF,
-                           (_Float16)-HALF, (_Float16)-HALF, (_Float16)-HALF, (_Float16)-HALF};
 
     f4 o[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     float m_run = -__builtin_inff(), l_run = 0.0f, vb_run = 0.0f;
 
-    for (int j = 0; j < np; ++j) {
-        KUSH_WAIT_VM(R::DMA * (RING - 2));                       // page j has landed in its slot
-        issue_page<D, BITS, RING>(ring, j + RING - 1, np, bt + p0 + w, NW, head_base, bs, voff);   // slot of page j - 1
-        const uint8_t* slot = ring + (j % RING) * R::SLOT;
-
-        f4 sacc[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};
-        f4 kacc = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int kk = 0; kk < KSTEPS; ++kk) {
-            h8 ks8, kb8;
-            if constexpr (BITS == 4) {
-                const int d0 = q * (D / 8) + 4 * kk;
-                const h4v a = *reinterpret_cast<const h4v*>(slot + F::OFF_KS + 2 * d0);
-                const h4v b = *reinterpret_cast<const h4v*>(slot + F::OFF_KS + 2 * (d0 + D / 2));
-                const h4v c = *reinterpret_cast<const h4v*>(slot + F::OFF_KB + 2 * d0);
-                const h4v d = *reinterpret_cast<const h4v*>(slot + F::OFF_KB + 2 * (d0 + D / 2));
-                ks8 = h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-                kb8 = h8{c[0], c[1], c[2], c[3], d[0], d[1], d[2], d[3]};
-            } else {
-                const int d0 = q * (D / 4) + 8 * kk;
-                ks8 = *reinterpret_cast<const h8*>(slot + F::OFF_KS + 2 * d0);
-                kb8 = *reinterpret_cast<const h8*>(slot + F::OFF_KB + 2 * d0);
-            }
-            const h8 qp = qh[kk] * ks8;                       // fp16 multiply, as the reference TC path
-            // bias terms: every row of A is the same vector, so every output row holds the sum for
-            // head g = r16: sum_d kb[d] q[g][d] (hi + lo) - HALF sum_d Q'[g][d] (the code offset)
-            kacc = mfma16(kb8, qh[kk], kacc);
-            kacc = mfma16(kb8, ql[kk], kacc);
-            kacc = mfma16(neg_half, qp, kacc);
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-                // K code slice of row 16 tt + r16 for this K-step, read from the swizzled slot
-                const int row = 16 * tt + r16;
-                h8 a;
-                if constexpr (BITS == 4) {
-                    // bytes q KBYTES + 4 kk .. + 3 of the row
-                    const int byte = q * KBYTES + 4 * kk;
-                    const uint32_t wv =
-                        *reinterpret_cast<const uint32_t*>(slot + slot_chunk<D, BITS>(row, byte / 16) + byte % 16);
-                    a = int4_sub(wv);
-                } else {
-                    const int byte = q * KBYTES + 8 * kk;
-                    const u2 wv = *reinterpret_cast<const u2*>(slot + slot_chunk<D, BITS>(row, byte / 16) + byte % 16);
-                    a = int8_sub(wv[0], wv[1]);
-                }
-                sacc[tt] = mfma16(a, qp, sacc[tt]);
-            }
-        }
-        float x[8];
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) x[jj] = __builtin_fmaf(sacc[jj >> 2][jj & 3], TWO24, kacc[0]);
-        consume_page<D, BITS>(slot, o, x, PAGE, m_run, l_run, vb_run, lane);
+    // The ring unrolled by its depth, so every slot is a fixed array. A step is reached only through
+    // the step before it (past the last page the loop exits), so the compiler's view of the
+    // outstanding DMAs at each read is exact and it adds no wait of its own.
+#define KUSH_PAGE_STEP(K)                                                                                          \
+    {                                                                                                              \
+        KUSH_WAIT_VM(R::DMA * (RING - 2));                                   /* page j0 + K has landed */          \
+        KUSH_ISSUE((pick_slot<((K) + RING - 1) % RING>(sl0, sl1, sl2, sl3)), j0 + (K) + RING - 1); /* slot of j0+K-1 */\
+        const uint8_t* slot = pick_slot<(K)>(sl0, sl1, sl2, sl3);                                                  \
+        float x[8];                                                                                                \
+        page_scores<D, BITS>(slot, qh, ql, x, lane);                                                               \
+        consume_page<D, BITS>(slot, o, x, PAGE, m_run, l_run, vb_run, lane);                                       \
+        if (j0 + (K) + 1 >= nc) break;                                                                             \
     }
+#define KUSH_RING_LOOP()                                     \
+    for (int j0 = 0; nc > 0; j0 += RING) {                   \
+        KUSH_PAGE_STEP(0)                                    \
+        KUSH_PAGE_STEP(1)                                    \
+        if constexpr (RING > 2) KUSH_PAGE_STEP(2)            \
+        if constexpr (RING > 3) KUSH_PAGE_STEP(3)            \
+    }
+    // the first chunk has a loop of its own: one entry state per ring loop keeps the waits exact
+    KUSH_RING_LOOP()
+    for (c0 = 64; c0 < np; c0 += 64) {
+        nc = min(np - c0, 64);                                   // next chunk: its ids, then its first pages
+        ids = lane < nc ? bt_w[(c0 + lane) * NW] : 0;
+        KUSH_PROLOGUE()
+        KUSH_RING_LOOP()
+    }
+#undef KUSH_RING_LOOP
+#undef KUSH_PAGE_STEP
+#undef KUSH_PROLOGUE
+#undef KUSH_ISSUE
     KUSH_WAIT_VM(0);                                             // drain the trailing (empty) issues
     __syncthreads();                                             // qs_l ready; rings idle
 
-    // partial last page: exact K from the tail, V rows from its record (last split only)
-    if (has_tail && w == (p1 - p0) % NW) {
-        const IN* tk = tail_k + ((int64_t)tail_idx[s] * H + h) * PAGE * D;
-        uint8_t* slot = ring;                                    // slot 0 of this wave's ring
-        issue_page<D, BITS, RING>(ring, 0, 1, bt + full, 0, head_base, bs, voff);
-        const int t = lane & 31, hf = lane >> 5;
-        float acc[16];
+    // partial last page (last split only): V rows from its record, staged by the wave that owns the
+    // page; exact fp32 K . q scores from the tail, spread over all waves (lane: token lane % 32, heads
+    // 2 w + lane / 32 + 2 NW i)
+    if (has_tail) {
+        const bool own = w == (p1 - p0) % NW;
+        if (own) issue_page<D, BITS>(sl0, true, bt[full], head_base, bs, voff);
+        constexpr int HPL = 16 / (2 * NW);           // heads per lane
+        const int t = lane & 31, hg = 2 * w + (lane >> 5);
+        const IN* tk = tail_k + (((int64_t)tail_idx[s] * H + h) * PAGE + min(t, tail_n - 1)) * D;
+        float acc[HPL];
 #pragma unroll
-        for (int g = 0; g < 16; ++g) acc[g] = 0.0f;
-        if (t < tail_n) {
-            for (int d = hf * (D / 2); d < (hf + 1) * (D / 2); d += 4) {
-                const float k0 = to_f32(tk[t * D + d]), k1 = to_f32(tk[t * D + d + 1]);
-                const float k2 = to_f32(tk[t * D + d + 2]), k3 = to_f32(tk[t * D + d + 3]);
+        for (int i = 0; i < HPL; ++i) acc[i] = 0.0f;
+#pragma unroll 4
+        for (int d = 0; d < D; d += 8) {
+            float kx[8];
+            load8(tk + d, kx);
 #pragma unroll
-                for (int g = 0; g < 16; ++g) {
-                    const float4 q4 = *reinterpret_cast<const float4*>(&qs_l[g * D + d]);
-                    acc[g] += q4.x * k0 + q4.y * k1 + q4.z * k2 + q4.w * k3;
-                }
+            for (int i = 0; i < HPL; ++i) {
+                const float4 qa = *reinterpret_cast<const float4*>(&qs_l[(hg + 2 * NW * i) * D + d]);
+                const float4 qb = *reinterpret_cast<const float4*>(&qs_l[(hg + 2 * NW * i) * D + d + 4]);
+                acc[i] += qa.x * kx[0] + qa.y * kx[1] + qa.z * kx[2] + qa.w * kx[3] +
+                          qb.x * kx[4] + qb.y * kx[5] + qb.z * kx[6] + qb.w * kx[7];
             }
         }
 #pragma unroll
-        for (int g = 0; g < 16; ++g) {
-            acc[g] += __shfl_xor(acc[g], 32, WAVE);
-            if (hf == 0) sc_l[g * PAGE + t] = t < tail_n ? acc[g] : -__builtin_inff();
-        }
-        float x[8];
+        for (int i = 0; i < HPL; ++i) sc_l[(hg + 2 * NW * i) * PAGE + t] = t < tail_n ? acc[i] : -__builtin_inff();
+        __syncthreads();
+        if (own) {
+            float x[8];
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) x[jj] = sc_l[r16 * PAGE + tok(q, jj)];
-        KUSH_WAIT_VM(0);
-        consume_page<D, BITS>(slot, o, x, tail_n, m_run, l_run, vb_run, lane);
+            for (int jj = 0; jj < 8; ++jj) x[jj] = sc_l[r16 * PAGE + tok(q, jj)];
+            KUSH_WAIT_VM(0);
+            consume_page<D, BITS>(sl0, o, x, tail_n, m_run, l_run, vb_run, lane);
+        }
     }
 
-    // merge the waves: every wave rescales to the workgroup max and adds into LDS in turn
+    // Merge the waves. Every wave rescales its O to the workgroup max and stores it in the idle rings
+    // (region of wave ww: 16 D floats, dims d as [d / 4][head][d % 4], one 16-byte store per lane and
+    // tile); after one barrier, wave w sums tiles w, w + NW, ... over the waves and writes them out.
+    constexpr int OBYTES = 16 * D * 4;
+    constexpr int PER = NW * R::SLOT / OBYTES;                 // wave regions per ring array
+    static_assert(PER >= 1 && 2 * PER >= NW, "the merge needs 16 D floats per wave in two ring arrays");
     l_run = rows_sum(l_run);
     vb_run = rows_sum(vb_run);
-    __syncthreads();
     if (q == 0) {
         m_l[w * 16 + r16] = m_run;
         l_l[w * 16 + r16] = l_run;
     }
-    __syncthreads();
+    __syncthreads();                                             // rings idle, m_l / l_l complete
     float M = -__builtin_inff();
 #pragma unroll
     for (int ww = 0; ww < NW; ++ww) M = __builtin_fmaxf(M, m_l[ww * 16 + r16]);
-    const float f = m_run == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m_run - M);
-    float* mbuf = qs_l;
-#pragma unroll 1
-    for (int ww = 0; ww < NW; ++ww) {
-        if (w == ww) {
+    {
+        const float f = m_run == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m_run - M);
+        uint8_t* reg = w < PER ? ring0 + w * OBYTES : ring1 + (w - PER) * OBYTES;
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
+        for (int dt = 0; dt < DT; ++dt) {
+            f4 v;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int idx = r16 * D + 16 * dt + 4 * q + i;
-                    const float val = __builtin_fmaf(o[dt][i], TWO24, vb_run) * f;
-                    mbuf[idx] = ww == 0 ? val : mbuf[idx] + val;
-                }
+            for (int i = 0; i < 4; ++i) v[i] = __builtin_fmaf(o[dt][i], TWO24, vb_run) * f;
+            *reinterpret_cast<f4*>(reg + (((4 * dt + q) * 16 + r16) * 4) * 4) = v;
         }
-        __syncthreads();
     }
-    for (int i = threadIdx.x; i < Gc * D; i += NW * WAVE) {
-        const int g = i / D, d = i % D;
-        float Mg = -__builtin_inff();
+    float L = 0.0f;                                              // softmax denominator of head r16
+    if (M > -__builtin_inff()) {
 #pragma unroll
-        for (int ww = 0; ww < NW; ++ww) Mg = __builtin_fmaxf(Mg, m_l[ww * 16 + g]);
-        float L = 0.0f;
-        if (Mg > -__builtin_inff()) {
+        for (int ww = 0; ww < NW; ++ww) {
+            const float mw = m_l[ww * 16 + r16];
+            if (mw > -__builtin_inff()) L += l_l[ww * 16 + r16] * __builtin_amdgcn_exp2f(mw - M);
+        }
+    }
+    __syncthreads();
+    const float inv_l = L > 0.0f ? 1.0f / L : 0.0f;
+    const int64_t pb = (((int64_t)s * H + h) * NS + z) * G + g0 + r16;   // partials row of head r16
+    for (int dt = w; dt < DT; dt += NW) {
+        f4 acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int ww = 0; ww < NW; ++ww) {
-                const float mw = m_l[ww * 16 + g];
-                if (mw > -__builtin_inff()) L += l_l[ww * 16 + g] * __builtin_amdgcn_exp2f(mw - Mg);
+        for (int ww = 0; ww < NW; ++ww) {
+            const uint8_t* reg = ww < PER ? ring0 + ww * OBYTES : ring1 + (ww - PER) * OBYTES;
+            acc += *reinterpret_cast<const f4*>(reg + (((4 * dt + q) * 16 + r16) * 4) * 4);
+        }
+        if (r16 < Gc) {
+            const int d0 = 16 * dt + 4 * q;
+            if (NS == 1) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) out[qbase + r16 * D + d0 + i] = from_f32<IN>(acc[i] * inv_l);
+            } else {
+                *reinterpret_cast<f4*>(part_o + pb * D + d0) = acc;
             }
         }
-        const float val = mbuf[g * D + d];
-        if (NS == 1) {
-            out[qbase + i] = from_f32<IN>(L > 0.0f ? val / L : 0.0f);
-        } else {
-            const int64_t pb = (((int64_t)s * H + h) * NS + z) * G + g0 + g;
-            part_o[pb * D + d] = val;
-            if (d == 0) {
-                part_ml[2 * pb] = Mg;
-                part_ml[2 * pb + 1] = L;
-            }
-        }
+    }
+    if (NS > 1 && w == 0 && q == 0 && r16 < Gc) {
+        part_ml[2 * pb] = M;
+        part_ml[2 * pb + 1] = L;
     }
     if (NS == 1 || sync == nullptr) return;
 
@@ -573,6 +660,7 @@ extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const v
         return kush_fail(-2, "kush_decode: n_splits %d needs the partial buffers", n_splits);
     if (((uintptr_t)cache | (uint64_t)block_stride | (uint64_t)head_stride) & 15)
         return kush_fail(-2, "kush_decode: cache records must be 16-byte aligned");
+    if (((uintptr_t)q | (uintptr_t)tail_k) & 15) return kush_fail(-2, "kush_decode: q and tail_k must be 16-byte aligned");
     if (waves == 0) waves = 8;
     if (waves != 2 && waves != 4 && waves != 8) return kush_fail(-2, "kush_decode: waves must be 0, 2, 4 or 8");
     const int n_gc = (group + 15) / 16;
