@@ -78,8 +78,9 @@ int kush_write(int head_dim, int bits, int dtype, const void* k, const void* v, 
  * (_ops.py:204-208). With split_sync (int32 [n_seqs*hkv*ceil(group/16)], zero before the first
  * call) the last workgroup of each (sequence, kv head) merges the splits into out itself and
  * resets its counter, so the buffer stays zero between calls; calls that share split_sync must
- * not overlap. Without it (NULL), run kush_combine afterwards. waves: 4, 8 or 16 waves per
- * workgroup (0 = 4).
+ * not overlap. Without it (NULL), run kush_combine afterwards. waves: 2, 4 or 8 waves per
+ * workgroup (0 = 8; a configuration whose page ring does not fit in LDS falls back to fewer).
+ * q and tail_k must be 16-byte aligned.
  * Replaces kush_decode_tc / kush_decode (gpu.mojo:566-807, :840-1040) and, with split_sync, the
  * kush_combine launch (gpu.mojo:469-491) as issued by Ops.decode (_ops.py:191-213). */
 int kush_decode(int head_dim, int bits, int group, int dtype, const void* q, void* out, const void* cache,
