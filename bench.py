@@ -55,6 +55,11 @@ def parse_args(argv=None):
     ap.add_argument("--sequential", action="store_true", help="pages in order instead of a random permutation")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="instead of the decode, run --steps device-to-device copies of MIB MiB: the plain copy "
+                         "kernel of known size that scales rocprofv3's FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--traffic", default=str(ROOT / "profiles" / "decode_c2_traffic.md"),
+                    help="rocprofv3 counter summary whose 'traffic_bytes_per_launch' fills roofline.traffic")
     return ap.parse_args(argv)
 
 
@@ -209,6 +214,38 @@ def cpu_baseline(w, budget_s: float):
             "us_per_step_extrapolated": round(med / frac * 1e6, 1)}
 
 
+def measured_traffic(path: str, workload: str):
+    """HBM bytes per decode launch from a committed counter summary (FETCH_SIZE + WRITE_SIZE of the
+    same workload, each scaled by the copy-kernel calibration), or None."""
+    try:
+        text = Path(path).read_text()
+    except OSError:
+        return None
+    import re
+    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", text, re.M)
+    w = re.search(r"^workload:\s*(.+)$", text, re.M)
+    if not m or not w or w.group(1).strip() != workload:
+        return None
+    return int(m.group(1))
+
+
+def copy_calibration(a) -> None:
+    """Plain copies of a known size, for the byte counters' scale factor."""
+    n = a.calibrate_copy << 20
+    x = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / a.steps
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "copies": a.steps + 3,
+                      "us_per_copy": round(dt * 1e6, 2), "GB/s": round(2 * n / dt / 1e9, 1)}), flush=True)
+
+
 def main(argv=None):
     a = parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -218,6 +255,9 @@ def main(argv=None):
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU")
     dev = "cuda:0"
+    if a.calibrate_copy:
+        copy_calibration(a)
+        return
     w = make_workload(a, dev)
     ns = a.splits or w["ops"].splits(w["B"], w["Hkv"], w["N"] // PAGE)
     alg = algorithmic_bytes(w)
@@ -231,6 +271,8 @@ def main(argv=None):
 
     wv = a.waves or w["ops"].waves(w["B"], w["Hkv"], ns)
     ms = time_steps(w, ns, wv, a.steps, a.warmup)
+    workload = (f"C2 Qwen2.5-7B decode layer: {a.hq} q / {a.hkv} kv heads, D {a.dim}, int{a.bits}, page 32, "
+                f"batch {a.batch} x {a.ctx} tokens")
     ms_dec = ms                                   # one kernel per step: the decode kernel is the step
     gbs = alg / ms / 1e6
     gbs_dec = alg / ms_dec / 1e6
@@ -251,11 +293,11 @@ def main(argv=None):
         "dtype": "int4 records, f16 MFMA, f32 accumulate, bf16 q/out",
         "data": "synthetic (seeded; K bias sigma 6 on 10% of channels; random page placement; "
                 f"{a.pools} rotated pools)",
-        "config": {"workload": f"C2 Qwen2.5-7B decode layer: {a.hq} q / {a.hkv} kv heads, D {a.dim}, int{a.bits}, "
-                               f"page 32, batch {a.batch} x {a.ctx} tokens", "global_batch": a.batch,
+        "config": {"workload": workload, "global_batch": a.batch,
                    "seq_len": a.ctx, "parallelism": "single GPU", "split_k": ns, "waves": wv, "pools": a.pools},
         "roofline": {"bound": "hbm", "achieved": round(gbs_dec, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs_dec / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(gbs_dec / PEAK_HBM_GBS, 4),
+                     "traffic": measured_traffic(a.traffic, f"{workload}, splits {ns}, waves {wv}"),
                      "kernel": f"decode_kernel<{a.dim},{a.bits},bf16,{wv}>", "kernel_us": round(ms_dec * 1e3, 2),
                      "algorithmic_bytes": alg},
         "cpu_baseline": None,

@@ -186,7 +186,8 @@ __device__ __forceinline__ v2i gather_vt(const uint8_t* slot, int ct, int lane) 
 
 // Softmax update of one page (scores x in log2 units, tokens tok(q, j); tokens >= valid masked) and
 // its PV accumulation from the staged V codes. o accumulates in units of 2^-24 (subnormal codes);
-// vb_run carries the V biases and the code offset: v = vs * (n - HALF) + vb = vs * n + (vb - HALF vs).
+// vb_run carries the V biases and the code offset: with P' = fp16(e vs), the page adds
+// sum P' n (MFMA) + sum (e vb - HALF P') (here), i.e. sum e (vs' c + vb) with vs' = P' / e.
 template <int D, int BITS>
 __device__ __forceinline__ void consume_page(const uint8_t* slot, f4 (&o)[D / 16], const float (&x)[8], int valid,
                                              float& m_run, float& l_run, float& vb_run, int lane) {
@@ -214,10 +215,10 @@ __device__ __forceinline__ void consume_page(const uint8_t* slot, f4 (&o)[D / 16
         const float vsj = (float)(j < 4 ? vs0[j] : vs1[j - 4]);
         const float vbj = (float)(j < 4 ? vb0[j] : vb1[j - 4]);
         const float e = ok ? __builtin_amdgcn_exp2f(x[j] - m_new) : 0.0f;
-        const float ev = e * vsj;
+        pw[j] = (_Float16)(e * vsj);
         lsum += e;
-        vbsum += ok ? e * vbj - HALF * ev : 0.0f;
-        pw[j] = (_Float16)(ok ? ev : 0.0f);
+        // the code offset uses the rounded weight the MFMA sees: sum P' (n - HALF) is then exact
+        vbsum = __builtin_fmaf(-HALF, (float)pw[j], __builtin_fmaf(e, vbj, vbsum));
     }
     l_run = l_run * corr + lsum;
     vb_run = vb_run * corr + vbsum;
@@ -260,8 +261,9 @@ __device__ __forceinline__ void issue_page(uint8_t* dst, bool valid, int blk, co
 }
 
 // Scores of the 32 tokens of a staged page in log2 units: x[j] for token tok(q, j), head r16.
-// S^T = K . Q'^T on codes n = c + HALF as subnormal fp16 (units of 2^-24); the bias
-// sum_d kb[d] q[d] and the offset -HALF sum_d Q'[d] come from MFMAs whose A rows are all equal.
+// S^T = K . Q'^T on codes n = c + HALF as subnormal fp16 (units of 2^-24), Q' as an fp16 hi / lo
+// pair; the bias sum_d kb[d] q[d] and the offset -HALF sum_d Q'[d] come from MFMAs whose A rows are
+// all equal.
 template <int D, int BITS>
 __device__ __forceinline__ void page_scores(const uint8_t* slot, const h8 (&qh)[D / 32], const h8 (&ql)[D / 32],
                                             float (&x)[8], int lane) {
@@ -294,12 +296,19 @@ __device__ __forceinline__ void page_scores(const uint8_t* slot, const h8 (&qh)[
         const int d0 = kdim<D, BITS>(kk, q, 0);
         const h8 ks8 = *reinterpret_cast<const h8*>(slot + F::OFF_KS + 2 * d0);
         const h8 kb8 = *reinterpret_cast<const h8*>(slot + F::OFF_KB + 2 * d0);
-        const h8 qp = qh[kk] * ks8;                       // fp16 multiply, as the reference TC path
+        // Q' = q ks as an fp16 pair: qp = fp16(qh ks), qr = the exact residual of that product plus
+        // ql ks, rounded once (relative error ~2^-22 overall, where qp alone carries 2^-12)
+        const h8 qp = qh[kk] * ks8;
+        h8 qr = __builtin_elementwise_fma(qh[kk], ks8, -qp);
+        qr = __builtin_elementwise_fma(ql[kk], ks8, qr);
         kacc = mfma16(kb8, qh[kk], kacc);
         kacc = mfma16(kb8, ql[kk], kacc);
         kacc = mfma16(neg_half, qp, kacc);
+        kacc = mfma16(neg_half, qr, kacc);
         sacc[0] = mfma16(a[0], qp, sacc[0]);
         sacc[1] = mfma16(a[1], qp, sacc[1]);
+        sacc[0] = mfma16(a[0], qr, sacc[0]);
+        sacc[1] = mfma16(a[1], qr, sacc[1]);
     }
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) x[jj] = __builtin_fmaf(sacc[jj >> 2][jj & 3], TWO24, kacc[0]);

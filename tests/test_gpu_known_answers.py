@@ -51,7 +51,10 @@ def test_gpu_exact_records_and_decode(golden, D, bits, appends):
     q = torch.from_numpy(golden[key + "q"])[None].cuda()
     for qq, ref in ((q, golden[key + "out"]), (torch.zeros_like(q), golden[key + "out_q0"])):
         out = c.attend(0, qq)[0].double().cpu().numpy()
-        assert np.abs(out - ref).max() <= out_tol(torch.from_numpy(ref), torch.float32)
+        # max-abs 2e-3 at unit output scale; these constructed V reach |485|, where the bound is
+        # relative: 2e-3 * max(1, max |ref|) (fp16 weights carry 2^-11 relative rounding)
+        scale = max(1.0, float(np.abs(ref).max()))
+        assert np.abs(out - ref).max() <= out_tol(torch.from_numpy(ref), torch.float32, base=2e-3 * scale)
 
 
 @pytest.mark.parametrize("case,bits", [("ties", 4), ("const", 4), ("const", 8), ("clamp", 4)])
