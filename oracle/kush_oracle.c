@@ -20,19 +20,21 @@
  * -ffp-contract=off), round-half-to-even for codes (the reference's own test restatement,
  * tests/test_cpu.py:16-24, uses torch.round), RNE fp32->fp16 for scales and biases.
  *
- * Parity status (what pins each function; the tests in tests/test_oracle*.py hold the checks):
- *   quantization (qparams/qcode/pack4, record layout): pinned by the reference test restatement
- *     ref_quantize/split_record (test_cpu.py:16-37), closed-form known answers
- *     (tests/golden/known_answers.npz) and nearest-level brute force on small inputs.
- *     Exact round ties: pinned only against torch.round (half-to-even), the reference test's
- *     oracle; Mojo's own tie rule is not visible in the reference ("parity unpinned" for ties).
- *   append / write: pinned by the ragged simulation semantics (test_ragged.py:112-129) and by
- *     bulk-vs-append equality (test_cpu.py:40-76).
- *   decode: pinned against softmax attention over the dequantized cache (test_cpu.py:79-96).
- *   fwht: pinned bit-exact against the canonical torch order (_ops.py:383-395) and against the
- *     dense Hadamard product.
- *   unpack: pinned against an fp64 torch reference on the reference's fixture shape
- *     (tests/_unpack_case.py, _ops.py:398-436).
+ * Parity status (what pins each function):
+ *   quantization (qparams/qcode/pack4, record layout): by-construction known answers
+ *     (tests/golden/known_answers.npz via tests/test_known_answers.py: exact dyadic scales and
+ *     codes, constant groups, the clamp at a subnormal fp16 scale), the reference test's own
+ *     restatement ref_quantize/split_record (test_cpu.py:16-37; tests/test_oracle.py) and a
+ *     brute-force nearest-level search with clamp.
+ *     Exact round ties: pinned only to torch.round (half-to-even), the reference test's oracle;
+ *     Mojo's own tie rule is not visible in the reference: parity unpinned for ties.
+ *   append / write: the ragged vLLM simulation (test_ragged.py semantics), bulk-vs-append
+ *     equality (test_cpu.py:40-76) and padding rows (tests/test_known_answers.py).
+ *   decode: softmax attention over the dequantized cache (test_cpu.py:79-96) and float64 attention
+ *     over exactly dequantizable records; exp only through those tolerances.
+ *   fwht: bit-exact against the canonical torch order (_ops.py:383-395), close to the dense
+ *     Hadamard product (tests/test_host.py).
+ *   unpack: parity unpinned (no check yet; not on the decode/write hot path).
  */
 #include <math.h>
 #include <stdint.h>
