@@ -130,8 +130,13 @@ __device__ __forceinline__ uint32_t src_chunk(int L) {
     return (uint32_t)(r * R::CPR + (j ^ swz<D, BITS>(r)));
 }
 
-// s_waitcnt with only vmcnt(N) (gfx9 encoding: vmcnt [3:0] + [15:14], expcnt [6:4], lgkmcnt [11:8])
-#define KUSH_WAIT_VM(N) __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | (7 << 4) | (15 << 8))
+// s_waitcnt with only vmcnt(N) (gfx9 encoding: vmcnt [3:0] + [15:14], expcnt [6:4], lgkmcnt [11:8]),
+// then a compiler barrier: no LDS read of the landed data is moved above the wait
+#define KUSH_WAIT_VM(N)                                                                          \
+    do {                                                                                         \
+        __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | (7 << 4) | (15 << 8));      \
+        asm volatile("" ::: "memory");                                                           \
+    } while (0)
 
 // Subnormal fp16 codes: the bit pattern n (0..255) is the fp16 value n * 2^-24, exact, so unsigned
 // code bytes become MFMA operands with one byte shuffle and no arithmetic; the products are exact in
@@ -184,41 +189,47 @@ __device__ __forceinline__ v2i gather_vt(const uint8_t* slot, int ct, int lane) 
     return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(src));
 }
 
-// Softmax update of one page (scores x in log2 units, tokens tok(q, j); tokens >= valid masked) and
-// its PV accumulation from the staged V codes. o accumulates in units of 2^-24 (subnormal codes);
-// vb_run carries the V biases and the code offset: with P' = fp16(e vs), the page adds
-// sum P' n (MFMA) + sum (e vb - HALF P') (here), i.e. sum e (vs' c + vb) with vs' = P' / e.
-template <int D, int BITS>
-__device__ __forceinline__ void consume_page(const uint8_t* slot, f4 (&o)[D / 16], const float (&x)[8], int valid,
-                                             float& m_run, float& l_run, float& vb_run, int lane) {
+// Softmax update over NP staged pages at once (scores x[p] in log2 units for tokens tok(q, j);
+// masked tokens carry -inf) and their PV accumulation from the staged V codes. o accumulates in
+// units of 2^-24 (subnormal codes); vb_run carries the V biases and the code offset: with
+// P' = fp16(e vs), a page adds sum P' n (MFMA) + sum (e vb - HALF P') (here), i.e.
+// sum e (vs' c + vb) with vs' = P' / e.
+template <int D, int BITS, int NP>
+__device__ __forceinline__ void consume_pages(const uint8_t* const (&slot)[NP], f4 (&o)[D / 16],
+                                              const float (&x)[NP][8], float& m_run, float& l_run, float& vb_run,
+                                              int lane) {
     using F = Fmt<D, BITS>;
     constexpr float HALF = (float)F::HALF;
     const int q = lane >> 4;
-    float pm = x[0];
+    float pm = x[0][0];
 #pragma unroll
-    for (int j = 1; j < 8; ++j) pm = __builtin_fmaxf(pm, x[j]);
-    // the reference point of the exponentials moves only when the page max exceeds it by more than
-    // 2^3: weights stay <= 8 (P' = e vs stays far from fp16 overflow) and most pages skip the O rescale
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pm = __builtin_fmaxf(pm, x[p][j]);
+    // the reference point of the exponentials moves only when the max exceeds it by more than 2^3:
+    // weights stay <= 8 (P' = e vs stays far from fp16 overflow) and most steps skip the O rescale
     pm = rows_max(pm);
     const float m_new = pm > m_run + 3.0f ? pm : m_run;
-    const float corr = __builtin_amdgcn_exp2f(m_run - m_new);   // first page: exp2(-inf) = 0
+    const float corr = __builtin_amdgcn_exp2f(m_run - m_new);   // first step: exp2(-inf) = 0
 
-    const h4v vs0 = *reinterpret_cast<const h4v*>(slot + F::OFF_VS + 8 * q);
-    const h4v vs1 = *reinterpret_cast<const h4v*>(slot + F::OFF_VS + 32 + 8 * q);
-    const h4v vb0 = *reinterpret_cast<const h4v*>(slot + F::OFF_VB + 8 * q);
-    const h4v vb1 = *reinterpret_cast<const h4v*>(slot + F::OFF_VB + 32 + 8 * q);
     float lsum = 0.0f, vbsum = 0.0f;
-    h8 pw;
+    h8 pw[NP];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const bool ok = tok(q, j) < valid;
-        const float vsj = (float)(j < 4 ? vs0[j] : vs1[j - 4]);
-        const float vbj = (float)(j < 4 ? vb0[j] : vb1[j - 4]);
-        const float e = ok ? __builtin_amdgcn_exp2f(x[j] - m_new) : 0.0f;
-        pw[j] = (_Float16)(e * vsj);
-        lsum += e;
-        // the code offset uses the rounded weight the MFMA sees: sum P' (n - HALF) is then exact
-        vbsum = __builtin_fmaf(-HALF, (float)pw[j], __builtin_fmaf(e, vbj, vbsum));
+    for (int p = 0; p < NP; ++p) {
+        const h4v vs0 = *reinterpret_cast<const h4v*>(slot[p] + F::OFF_VS + 8 * q);
+        const h4v vs1 = *reinterpret_cast<const h4v*>(slot[p] + F::OFF_VS + 32 + 8 * q);
+        const h4v vb0 = *reinterpret_cast<const h4v*>(slot[p] + F::OFF_VB + 8 * q);
+        const h4v vb1 = *reinterpret_cast<const h4v*>(slot[p] + F::OFF_VB + 32 + 8 * q);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float vsj = (float)(j < 4 ? vs0[j] : vs1[j - 4]);
+            const float vbj = (float)(j < 4 ? vb0[j] : vb1[j - 4]);
+            const float e = __builtin_amdgcn_exp2f(x[p][j] - m_new);
+            pw[p][j] = (_Float16)(e * vsj);
+            lsum += e;
+            // the code offset uses the rounded weight the MFMA sees: sum P' (n - HALF) is then exact
+            vbsum = __builtin_fmaf(-HALF, (float)pw[p][j], __builtin_fmaf(e, vbj, vbsum));
+        }
     }
     l_run = l_run * corr + lsum;
     vb_run = vb_run * corr + vbsum;
@@ -230,34 +241,45 @@ __device__ __forceinline__ void consume_page(const uint8_t* slot, f4 (&o)[D / 16
 
     constexpr int NCOL = BITS == 4 ? D / 32 : D / 16;
 #pragma unroll
-    for (int ct = 0; ct < NCOL; ++ct) {
-        const v2i w = gather_vt<D, BITS>(slot, ct, lane);
-        if constexpr (BITS == 4) {
-            h8 lo, hi;
-            int4_sub2((uint32_t)w[0], (uint32_t)w[1], lo, hi);
-            o[ct] = mfma16(lo, pw, o[ct]);
-            o[ct + D / 32] = mfma16(hi, pw, o[ct + D / 32]);
-        } else {
-            o[ct] = mfma16(int8_sub((uint32_t)w[0], (uint32_t)w[1]), pw, o[ct]);
+    for (int ct = 0; ct < NCOL; ++ct)
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const v2i w = gather_vt<D, BITS>(slot[p], ct, lane);
+            if constexpr (BITS == 4) {
+                h8 lo, hi;
+                int4_sub2((uint32_t)w[0], (uint32_t)w[1], lo, hi);
+                o[ct] = mfma16(lo, pw[p], o[ct]);
+                o[ct + D / 32] = mfma16(hi, pw[p], o[ct + D / 32]);
+            } else {
+                o[ct] = mfma16(int8_sub((uint32_t)w[0], (uint32_t)w[1]), pw[p], o[ct]);
+            }
         }
-    }
 }
 
-// Stage the record of block blk into LDS at dst: R::DMA buffer-to-LDS loads of 1 KB. An invalid
-// page (past the wave's last) gets an empty buffer range: the loads touch no memory but still count
-// in vmcnt like a real page.
+// Stage the record of block blk into LDS at dst: R::DMA buffer-to-LDS loads of 1 KB (lanes past the
+// record's end read zeros). An invalid page (past the wave's last) gets an empty buffer range: the
+// loads then fill the slot with zeros and touch no memory, and still count in vmcnt like a real page.
+// The loads are written in asm so that the compiler does not track them: the page loop waits for
+// them with explicit vmcnt counts alone. Vector loads complete in order, so any vector memory op the
+// compiler adds (issued later) only makes those waits stricter.
 template <int D, int BITS>
 __device__ __forceinline__ void issue_page(uint8_t* dst, bool valid, int blk, const uint8_t* head_base, int64_t bs,
                                            const uint32_t* voff) {
     using F = Fmt<D, BITS>;
     using R = Ring<D, BITS>;
-    const uint8_t* rec = head_base + (int64_t)blk * bs;
-    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)rec, 0, valid ? F::REC : 0, 0x00020000);
-    asm volatile("" ::: "memory");
+    const uint64_t rec = (uint64_t)(uintptr_t)(head_base + (int64_t)blk * bs);
+    // raw buffer descriptor: base, stride 0, num_records (0: every lane out of range), dword format
+    const u4 rsrc = u4{(uint32_t)rec, (uint32_t)(rec >> 32) & 0xFFFFu, valid ? (uint32_t)F::REC : 0u, 0x00020000u};
+    const uint32_t lds = (uint32_t)(uintptr_t)(lds_void*)dst;
+    // m0 is reserved by the compiler; nothing else in the decode kernels uses it (checked on their
+    // assembly by tests/test_isa.py), so setting it here is safe
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 #pragma unroll
     for (int i = 0; i < R::DMA; ++i)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(dst + i * WAVE * 16), 16, voff[i], 0, 0, 0);
-    asm volatile("" ::: "memory");
+        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                     :: "s"(lds + i * WAVE * 16), "v"(voff[i]), "s"(rsrc) : "memory", "m0");
+#pragma clang diagnostic pop
 }
 
 // Scores of the 32 tokens of a staged page in log2 units: x[j] for token tok(q, j), head r16.
@@ -314,42 +336,32 @@ __device__ __forceinline__ void page_scores(const uint8_t* slot, const h8 (&qh)[
     for (int jj = 0; jj < 8; ++jj) x[jj] = __builtin_fmaf(sacc[jj >> 2][jj & 3], TWO24, kacc[0]);
 }
 
-template <int K>
-__device__ __forceinline__ uint8_t* pick_slot(uint8_t* s0, uint8_t* s1, uint8_t* s2, uint8_t* s3) {
-    if constexpr (K == 0) return s0;
-    else if constexpr (K == 1) return s1;
-    else if constexpr (K == 2) return s2;
-    else return s3;
-}
-
-// Static LDS of one decode workgroup: NW rings of RING slots, q for the exact-K tail (also the merge
-// buffer), tail scores, per-wave softmax state.
-template <int D, int BITS, int NW, int RING>
+// Static LDS of one decode workgroup: two arrays, each holding one page pair per wave (wave w at
+// 2 w SLOT), nothing else. After the page loop the idle arrays hold everything else: the cross-wave
+// merge in the first; the exact-K tail's q and scores, the waves' softmax state and the split-K flag
+// in the second.
+template <int D, int BITS, int NW>
 constexpr int decode_lds_bytes() {
-    return NW * RING * Ring<D, BITS>::SLOT + 16 * D * 4 + 16 * PAGE * 4 + 2 * NW * 16 * 4 + 16;
-}
-
-// Ring depth for NW waves: the deepest ring (4 at most) that keeps 8 waves per CU within its 160 KB
-// of LDS (NW = 8: one workgroup per CU; NW = 4: two; NW = 2: four). Records too large for that get
-// the whole CU at NW = 2 (occupancy then bounded by LDS); 0 if no ring of 2 fits at all.
-template <int D, int BITS, int NW>
-constexpr int ring_fit(int budget) {
-    for (int r = 4; r >= 2; --r)
-        if (decode_lds_bytes<D, BITS, NW, 4>() - (4 - r) * NW * Ring<D, BITS>::SLOT <= budget) return r;
-    return 0;
+    return 4 * NW * Ring<D, BITS>::SLOT;
 }
 
 template <int D, int BITS, int NW>
-constexpr int ring_for() {
-    constexpr int shared = ring_fit<D, BITS, NW>(150 * 1024 * NW / 8);
-    return shared >= 2 || NW != 2 ? shared : ring_fit<D, BITS, NW>(150 * 1024);
+constexpr bool decode_fits() {
+    return decode_lds_bytes<D, BITS, NW>() <= 160 * 1024;
 }
+
+// byte offsets in the second array of the after-loop scratch: q [16][D] fp32, tail scores [16][PAGE],
+// m and l per wave and head [NW][16] each, the split-K flag
+template <int D>
+struct AfterLoop {
+    static constexpr int Q_OFF = 0, SC_OFF = 16 * D * 4, ML_OFF = SC_OFF + 16 * PAGE * 4;
+};
 
 // grid (S, Hkv, n_splits * ceil(G / 16)), block NW * 64.
 // NS > 1: each workgroup writes its split's partials; with `sync` (one zeroed int32 per
 // (sequence, kv head, head chunk)), the last workgroup of a (sequence, kv head, head chunk) to
 // finish merges all splits into `out` and resets its counter, so no second launch is needed.
-template <int D, int BITS, typename IN, int NW, int RING>
+template <int D, int BITS, typename IN, int NW>
 __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     const IN* __restrict__ qg, IN* __restrict__ out, const uint8_t* __restrict__ cache, int64_t bs, int64_t hs,
     const IN* __restrict__ tail_k, const int32_t* __restrict__ tail_idx, const int32_t* __restrict__ block_table,
@@ -360,19 +372,19 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     constexpr int KSTEPS = D / 32;
     constexpr int DT = D / 16;
     constexpr float TWO24 = 16777216.0f;
-    static_assert(RING >= 2, "a ring needs two slots");
     static_assert(NW == 2 || NW == 4 || NW == 8, "the tail splits 16 heads over 2 NW lane halves");
+    using AL = AfterLoop<D>;
+    static_assert(2 * NW * R::SLOT >= AL::ML_OFF + 2 * NW * 16 * 4 + 16, "the after-loop scratch must fit");
+    static_assert(2 * R::DMA <= 63, "vmcnt holds at most 63 loads");
 
-    // one array per ring slot (wave w at offset w R::SLOT): the compiler then tells the slots apart
-    // and leaves the DMA waits to the explicit vmcnt below
-    __shared__ __align__(1024) uint8_t ring0[NW * R::SLOT];
-    __shared__ __align__(1024) uint8_t ring1[NW * R::SLOT];
-    __shared__ __align__(1024) uint8_t ring2[RING > 2 ? NW * R::SLOT : 16];
-    __shared__ __align__(1024) uint8_t ring3[RING > 3 ? NW * R::SLOT : 16];
-    __shared__ __align__(16) float qs_l[16 * D];     // fp32 q sm log2e for the exact-K tail; then merge buffer
-    __shared__ float sc_l[16 * PAGE];                // tail scores
-    __shared__ float m_l[NW * 16], l_l[NW * 16];
-    __shared__ int last_flag;
+    // one array per page pair (wave w at 2 w R::SLOT): the compiler tells the pairs apart and leaves
+    // the DMA waits to the explicit vmcnt below (it need not tell the two pages of a pair apart: a
+    // pair is only read once both have landed)
+    __shared__ __align__(16) uint8_t ringA[2 * NW * R::SLOT];
+    __shared__ __align__(16) uint8_t ringB[2 * NW * R::SLOT];
+    float* const m_l = reinterpret_cast<float*>(ringB + AL::ML_OFF);      // after the loop only
+    float* const l_l = m_l + NW * 16;
+    int* const last_flag = reinterpret_cast<int*>(l_l + NW * 16);
 
     const int lane = threadIdx.x & (WAVE - 1);
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);   // wave-uniform: scalar page loop
@@ -389,10 +401,10 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     const uint8_t* head_base = cache + (int64_t)h * hs;
     const int64_t qbase = ((int64_t)s * H + h) * G * D + (int64_t)g0 * D;
     const bool has_tail = tail_n > 0 && z == NS - 1;
-    uint8_t* const sl0 = ring0 + w * R::SLOT;
-    uint8_t* const sl1 = ring1 + w * R::SLOT;
-    uint8_t* const sl2 = ring2 + (RING > 2 ? w * R::SLOT : 0);
-    uint8_t* const sl3 = ring3 + (RING > 3 ? w * R::SLOT : 0);
+    uint8_t* const sl0 = ringA + 2 * w * R::SLOT;
+    uint8_t* const sl1 = sl0 + R::SLOT;
+    uint8_t* const sl2 = ringB + 2 * w * R::SLOT;
+    uint8_t* const sl3 = sl2 + R::SLOT;
 
     // per-lane DMA source offsets (swizzled code rows), fixed for every page
     uint32_t voff[R::DMA];
@@ -400,14 +412,14 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     for (int i = 0; i < R::DMA; ++i) voff[i] = src_chunk<D, BITS>(WAVE * i + lane) * 16u;
 
     // Page j of this wave is p0 + w + j NW. The wave walks its pages in chunks of 64, whose block ids
-    // sit in one VGPR (lane i: page c0 + i) and reach the scalar unit by v_readlane; page c0 + j of
-    // a chunk lands in ring slot j % RING. Every issue is R::DMA instructions, also past the chunk's
-    // end (an empty buffer range: no memory access), so vmcnt counts stay exact: before reading
-    // page j, at most (RING - 2) later pages may still be in flight.
+    // sit in one VGPR (lane i: page c0 + i) and reach the scalar unit by v_readlane, and within a
+    // chunk in pairs: pair (j, j + 1) in slots (0, 1) or (2, 3) while the next pair is in flight in
+    // the other two. Every issue is R::DMA instructions, also past the chunk's end (an empty buffer
+    // range: no memory access), so vmcnt counts stay exact.
     const int np = p1 - p0 > w ? (p1 - p0 - w + NW - 1) / NW : 0;       // pages of this wave
     const int32_t* bt_w = bt + p0 + w;
     int c0, nc = min(np, 64);                                            // chunk start, pages in it
-    int ids = lane < nc ? bt_w[lane * NW] : 0;
+    int ids = lane < nc ? bt_w[lane * NW] : 0;     // block ids of the wave's first 64 pages
 
     // this lane's q head (B column r16) over its contraction dims (8 consecutive dims per K-step),
     // loaded after the block ids and before the first DMAs, so that each wait covers only what it
@@ -419,10 +431,11 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
 
 #define KUSH_ISSUE(SLOT, J) \
     issue_page<D, BITS>(SLOT, (J) < nc, (J) < nc ? __builtin_amdgcn_readlane(ids, (J) & 63) : 0, head_base, bs, voff)
-#define KUSH_PROLOGUE()                                  \
-    KUSH_ISSUE(sl0, 0);                                  \
-    if constexpr (RING > 2) KUSH_ISSUE(sl1, 1);          \
-    if constexpr (RING > 3) KUSH_ISSUE(sl2, 2);
+#define KUSH_PROLOGUE()   \
+    KUSH_ISSUE(sl0, 0);   \
+    KUSH_ISSUE(sl1, 1);   \
+    KUSH_ISSUE(sl2, 2);   \
+    KUSH_ISSUE(sl3, 3);
     KUSH_PROLOGUE()
 
     h8 qh[KSTEPS], ql[KSTEPS];
@@ -435,37 +448,35 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
             qh[kk][j] = hi;
             ql[kk][j] = (_Float16)(xq - (float)hi);
         }
-    if (has_tail && w == 0) {                         // wave 0 holds q of all 16 heads over all dims
-#pragma unroll
-        for (int kk = 0; kk < KSTEPS; ++kk)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) qs_l[r16 * D + kdim<D, BITS>(kk, q, j)] = gv ? qv[kk][j] * sm_log2 : 0.0f;
-    }
 
     f4 o[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     float m_run = -__builtin_inff(), l_run = 0.0f, vb_run = 0.0f;
 
-    // The ring unrolled by its depth, so every slot is a fixed array. A step is reached only through
-    // the step before it (past the last page the loop exits), so the compiler's view of the
-    // outstanding DMAs at each read is exact and it adds no wait of its own.
-#define KUSH_PAGE_STEP(K)                                                                                          \
-    {                                                                                                              \
-        KUSH_WAIT_VM(R::DMA * (RING - 2));                                   /* page j0 + K has landed */          \
-        KUSH_ISSUE((pick_slot<((K) + RING - 1) % RING>(sl0, sl1, sl2, sl3)), j0 + (K) + RING - 1); /* slot of j0+K-1 */\
-        const uint8_t* slot = pick_slot<(K)>(sl0, sl1, sl2, sl3);                                                  \
-        float x[8];                                                                                                \
-        page_scores<D, BITS>(slot, qh, ql, x, lane);                                                               \
-        consume_page<D, BITS>(slot, o, x, PAGE, m_run, l_run, vb_run, lane);                                       \
-        if (j0 + (K) + 1 >= nc) break;                                                                             \
+    // One pair step: its two pages have landed once at most the next pair's loads are outstanding;
+    // scores of both pages, one softmax update, PV of both; then, every read of the two slots
+    // complete (lgkmcnt 0), they take pages J + 4, J + 5. An odd last page pairs with a masked one.
+#define KUSH_PAIR(SA, SB, J)                                                                  \
+    {                                                                                         \
+        KUSH_WAIT_VM(2 * R::DMA);                                                             \
+        float x[2][8];                                                                        \
+        page_scores<D, BITS>(SA, qh, ql, x[0], lane);                                         \
+        page_scores<D, BITS>(SB, qh, ql, x[1], lane);                                         \
+        if ((J) + 1 >= nc) {                                                                  \
+            _Pragma("unroll") for (int jj = 0; jj < 8; ++jj) x[1][jj] = -__builtin_inff();    \
+        }                                                                                     \
+        const uint8_t* const sp[2] = {SA, SB};                                                \
+        consume_pages<D, BITS, 2>(sp, o, x, m_run, l_run, vb_run, lane);                      \
+        if ((J) + 2 >= nc) break;                                                             \
+        __builtin_amdgcn_s_waitcnt(0xC07F);                    /* lgkmcnt(0): slot reads done */ \
+        KUSH_ISSUE(SA, (J) + 4);                                                              \
+        KUSH_ISSUE(SB, (J) + 5);                                                              \
     }
-#define KUSH_RING_LOOP()                                     \
-    for (int j0 = 0; nc > 0; j0 += RING) {                   \
-        KUSH_PAGE_STEP(0)                                    \
-        KUSH_PAGE_STEP(1)                                    \
-        if constexpr (RING > 2) KUSH_PAGE_STEP(2)            \
-        if constexpr (RING > 3) KUSH_PAGE_STEP(3)            \
+#define KUSH_RING_LOOP()                           \
+    for (int j0 = 0; nc > 0; j0 += 4) {            \
+        KUSH_PAIR(sl0, sl1, j0)                    \
+        KUSH_PAIR(sl2, sl3, j0 + 2)                \
     }
     // the first chunk has a loop of its own: one entry state per ring loop keeps the waits exact
     KUSH_RING_LOOP()
@@ -476,19 +487,29 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
         KUSH_RING_LOOP()
     }
 #undef KUSH_RING_LOOP
-#undef KUSH_PAGE_STEP
+#undef KUSH_PAIR
 #undef KUSH_PROLOGUE
 #undef KUSH_ISSUE
     KUSH_WAIT_VM(0);                                             // drain the trailing (empty) issues
-    __syncthreads();                                             // qs_l ready; rings idle
+    __syncthreads();                                             // rings idle
 
     // partial last page (last split only): V rows from its record, staged by the wave that owns the
-    // page; exact fp32 K . q scores from the tail, spread over all waves (lane: token lane % 32, heads
-    // 2 w + lane / 32 + 2 NW i)
+    // page in its slot 0; exact fp32 K . q scores from the tail, spread over all waves (lane: token
+    // lane % 32, heads 2 w + lane / 32 + 2 NW i), with q (fp32, hi + lo) and the scores in the rings
     if (has_tail) {
-        const bool own = w == (p1 - p0) % NW;
-        if (own) issue_page<D, BITS>(sl0, true, bt[full], head_base, bs, voff);
-        constexpr int HPL = 16 / (2 * NW);           // heads per lane
+        float* const qs = reinterpret_cast<float*>(ringB + AL::Q_OFF);    // [16][D] q sm log2e
+        float* const sc = reinterpret_cast<float*>(ringB + AL::SC_OFF);   // [16][PAGE] tail scores
+        const int ow = (p1 - p0) % NW;
+        uint8_t* const tslot = ringA + 2 * ow * R::SLOT;
+        if (w == ow) issue_page<D, BITS>(tslot, true, bt[full], head_base, bs, voff);
+        if (w == 0) {                                            // wave 0 holds q of all 16 heads over all dims
+#pragma unroll
+            for (int kk = 0; kk < KSTEPS; ++kk)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) qs[r16 * D + kdim<D, BITS>(kk, q, j)] = (float)qh[kk][j] + (float)ql[kk][j];
+        }
+        __syncthreads();
+        constexpr int HPL = 16 / (2 * NW);                       // heads per lane
         const int t = lane & 31, hg = 2 * w + (lane >> 5);
         const IN* tk = tail_k + (((int64_t)tail_idx[s] * H + h) * PAGE + min(t, tail_n - 1)) * D;
         float acc[HPL];
@@ -500,21 +521,22 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
             load8(tk + d, kx);
 #pragma unroll
             for (int i = 0; i < HPL; ++i) {
-                const float4 qa = *reinterpret_cast<const float4*>(&qs_l[(hg + 2 * NW * i) * D + d]);
-                const float4 qb = *reinterpret_cast<const float4*>(&qs_l[(hg + 2 * NW * i) * D + d + 4]);
+                const float4 qa = *reinterpret_cast<const float4*>(&qs[(hg + 2 * NW * i) * D + d]);
+                const float4 qb = *reinterpret_cast<const float4*>(&qs[(hg + 2 * NW * i) * D + d + 4]);
                 acc[i] += qa.x * kx[0] + qa.y * kx[1] + qa.z * kx[2] + qa.w * kx[3] +
                           qb.x * kx[4] + qb.y * kx[5] + qb.z * kx[6] + qb.w * kx[7];
             }
         }
 #pragma unroll
-        for (int i = 0; i < HPL; ++i) sc_l[(hg + 2 * NW * i) * PAGE + t] = t < tail_n ? acc[i] : -__builtin_inff();
+        for (int i = 0; i < HPL; ++i) sc[(hg + 2 * NW * i) * PAGE + t] = t < tail_n ? acc[i] : -__builtin_inff();
         __syncthreads();
-        if (own) {
-            float x[8];
+        if (w == ow) {
+            float x[1][8];
 #pragma unroll
-            for (int jj = 0; jj < 8; ++jj) x[jj] = sc_l[r16 * PAGE + tok(q, jj)];
+            for (int jj = 0; jj < 8; ++jj) x[0][jj] = sc[r16 * PAGE + tok(q, jj)];
             KUSH_WAIT_VM(0);
-            consume_page<D, BITS>(sl0, o, x, tail_n, m_run, l_run, vb_run, lane);
+            const uint8_t* const sp[1] = {tslot};
+            consume_pages<D, BITS, 1>(sp, o, x, m_run, l_run, vb_run, lane);
         }
     }
 
@@ -522,8 +544,7 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     // (region of wave ww: 16 D floats, dims d as [d / 4][head][d % 4], one 16-byte store per lane and
     // tile); after one barrier, wave w sums tiles w, w + NW, ... over the waves and writes them out.
     constexpr int OBYTES = 16 * D * 4;
-    constexpr int PER = NW * R::SLOT / OBYTES;                 // wave regions per ring array
-    static_assert(PER >= 1 && 2 * PER >= NW, "the merge needs 16 D floats per wave in two ring arrays");
+    static_assert(NW * OBYTES <= 2 * NW * R::SLOT, "the merge needs 16 D floats per wave in the first array");
     l_run = rows_sum(l_run);
     vb_run = rows_sum(vb_run);
     if (q == 0) {
@@ -536,7 +557,7 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     for (int ww = 0; ww < NW; ++ww) M = __builtin_fmaxf(M, m_l[ww * 16 + r16]);
     {
         const float f = m_run == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m_run - M);
-        uint8_t* reg = w < PER ? ring0 + w * OBYTES : ring1 + (w - PER) * OBYTES;
+        uint8_t* reg = ringA + w * OBYTES;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
             f4 v;
@@ -560,7 +581,7 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
         f4 acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int ww = 0; ww < NW; ++ww) {
-            const uint8_t* reg = ww < PER ? ring0 + ww * OBYTES : ring1 + (ww - PER) * OBYTES;
+            const uint8_t* reg = ringA + ww * OBYTES;
             acc += *reinterpret_cast<const f4*>(reg + (((4 * dt + q) * 16 + r16) * 4) * 4);
         }
         if (r16 < Gc) {
@@ -588,11 +609,11 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
         const int n_gc = gridDim.z / NS;
         int32_t* ctr = sync + ((int64_t)s * H + h) * n_gc + gc;
         const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        last_flag = prev == NS - 1;
+        *last_flag = prev == NS - 1;
         if (prev == NS - 1) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    if (!last_flag) return;
+    if (!*last_flag) return;
     const int64_t base = ((int64_t)s * H + h) * NS;
     for (int i = threadIdx.x; i < Gc * D; i += NW * WAVE) {
         const int g = g0 + i / D, d = i % D;
@@ -646,8 +667,7 @@ static int launch_decode(dim3 grid, hipStream_t stream, const void* q, void* out
                          int64_t hs, const void* tail_k, const int32_t* tail_idx, const int32_t* block_table,
                          const int32_t* seq_lens, int64_t bt_stride, int hkv, int group, float sm_log2, int n_splits,
                          float* part_ml, float* part_o, int32_t* sync) {
-    constexpr int RING = ring_for<D, BITS, NW>();
-    decode_kernel<D, BITS, IN, NW, RING><<<grid, dim3(NW * WAVE), 0, stream>>>(
+    decode_kernel<D, BITS, IN, NW><<<grid, dim3(NW * WAVE), 0, stream>>>(
         (const IN*)q, (IN*)out, (const uint8_t*)cache, bs, hs, (const IN*)tail_k, tail_idx, block_table, seq_lens,
         bt_stride, hkv, group, sm_log2, n_splits, part_ml, part_o, sync);
     return kush_check_launch("kush_decode");
@@ -685,11 +705,12 @@ extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const v
                          bt_stride, hkv, group, sm_log2, n_splits, part_ml, part_o, split_sync
         // the largest of the requested, 4 and 2 waves whose rings fit in LDS
         if (waves >= 8) {
-            if constexpr (ring_for<D, BITS, 8>() >= 2) return launch_decode<D, BITS, IN, 8>(KUSH_DECODE_ARGS);
+            if constexpr (decode_fits<D, BITS, 8>()) return launch_decode<D, BITS, IN, 8>(KUSH_DECODE_ARGS);
         }
         if (waves >= 4) {
-            if constexpr (ring_for<D, BITS, 4>() >= 2) return launch_decode<D, BITS, IN, 4>(KUSH_DECODE_ARGS);
+            if constexpr (decode_fits<D, BITS, 4>()) return launch_decode<D, BITS, IN, 4>(KUSH_DECODE_ARGS);
         }
+        static_assert(decode_fits<D, BITS, 2>(), "two waves' rings must fit in LDS");
         return launch_decode<D, BITS, IN, 2>(KUSH_DECODE_ARGS);
 #undef KUSH_DECODE_ARGS
     });

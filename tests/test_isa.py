@@ -1,0 +1,63 @@
+"""Static checks of the decode kernels' gfx950 assembly (hipcc -S, on the CPU).
+
+The page loop issues its buffer-to-LDS loads in asm, out of the compiler's sight, and waits for
+them with explicit vmcnt counts; the asm sets m0, which the compiler reserves. That is sound only
+while (1) nothing else in these kernels reads m0 (no movrel / gpr-index instructions, every write
+of m0 is the one our load sequence makes) and (2) the compiler inserts no LDS-DMA of its own."""
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+SRC = ROOT / "kushkash_amd" / "csrc" / "kush_decode.hip"
+
+
+@pytest.fixture(scope="module")
+def asm(tmp_path_factory):
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(hipcc).exists():
+        pytest.skip("hipcc not available")
+    from kushkash_amd.build import FLAGS
+    out = tmp_path_factory.mktemp("isa") / "kush_decode.s"
+    flags = [f for f in FLAGS if f not in ("-shared", "-fPIC")]
+    subprocess.run([hipcc, *flags, f"-I{ROOT / 'include'}", "-S", "--cuda-device-only", str(SRC), "-o", str(out)],
+                   check=True, capture_output=True)
+    return out.read_text()
+
+
+def kernels(asm_text: str) -> dict[str, list[str]]:
+    """kernel symbol -> its instruction lines (decode kernels only)."""
+    out, cur = {}, None
+    for line in asm_text.splitlines():
+        m = re.match(r"^(_ZN4kush13decode_kernel\w+):", line)
+        if m:
+            cur = m.group(1)
+            out[cur] = []
+        elif cur and re.match(r"^\s*\.Lfunc_end", line):
+            cur = None
+        elif cur:
+            out[cur].append(line.split(";")[0].strip())
+    return out
+
+
+def test_m0_is_only_the_lds_load_base(asm):
+    ks = kernels(asm)
+    assert len(ks) >= 30, "expected every decode kernel instantiation"
+    for name, lines in ks.items():
+        for i, ins in enumerate(lines):
+            assert not re.match(r"(v_movrel|s_movrel|s_set_gpr_idx|v_interp|ds_gws|s_sendmsg)", ins), (name, ins)
+            if "m0" in ins:
+                assert re.match(r"s_mov_b32 m0, s\d+$", ins), (name, ins)
+                nxt = next(l for l in lines[i + 1:] if l)
+                assert re.match(r"buffer_load_dwordx4 v\d+, s\[\d+:\d+\], 0 offen lds$", nxt), (name, nxt)
+
+
+def test_every_lds_load_is_ours(asm):
+    for name, lines in kernels(asm).items():
+        for i, ins in enumerate(lines):
+            if ins.endswith(" lds") or "_lds_" in ins:
+                prev = [l for l in lines[:i] if l][-1]
+                assert prev.startswith("s_mov_b32 m0,"), (name, prev, ins)
