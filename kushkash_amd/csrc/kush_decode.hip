@@ -89,7 +89,9 @@ __device__ __forceinline__ int tok(int q, int j) { return 16 * (j >> 2) + 4 * q 
 // placed XOR-swizzled within their row, chunk c of row r at position c ^ swz(r), so the column-wise
 // V gathers and the K row reads spread over the 64 LDS banks; the scales and biases stay in place.
 // The swizzle is applied on the source side: the lane that fills LDS chunk L loads record chunk
-// src_chunk(L).
+// src_chunk(L). A slot is exactly one record: instruction i covers chunks [64 i, 64 i + 64), except
+// the last, which covers the record's last 64 chunks and so rewrites the overlap with the same bytes
+// (a lane past the end of its 1 KB would write zeros beyond the slot).
 template <int D, int BITS>
 struct Ring {
     using F = Fmt<D, BITS>;
@@ -97,8 +99,11 @@ struct Ring {
     static constexpr int CODE_CHUNKS = 64 * CPR;            // K rows then V rows
     static constexpr int CHUNKS = F::REC / 16;
     static constexpr int DMA = (CHUNKS + WAVE - 1) / WAVE;   // 1 KB instructions per page
-    static constexpr int SLOT = DMA * WAVE * 16;            // LDS bytes per ring slot
+    static constexpr int SLOT = F::REC;                     // LDS bytes per ring slot
     static constexpr int RSHIFT = F::DC >= 256 ? 0 : (F::DC == 128 ? 1 : (F::DC == 64 ? 2 : 3));
+    static_assert(CHUNKS >= WAVE, "a record spans at least one full instruction");
+    // first LDS chunk filled by instruction i
+    static constexpr int chunk0(int i) { return i < DMA - 1 ? WAVE * i : CHUNKS - WAVE; }
 };
 
 // Swizzle of code row r (0-31 K, 32-63 V). K rows are read row-wise (16 rows by 16 lanes):
@@ -256,9 +261,9 @@ __device__ __forceinline__ void consume_pages(const uint8_t* const (&slot)[NP], 
         }
 }
 
-// Stage the record of block blk into LDS at dst: R::DMA buffer-to-LDS loads of 1 KB (lanes past the
-// record's end read zeros). An invalid page (past the wave's last) gets an empty buffer range: the
-// loads then fill the slot with zeros and touch no memory, and still count in vmcnt like a real page.
+// Stage the record of block blk into LDS at dst: R::DMA buffer-to-LDS loads of 1 KB. An invalid page
+// (past the window's last) gets an empty buffer range: the loads then fill the slot with zeros and
+// touch no memory, and still count in vmcnt like a real page.
 // The loads are written in asm so that the compiler does not track them: the page loop waits for
 // them with explicit vmcnt counts alone. Vector loads complete in order, so any vector memory op the
 // compiler adds (issued later) only makes those waits stricter.
@@ -278,7 +283,7 @@ __device__ __forceinline__ void issue_page(uint8_t* dst, bool valid, int blk, co
 #pragma unroll
     for (int i = 0; i < R::DMA; ++i)
         asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                     :: "s"(lds + i * WAVE * 16), "v"(voff[i]), "s"(rsrc) : "memory", "m0");
+                     :: "s"(lds + R::chunk0(i) * 16), "v"(voff[i]), "s"(rsrc) : "memory", "m0");
 #pragma clang diagnostic pop
 }
 
@@ -336,13 +341,16 @@ __device__ __forceinline__ void page_scores(const uint8_t* slot, const h8 (&qh)[
     for (int jj = 0; jj < 8; ++jj) x[jj] = __builtin_fmaf(sacc[jj >> 2][jj & 3], TWO24, kacc[0]);
 }
 
+// Pages per window of the page loop: the block ids of a window sit in an LDS table.
+constexpr int WIN = 2048;
+
 // Static LDS of one decode workgroup: two arrays, each holding one page pair per wave (wave w at
-// 2 w SLOT), nothing else. After the page loop the idle arrays hold everything else: the cross-wave
-// merge in the first; the exact-K tail's q and scores, the waves' softmax state and the split-K flag
-// in the second.
+// 2 w SLOT), the window's block-id table and the pair counter. After the page loop the idle arrays
+// hold everything else: the cross-wave merge in the first; the exact-K tail's q and scores, the
+// waves' softmax state and the split-K flag in the second.
 template <int D, int BITS, int NW>
 constexpr int decode_lds_bytes() {
-    return 4 * NW * Ring<D, BITS>::SLOT;
+    return 4 * NW * Ring<D, BITS>::SLOT + 4 * WIN + 16;
 }
 
 template <int D, int BITS, int NW>
@@ -382,6 +390,8 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     // pair is only read once both have landed)
     __shared__ __align__(16) uint8_t ringA[2 * NW * R::SLOT];
     __shared__ __align__(16) uint8_t ringB[2 * NW * R::SLOT];
+    __shared__ __align__(16) int tbl[WIN];                               // block ids of the window
+    __shared__ uint32_t pair_ctr;                                        // next pair of the window
     float* const m_l = reinterpret_cast<float*>(ringB + AL::ML_OFF);      // after the loop only
     float* const l_l = m_l + NW * 16;
     int* const last_flag = reinterpret_cast<int*>(l_l + NW * 16);
@@ -409,105 +419,115 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     // per-lane DMA source offsets (swizzled code rows), fixed for every page
     uint32_t voff[R::DMA];
 #pragma unroll
-    for (int i = 0; i < R::DMA; ++i) voff[i] = src_chunk<D, BITS>(WAVE * i + lane) * 16u;
-
-    // Page j of this wave is p0 + w + j NW. The wave walks its pages in chunks of 64, whose block ids
-    // sit in one VGPR (lane i: page c0 + i) and reach the scalar unit by v_readlane, and within a
-    // chunk in pairs: pair (j, j + 1) in slots (0, 1) or (2, 3) while the next pair is in flight in
-    // the other two. Every issue is R::DMA instructions, also past the chunk's end (an empty buffer
-    // range: no memory access), so vmcnt counts stay exact.
-    const int np = p1 - p0 > w ? (p1 - p0 - w + NW - 1) / NW : 0;       // pages of this wave
-    const int32_t* bt_w = bt + p0 + w;
-    int c0, nc = min(np, 64);                                            // chunk start, pages in it
-    int ids = lane < nc ? bt_w[lane * NW] : 0;     // block ids of the wave's first 64 pages
-
-    // this lane's q head (B column r16) over its contraction dims (8 consecutive dims per K-step),
-    // loaded after the block ids and before the first DMAs, so that each wait covers only what it
-    // needs. Lanes of heads past the chunk read the chunk's last head and zero it.
-    const bool gv = r16 < Gc;
-    float qv[KSTEPS][8];
-#pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) load8(qg + qbase + (int64_t)min(r16, Gc - 1) * D + kdim<D, BITS>(kk, q, 0), qv[kk]);
-
-#define KUSH_ISSUE(SLOT, J) \
-    issue_page<D, BITS>(SLOT, (J) < nc, (J) < nc ? __builtin_amdgcn_readlane(ids, (J) & 63) : 0, head_base, bs, voff)
-#define KUSH_PROLOGUE()   \
-    KUSH_ISSUE(sl0, 0);   \
-    KUSH_ISSUE(sl1, 1);   \
-    KUSH_ISSUE(sl2, 2);   \
-    KUSH_ISSUE(sl3, 3);
-    KUSH_PROLOGUE()
-
-    h8 qh[KSTEPS], ql[KSTEPS];
-#pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float xq = gv ? qv[kk][j] * sm_log2 : 0.0f;
-            const _Float16 hi = (_Float16)xq;
-            qh[kk][j] = hi;
-            ql[kk][j] = (_Float16)(xq - (float)hi);
-        }
+    for (int i = 0; i < R::DMA; ++i) voff[i] = src_chunk<D, BITS>(R::chunk0(i) + lane) * 16u;
 
     f4 o[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     float m_run = -__builtin_inff(), l_run = 0.0f, vb_run = 0.0f;
 
-    // One pair step: its two pages have landed once at most the next pair's loads are outstanding;
-    // scores of both pages, one softmax update, PV of both; then, every read of the two slots
-    // complete (lgkmcnt 0), they take pages J + 4, J + 5. An odd last page pairs with a masked one.
-#define KUSH_PAIR(SA, SB, J)                                                                  \
-    {                                                                                         \
-        KUSH_WAIT_VM(2 * R::DMA);                                                             \
-        float x[2][8];                                                                        \
-        page_scores<D, BITS>(SA, qh, ql, x[0], lane);                                         \
-        page_scores<D, BITS>(SB, qh, ql, x[1], lane);                                         \
-        if ((J) + 1 >= nc) {                                                                  \
-            _Pragma("unroll") for (int jj = 0; jj < 8; ++jj) x[1][jj] = -__builtin_inff();    \
-        }                                                                                     \
-        const uint8_t* const sp[2] = {SA, SB};                                                \
-        consume_pages<D, BITS, 2>(sp, o, x, m_run, l_run, vb_run, lane);                      \
-        if ((J) + 2 >= nc) break;                                                             \
-        __builtin_amdgcn_s_waitcnt(0xC07F);                    /* lgkmcnt(0): slot reads done */ \
-        KUSH_ISSUE(SA, (J) + 4);                                                              \
-        KUSH_ISSUE(SB, (J) + 5);                                                              \
+    // The split's pages go out in pairs (k: pages 2k, 2k + 1 of the window) from a counter in LDS,
+    // over windows of WIN pages whose block ids are first copied to an LDS table: waves the hardware
+    // runs more often simply take more pairs, and all waves finish together. A wave holds two pairs,
+    // in slots (0, 1) and (2, 3): one is consumed while the other is in flight. A wave's pairs only
+    // grow, so once the pair it would consume is past the window's end, so is the one in flight. Each
+    // pair issue is 2 R::DMA instructions, also for a pair past the end (an empty buffer range: no
+    // memory access), so vmcnt counts stay exact.
+    if (p1 > p0) {
+        int wb = p0, wn = min(WIN, p1 - p0), pairs = (wn + 1) / 2;
+        const auto load_window = [&]() {
+            for (int i = threadIdx.x; i < wn; i += NW * WAVE) tbl[i] = bt[wb + i];
+            if (threadIdx.x == 0) pair_ctr = 2 * NW;
+        };
+#define KUSH_ISSUE_PAIR(SA, SB, P)                                                                 \
+    {                                                                                              \
+        const int2 id2 = *reinterpret_cast<const int2*>(tbl + min(2 * (P), WIN - 2));              \
+        issue_page<D, BITS>(SA, (P) < pairs, __builtin_amdgcn_readfirstlane(id2.x), head_base, bs, voff);  \
+        issue_page<D, BITS>(SB, 2 * (P) + 1 < wn, __builtin_amdgcn_readfirstlane(id2.y), head_base, bs, voff); \
     }
-#define KUSH_RING_LOOP()                           \
-    for (int j0 = 0; nc > 0; j0 += 4) {            \
-        KUSH_PAIR(sl0, sl1, j0)                    \
-        KUSH_PAIR(sl2, sl3, j0 + 2)                \
-    }
-    // the first chunk has a loop of its own: one entry state per ring loop keeps the waits exact
-    KUSH_RING_LOOP()
-    for (c0 = 64; c0 < np; c0 += 64) {
-        nc = min(np - c0, 64);                                   // next chunk: its ids, then its first pages
-        ids = lane < nc ? bt_w[(c0 + lane) * NW] : 0;
-        KUSH_PROLOGUE()
-        KUSH_RING_LOOP()
-    }
-#undef KUSH_RING_LOOP
-#undef KUSH_PAIR
-#undef KUSH_PROLOGUE
-#undef KUSH_ISSUE
-    KUSH_WAIT_VM(0);                                             // drain the trailing (empty) issues
-    __syncthreads();                                             // rings idle
+        // this lane's q head (B column r16) over its contraction dims (8 consecutive dims per K-step),
+        // in flight with the table loads, and converted before the barrier: no vector memory load of
+        // the compiler's is outstanding once the page DMAs start. Lanes of heads past the chunk read
+        // the chunk's last head and zero it.
+        const bool gv = r16 < Gc;
+        float qv[KSTEPS][8];
+#pragma unroll
+        for (int kk = 0; kk < KSTEPS; ++kk) load8(qg + qbase + (int64_t)min(r16, Gc - 1) * D + kdim<D, BITS>(kk, q, 0), qv[kk]);
+        load_window();
+        h8 qh[KSTEPS], ql[KSTEPS];
+#pragma unroll
+        for (int kk = 0; kk < KSTEPS; ++kk)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float xq = gv ? qv[kk][j] * sm_log2 : 0.0f;
+                const _Float16 hi = (_Float16)xq;
+                qh[kk][j] = hi;
+                ql[kk][j] = (_Float16)(xq - (float)hi);
+            }
+        int pa = w, pb = NW + w;                                         // the pairs in slots (0, 1), (2, 3)
+        __syncthreads();
+        KUSH_ISSUE_PAIR(sl0, sl1, pa)
+        KUSH_ISSUE_PAIR(sl2, sl3, pb)
 
-    // partial last page (last split only): V rows from its record, staged by the wave that owns the
-    // page in its slot 0; exact fp32 K . q scores from the tail, spread over all waves (lane: token
-    // lane % 32, heads 2 w + lane / 32 + 2 NW i), with q (fp32, hi + lo) and the scores in the rings
+        // One pair step: the pair has landed once at most the other pair's loads are outstanding;
+        // the next pair is taken from the counter (its result and the table read hide behind the
+        // scores), then scores of both pages, one softmax update, PV of both; then, every read of the
+        // two slots complete (lgkmcnt 0), they take the next pair. The second page of a window's odd
+        // last pair is masked.
+#define KUSH_STEP(SA, SB, P)                                                                       \
+    {                                                                                              \
+        if ((P) >= pairs) break;                                                                   \
+        KUSH_WAIT_VM(2 * R::DMA);                                                                  \
+        int nx = 0;                                                                                \
+        if (lane == 0) nx = (int)__builtin_amdgcn_atomic_inc32(&pair_ctr, ~0u, __ATOMIC_RELAXED, "workgroup"); \
+        float x[2][8];                                                                             \
+        page_scores<D, BITS>(SA, qh, ql, x[0], lane);                                              \
+        page_scores<D, BITS>(SB, qh, ql, x[1], lane);                                              \
+        if (2 * (P) + 1 >= wn) {                                                                   \
+            _Pragma("unroll") for (int jj = 0; jj < 8; ++jj) x[1][jj] = -__builtin_inff();         \
+        }                                                                                          \
+        nx = __builtin_amdgcn_readfirstlane(nx);                                                   \
+        const int2 id2 = *reinterpret_cast<const int2*>(tbl + min(2 * nx, WIN - 2));               \
+        const uint8_t* const sp[2] = {SA, SB};                                                     \
+        consume_pages<D, BITS, 2>(sp, o, x, m_run, l_run, vb_run, lane);                           \
+        __builtin_amdgcn_s_waitcnt(0xC07F);                    /* lgkmcnt(0): slot reads done */    \
+        issue_page<D, BITS>(SA, nx < pairs, __builtin_amdgcn_readfirstlane(id2.x), head_base, bs, voff);  \
+        issue_page<D, BITS>(SB, 2 * nx + 1 < wn, __builtin_amdgcn_readfirstlane(id2.y), head_base, bs, voff); \
+        (P) = nx;                                                                                  \
+    }
+        for (;;) {
+            for (;;) {
+                KUSH_STEP(sl0, sl1, pa)
+                KUSH_STEP(sl2, sl3, pb)
+            }
+            KUSH_WAIT_VM(0);                                     // drain the trailing (empty) issues
+            __syncthreads();                                     // table, counter and rings idle
+            wb += WIN;
+            if (wb >= p1) break;
+            wn = min(WIN, p1 - wb);
+            pairs = (wn + 1) / 2;
+            pa = w;
+            pb = NW + w;
+            load_window();
+            __syncthreads();
+            KUSH_ISSUE_PAIR(sl0, sl1, pa)
+            KUSH_ISSUE_PAIR(sl2, sl3, pb)
+        }
+#undef KUSH_STEP
+#undef KUSH_ISSUE_PAIR
+    }
+
+    // partial last page (last split only): V rows from its record, staged by one wave in its slot 0;
+    // exact fp32 K . q scores from the tail, spread over all waves (lane: token lane % 32, heads
+    // 2 w + lane / 32 + 2 NW i), with q (fp32, times sm log2 e) and the scores in the rings
     if (has_tail) {
         float* const qs = reinterpret_cast<float*>(ringB + AL::Q_OFF);    // [16][D] q sm log2e
         float* const sc = reinterpret_cast<float*>(ringB + AL::SC_OFF);   // [16][PAGE] tail scores
         const int ow = (p1 - p0) % NW;
         uint8_t* const tslot = ringA + 2 * ow * R::SLOT;
         if (w == ow) issue_page<D, BITS>(tslot, true, bt[full], head_base, bs, voff);
-        if (w == 0) {                                            // wave 0 holds q of all 16 heads over all dims
-#pragma unroll
-            for (int kk = 0; kk < KSTEPS; ++kk)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) qs[r16 * D + kdim<D, BITS>(kk, q, j)] = (float)qh[kk][j] + (float)ql[kk][j];
-        }
+        for (int i = threadIdx.x; i < 16 * D; i += NW * WAVE)
+            qs[i] = i < Gc * D ? to_f32(qg[qbase + i]) * sm_log2 : 0.0f;
         __syncthreads();
         constexpr int HPL = 16 / (2 * NW);                       // heads per lane
         const int t = lane & 31, hg = 2 * w + (lane >> 5);
