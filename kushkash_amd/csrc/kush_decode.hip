@@ -25,6 +25,8 @@
 //   C: rows 4q .. 4q+3 of column r.
 // Which physical dim or token a slot stands for is chosen here (kdim, tok), identically for A
 // and B, so only the C layout is relied upon.
+#include <cmath>
+
 #include "kush_common.h"
 
 namespace kush {
@@ -152,11 +154,45 @@ __device__ __forceinline__ h8 sub_codes4(uint32_t lo, uint32_t hi) {    // 4 + 4
                                      __builtin_amdgcn_perm(0u, hi, 0x0C010C00u), __builtin_amdgcn_perm(0u, hi, 0x0C030C02u)});
 }
 
-// two int4 words -> (low nibbles of both, high nibbles of both), as n = c + 8
-__device__ __forceinline__ void int4_sub2(uint32_t w0, uint32_t w1, h8& lo, h8& hi) {
-    const uint32_t x0 = w0 ^ 0x88888888u, x1 = w1 ^ 0x88888888u;
-    lo = sub_codes4(x0 & 0x0F0F0F0Fu, x1 & 0x0F0F0F0Fu);
-    hi = sub_codes4((x0 >> 4) & 0x0F0F0F0Fu, (x1 >> 4) & 0x0F0F0F0Fu);
+// int4 codes to operands. The xor with 0x88 turns a two's-complement nibble into n = c + 8; a
+// nibble is then masked in place: a low nibble is the subnormal n, a high nibble lands 4 bits up,
+// as 16 n. Each of (x ^ 0x88888888) & mask is one v_bitop3.
+constexpr uint32_t NIB_XOR = 0x88888888u, NIB_LO = 0x000F000Fu, NIB_HI = 0x00F000F0u;
+
+// K: two words (8 code bytes of a row, dims in order) -> the low nibbles (n) and the high nibbles
+// (16 n) of the 8 bytes, in byte order: v_perm spreads two bytes into the low bytes of the halves.
+__device__ __forceinline__ void k_codes4(uint32_t w0, uint32_t w1, h8& lo, h8& hi) {
+    const uint32_t p[4] = {__builtin_amdgcn_perm(0u, w0, 0x0C010C00u), __builtin_amdgcn_perm(0u, w0, 0x0C030C02u),
+                           __builtin_amdgcn_perm(0u, w1, 0x0C010C00u), __builtin_amdgcn_perm(0u, w1, 0x0C030C02u)};
+    u4 l, h;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        l[i] = (p[i] ^ NIB_XOR) & NIB_LO;
+        h[i] = (p[i] ^ NIB_XOR) & NIB_HI;
+    }
+    lo = __builtin_bit_cast(h8, l);
+    hi = __builtin_bit_cast(h8, h);
+}
+
+// V^T: two words of 4 token bytes each (PV slots 0-3, 4-7) -> low nibbles (n) and high nibbles
+// (16 n) in slot order 0 2 1 3 4 6 5 7: bytes 0 and 2 of a word are masked in place, bytes 1 and 3
+// after a shift by 8. The P' operand takes the same order (VSLOT).
+__device__ __forceinline__ void v_codes4(uint32_t w0, uint32_t w1, h8& lo, h8& hi) {
+    const uint32_t p[4] = {w0, w0 >> 8, w1, w1 >> 8};
+    u4 l, h;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        l[i] = (p[i] ^ NIB_XOR) & NIB_LO;
+        h[i] = (p[i] ^ NIB_XOR) & NIB_HI;
+    }
+    lo = __builtin_bit_cast(h8, l);
+    hi = __builtin_bit_cast(h8, h);
+}
+
+// PV slot held by operand position k (int4: the v_codes4 order; int8: in order)
+template <int BITS>
+__device__ __forceinline__ constexpr int vslot(int k) {
+    return BITS == 4 ? (k & 4) | ((k & 1) << 1) | ((k >> 1) & 1) : k;
 }
 
 // two int8 words (8 codes) -> n = c + 128
@@ -194,23 +230,25 @@ __device__ __forceinline__ v2i gather_vt(const uint8_t* slot, int ct, int lane) 
     return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(src));
 }
 
-// Softmax update over NP staged pages at once (scores x[p] in log2 units for tokens tok(q, j);
-// masked tokens carry -inf) and their PV accumulation from the staged V codes. o accumulates in
-// units of 2^-24 (subnormal codes); vb_run carries the V biases and the code offset: with
-// P' = fp16(e vs), a page adds sum P' n (MFMA) + sum (e vb - HALF P') (here), i.e.
-// sum e (vs' c + vb) with vs' = P' / e.
+// Softmax update over NP staged pages at once and their PV accumulation from the staged V codes.
+// Scores in log2 units are x = a s[p][j] + b[p] (a > 0) for tokens tok(q, j); masked tokens carry
+// s = -inf. o accumulates in units of 2^-24 (subnormal codes; int4 high-nibble tiles, o[D/32 ..],
+// in units of 2^-20); with P' = fp16(e vs) a page adds sum P' n (MFMA), -HALF sum P' (MFMA into
+// vacc, units of 2^-24) and sum e vb (vb_run), i.e. sum e (vs' c + vb) with vs' = P' / e.
 template <int D, int BITS, int NP>
-__device__ __forceinline__ void consume_pages(const uint8_t* const (&slot)[NP], f4 (&o)[D / 16],
-                                              const float (&x)[NP][8], float& m_run, float& l_run, float& vb_run,
-                                              int lane) {
+__device__ __forceinline__ void consume_pages(const uint8_t* const (&slot)[NP], f4 (&o)[D / 16], f4& vacc,
+                                              const float (&sv)[NP][8], float a, const float (&b)[NP],
+                                              float& m_run, float& l_run, float& vb_run, int lane) {
     using F = Fmt<D, BITS>;
-    constexpr float HALF = (float)F::HALF;
     const int q = lane >> 4;
-    float pm = x[0][0];
+    float pm = -__builtin_inff();
 #pragma unroll
-    for (int p = 0; p < NP; ++p)
+    for (int p = 0; p < NP; ++p) {
+        float mx = sv[p][0];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) pm = __builtin_fmaxf(pm, x[p][j]);
+        for (int j = 1; j < 8; ++j) mx = __builtin_fmaxf(mx, sv[p][j]);
+        pm = __builtin_fmaxf(pm, __builtin_fmaf(mx, a, b[p]));
+    }
     // the reference point of the exponentials moves only when the max exceeds it by more than 2^3:
     // weights stay <= 8 (P' = e vs stays far from fp16 overflow) and most steps skip the O rescale
     pm = rows_max(pm);
@@ -221,20 +259,23 @@ __device__ __forceinline__ void consume_pages(const uint8_t* const (&slot)[NP], 
     h8 pw[NP];
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
+        const float bp = b[p] - m_new;
         const h4v vs0 = *reinterpret_cast<const h4v*>(slot[p] + F::OFF_VS + 8 * q);
         const h4v vs1 = *reinterpret_cast<const h4v*>(slot[p] + F::OFF_VS + 32 + 8 * q);
         const h4v vb0 = *reinterpret_cast<const h4v*>(slot[p] + F::OFF_VB + 8 * q);
         const h4v vb1 = *reinterpret_cast<const h4v*>(slot[p] + F::OFF_VB + 32 + 8 * q);
+        _Float16 pv[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const float vsj = (float)(j < 4 ? vs0[j] : vs1[j - 4]);
             const float vbj = (float)(j < 4 ? vb0[j] : vb1[j - 4]);
-            const float e = __builtin_amdgcn_exp2f(x[p][j] - m_new);
-            pw[p][j] = (_Float16)(e * vsj);
+            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[p][j], a, bp));
+            pv[j] = (_Float16)__builtin_fmaf(e, vsj, 0.0f);   // e vs (fma_mix, then one pack per pair)
             lsum += e;
-            // the code offset uses the rounded weight the MFMA sees: sum P' (n - HALF) is then exact
-            vbsum = __builtin_fmaf(-HALF, (float)pw[p][j], __builtin_fmaf(e, vbj, vbsum));
+            vbsum = __builtin_fmaf(e, vbj, vbsum);
         }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) pw[p][k] = pv[vslot<BITS>(k)];
     }
     l_run = l_run * corr + lsum;
     vb_run = vb_run * corr + vbsum;
@@ -242,6 +283,7 @@ __device__ __forceinline__ void consume_pages(const uint8_t* const (&slot)[NP], 
     if (corr != 1.0f) {
 #pragma unroll
         for (int dt = 0; dt < D / 16; ++dt) o[dt] *= corr;
+        vacc *= corr;
     }
 
     constexpr int NCOL = BITS == 4 ? D / 32 : D / 16;
@@ -252,13 +294,18 @@ __device__ __forceinline__ void consume_pages(const uint8_t* const (&slot)[NP], 
             const v2i w = gather_vt<D, BITS>(slot[p], ct, lane);
             if constexpr (BITS == 4) {
                 h8 lo, hi;
-                int4_sub2((uint32_t)w[0], (uint32_t)w[1], lo, hi);
+                v_codes4((uint32_t)w[0], (uint32_t)w[1], lo, hi);
                 o[ct] = mfma16(lo, pw[p], o[ct]);
                 o[ct + D / 32] = mfma16(hi, pw[p], o[ct + D / 32]);
             } else {
                 o[ct] = mfma16(int8_sub((uint32_t)w[0], (uint32_t)w[1]), pw[p], o[ct]);
             }
         }
+    // -HALF sum P' per head: A rows all -HALF 2^-24 (fp16 bits 0x8000 | HALF, exact)
+    const _Float16 nh = __builtin_bit_cast(_Float16, (uint16_t)(0x8000u | (uint32_t)F::HALF));
+    const h8 neg_half = h8{nh, nh, nh, nh, nh, nh, nh, nh};
+#pragma unroll
+    for (int p = 0; p < NP; ++p) vacc = mfma16(neg_half, pw[p], vacc);
 }
 
 // Stage the record of block blk into LDS at dst: R::DMA buffer-to-LDS loads of 1 KB. An invalid page
@@ -287,58 +334,214 @@ __device__ __forceinline__ void issue_page(uint8_t* dst, bool valid, int blk, co
 #pragma clang diagnostic pop
 }
 
-// Scores of the 32 tokens of a staged page in log2 units: x[j] for token tok(q, j), head r16.
-// S^T = K . Q'^T on codes n = c + HALF as subnormal fp16 (units of 2^-24), Q' as an fp16 hi / lo
-// pair; the bias sum_d kb[d] q[d] and the offset -HALF sum_d Q'[d] come from MFMAs whose A rows are
-// all equal.
-template <int D, int BITS>
-__device__ __forceinline__ void page_scores(const uint8_t* slot, const h8 (&qh)[D / 32], const h8 (&ql)[D / 32],
-                                            float (&x)[8], int lane) {
+// Scores of the 64 tokens of a staged page pair (page 0 at s0, page 1 in the next slot):
+// x = a sacc[p][j / 4][j % 4] + kx[p] in log2 units for token tok(q, j) of page p, head r16, with
+// a = rs 2^24.
+// sacc = K . Q'^T on codes n = c + HALF as subnormal fp16 (units of 2^-24) and Q' = q' ks as an fp16
+// pair qp + qr, q' = q p2 (p2 a power of two: q' is exact in fp16 for bf16 / fp16 q; fp32 q adds
+// its low fp16 part ql). int4 high nibbles enter as 16 n against Q' / 16 (qa holds q' / 16 there).
+// kx = rs (sum_d kb[d] q'[d] - HALF sum_d ks[d] q'[d]): two MFMAs per K-step for both pages, their
+// A rows alternating between the pages' biases and scales (row r: page r % 2, so C register i holds
+// page i % 2).
+template <int D, int BITS, bool QLO>
+__device__ __forceinline__ void pair_scores(const uint8_t* s0, const h8 (&qa)[D / 32],
+                                            const h8 (&qla)[D / 32], const h8 (&qh)[D / 32], const h8 (&ql)[D / 32],
+                                            float (&sv)[2][8], float (&kx)[2], float rs, int lane) {
     using F = Fmt<D, BITS>;
     constexpr int KSTEPS = D / 32;
     constexpr int KBYTES = F::DC / 4;                // K code bytes per lane per 16-token tile
-    constexpr _Float16 NH = (_Float16)(-(float)F::HALF);
-    constexpr float TWO24 = 16777216.0f;
     const int r16 = lane & 15, q = lane >> 4;
-    const h8 neg_half = h8{NH, NH, NH, NH, NH, NH, NH, NH};
-    f4 sacc[2] = {f4{0.0f, 0.0f, 0.0f, 0.0f}, f4{0.0f, 0.0f, 0.0f, 0.0f}};
-    f4 kacc = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    const uint8_t* const sl[2] = {s0, s0 + Ring<D, BITS>::SLOT};
+    const uint8_t* const own = s0 + (r16 & 1) * Ring<D, BITS>::SLOT;
+    f4 sacc[2][2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) sacc[p][0] = sacc[p][1] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    f4 kb_acc = f4{0.0f, 0.0f, 0.0f, 0.0f}, ks_acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk) {
-        h8 a[2];
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            // code bytes of row 16 tt + r16 for this K-step, from the swizzled slot
-            const int row = 16 * tt + r16;
-            const int byte = q * KBYTES + 8 * (BITS == 4 ? kk >> 1 : kk);
-            const u2 wv = *reinterpret_cast<const u2*>(slot + slot_chunk<D, BITS>(row, byte / 16) + byte % 16);
-            if constexpr (BITS == 4) {
-                const uint32_t x0 = wv[0] ^ 0x88888888u, x1 = wv[1] ^ 0x88888888u;
-                a[tt] = (kk & 1) ? sub_codes4((x0 >> 4) & 0x0F0F0F0Fu, (x1 >> 4) & 0x0F0F0F0Fu)
-                                 : sub_codes4(x0 & 0x0F0F0F0Fu, x1 & 0x0F0F0F0Fu);
-            } else {
-                a[tt] = int8_sub(wv[0], wv[1]);
-            }
-        }
         const int d0 = kdim<D, BITS>(kk, q, 0);
-        const h8 ks8 = *reinterpret_cast<const h8*>(slot + F::OFF_KS + 2 * d0);
-        const h8 kb8 = *reinterpret_cast<const h8*>(slot + F::OFF_KB + 2 * d0);
-        // Q' = q ks as an fp16 pair: qp = fp16(qh ks), qr = the exact residual of that product plus
-        // ql ks, rounded once (relative error ~2^-22 overall, where qp alone carries 2^-12)
-        const h8 qp = qh[kk] * ks8;
-        h8 qr = __builtin_elementwise_fma(qh[kk], ks8, -qp);
-        qr = __builtin_elementwise_fma(ql[kk], ks8, qr);
-        kacc = mfma16(kb8, qh[kk], kacc);
-        kacc = mfma16(kb8, ql[kk], kacc);
-        kacc = mfma16(neg_half, qp, kacc);
-        kacc = mfma16(neg_half, qr, kacc);
-        sacc[0] = mfma16(a[0], qp, sacc[0]);
-        sacc[1] = mfma16(a[1], qp, sacc[1]);
-        sacc[0] = mfma16(a[0], qr, sacc[0]);
-        sacc[1] = mfma16(a[1], qr, sacc[1]);
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            h8 a[2];
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                // code bytes of row 16 tt + r16 for this K-step, from the swizzled slot
+                const int row = 16 * tt + r16;
+                const int byte = q * KBYTES + 8 * (BITS == 4 ? kk >> 1 : kk);
+                const u2 wv = *reinterpret_cast<const u2*>(sl[p] + slot_chunk<D, BITS>(row, byte / 16) + byte % 16);
+                if constexpr (BITS == 4) {
+                    h8 lo, hi;
+                    k_codes4(wv[0], wv[1], lo, hi);
+                    a[tt] = (kk & 1) ? hi : lo;
+                } else {
+                    a[tt] = int8_sub(wv[0], wv[1]);
+                }
+            }
+            const h8 ks8 = *reinterpret_cast<const h8*>(sl[p] + F::OFF_KS + 2 * d0);
+            // Q' = q' ks as an fp16 pair: qp = fp16(q' ks), qr = the exact residual of that product
+            // (plus ql ks for fp32 q), rounded once
+            const h8 qp = qa[kk] * ks8;
+            h8 qr = __builtin_elementwise_fma(qa[kk], ks8, -qp);
+            if constexpr (QLO) qr = __builtin_elementwise_fma(qla[kk], ks8, qr);
+            sacc[p][0] = mfma16(a[0], qp, sacc[p][0]);
+            sacc[p][1] = mfma16(a[1], qp, sacc[p][1]);
+            sacc[p][0] = mfma16(a[0], qr, sacc[p][0]);
+            sacc[p][1] = mfma16(a[1], qr, sacc[p][1]);
+        }
+        const h8 kbo = *reinterpret_cast<const h8*>(own + F::OFF_KB + 2 * d0);
+        const h8 kso = *reinterpret_cast<const h8*>(own + F::OFF_KS + 2 * d0);
+        kb_acc = mfma16(kbo, qh[kk], kb_acc);
+        ks_acc = mfma16(kso, qh[kk], ks_acc);
+        if constexpr (QLO) {
+            kb_acc = mfma16(kbo, ql[kk], kb_acc);
+            ks_acc = mfma16(kso, ql[kk], ks_acc);
+        }
     }
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj) x[jj] = __builtin_fmaf(sacc[jj >> 2][jj & 3], TWO24, kacc[0]);
+    for (int p = 0; p < 2; ++p) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sv[p][j] = sacc[p][j >> 2][j & 3];
+        kx[p] = rs * __builtin_fmaf(-(float)F::HALF, ks_acc[p], kb_acc[p]);
+    }
+}
+
+// ------------------------------------------------------------------ two page streams (G <= 8)
+// With at most 8 q heads per kv head, MFMA column c stands for head c % 8 of page stream c / 8: a
+// page pair puts page A in columns 0-7 and page B in columns 8-15, so each lane's Q', softmax and
+// P' work covers one (head, page) and no column is idle. Each column keeps its own online-softmax
+// state; the streams of a head are merged with the waves at the end.
+
+// Scores of a staged pair (page A at s0, page B in the next slot) for this lane's column: sv[j] for
+// token tok(q, j) of its page, x = a sv[j] + kx. The Q' operand is built once for both pages (each
+// column from its own page's scales); K of page A and of page B each meet it in their own MFMAs,
+// and a column keeps the product with its page.
+template <int D, int BITS, bool QLO>
+__device__ __forceinline__ void pair_scores2(const uint8_t* s0, const h8 (&qa)[D / 32], const h8 (&qla)[D / 32],
+                                             const h8 (&qh)[D / 32], const h8 (&ql)[D / 32], float (&sv)[8],
+                                             float& kx, float rs, int lane) {
+    using F = Fmt<D, BITS>;
+    constexpr int KSTEPS = D / 32;
+    constexpr int KBYTES = F::DC / 4;
+    constexpr int SLOT = Ring<D, BITS>::SLOT;
+    const int r16 = lane & 15, q = lane >> 4, st = r16 >> 3;
+    const uint8_t* const sl[2] = {s0, s0 + SLOT};
+    const uint8_t* const mine = s0 + st * SLOT;                 // the page of this lane's column
+    const uint8_t* const own = s0 + (r16 & 1) * SLOT;           // A row r16 of the bias MFMAs
+    f4 sacc[2][2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) sacc[p][0] = sacc[p][1] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    f4 kb_acc = f4{0.0f, 0.0f, 0.0f, 0.0f}, ks_acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+        const int d0 = kdim<D, BITS>(kk, q, 0);
+        const h8 ks8 = *reinterpret_cast<const h8*>(mine + F::OFF_KS + 2 * d0);
+        const h8 qp = qa[kk] * ks8;
+        h8 qr = __builtin_elementwise_fma(qa[kk], ks8, -qp);
+        if constexpr (QLO) qr = __builtin_elementwise_fma(qla[kk], ks8, qr);
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            h8 a[2];
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const int row = 16 * tt + r16;
+                const int byte = q * KBYTES + 8 * (BITS == 4 ? kk >> 1 : kk);
+                const u2 wv = *reinterpret_cast<const u2*>(sl[p] + slot_chunk<D, BITS>(row, byte / 16) + byte % 16);
+                if constexpr (BITS == 4) {
+                    h8 lo, hi;
+                    k_codes4(wv[0], wv[1], lo, hi);
+                    a[tt] = (kk & 1) ? hi : lo;
+                } else {
+                    a[tt] = int8_sub(wv[0], wv[1]);
+                }
+            }
+            sacc[p][0] = mfma16(a[0], qp, sacc[p][0]);
+            sacc[p][1] = mfma16(a[1], qp, sacc[p][1]);
+            sacc[p][0] = mfma16(a[0], qr, sacc[p][0]);
+            sacc[p][1] = mfma16(a[1], qr, sacc[p][1]);
+        }
+        const h8 kbo = *reinterpret_cast<const h8*>(own + F::OFF_KB + 2 * d0);
+        const h8 kso = *reinterpret_cast<const h8*>(own + F::OFF_KS + 2 * d0);
+        kb_acc = mfma16(kbo, qh[kk], kb_acc);
+        ks_acc = mfma16(kso, qh[kk], ks_acc);
+        if constexpr (QLO) {
+            kb_acc = mfma16(kbo, ql[kk], kb_acc);
+            ks_acc = mfma16(kso, ql[kk], ks_acc);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sv[j] = st ? sacc[1][j >> 2][j & 3] : sacc[0][j >> 2][j & 3];
+    kx = rs * __builtin_fmaf(-(float)F::HALF, st ? ks_acc[1] : ks_acc[0], st ? kb_acc[1] : kb_acc[0]);
+}
+
+// Softmax update of this lane's column over its page (scores x = a sv[j] + kx; masked tokens
+// sv = -inf; a column may be masked whole) and the PV accumulation of page A (at s0) into columns
+// 0-7 and page B (at s0 + ds) into columns 8-15: each MFMA takes P' with the other stream's
+// columns zeroed. Units as in consume_pages.
+template <int D, int BITS>
+__device__ __forceinline__ void consume2(const uint8_t* s0, int ds, f4 (&o)[D / 16], f4& vacc, const float (&sv)[8],
+                                         float a, float kx, float& m_run, float& l_run, float& vb_run, int lane) {
+    using F = Fmt<D, BITS>;
+    const int r16 = lane & 15, q = lane >> 4, st = r16 >> 3;
+    const uint8_t* const mine = s0 + st * ds;
+    float pm = sv[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) pm = __builtin_fmaxf(pm, sv[j]);
+    pm = rows_max(__builtin_fmaf(pm, a, kx));
+    const float m_new = pm > m_run + 3.0f ? pm : m_run;
+    const bool none = m_new == -__builtin_inff();                 // nothing seen yet in this column
+    const float corr = none ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+    const float bp = none ? 0.0f : kx - m_new;
+
+    const h4v vs0 = *reinterpret_cast<const h4v*>(mine + F::OFF_VS + 8 * q);
+    const h4v vs1 = *reinterpret_cast<const h4v*>(mine + F::OFF_VS + 32 + 8 * q);
+    const h4v vb0 = *reinterpret_cast<const h4v*>(mine + F::OFF_VB + 8 * q);
+    const h4v vb1 = *reinterpret_cast<const h4v*>(mine + F::OFF_VB + 32 + 8 * q);
+    float lsum = 0.0f, vbsum = 0.0f;
+    _Float16 pv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float vsj = (float)(j < 4 ? vs0[j] : vs1[j - 4]);
+        const float vbj = (float)(j < 4 ? vb0[j] : vb1[j - 4]);
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[j], a, bp));
+        pv[j] = (_Float16)__builtin_fmaf(e, vsj, 0.0f);
+        lsum += e;
+        vbsum = __builtin_fmaf(e, vbj, vbsum);
+    }
+    h8 pw;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) pw[k] = pv[vslot<BITS>(k)];
+    const u4 pu = __builtin_bit_cast(u4, pw);
+    const uint32_t keep_a = st ? 0u : ~0u;
+    const h8 pwa = __builtin_bit_cast(h8, pu & keep_a), pwb = __builtin_bit_cast(h8, pu & ~keep_a);
+    l_run = l_run * corr + lsum;
+    vb_run = vb_run * corr + vbsum;
+    m_run = m_new;
+    if (corr != 1.0f) {
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) o[dt] *= corr;
+        vacc *= corr;
+    }
+
+    constexpr int NCOL = BITS == 4 ? D / 32 : D / 16;
+#pragma unroll
+    for (int ct = 0; ct < NCOL; ++ct) {
+        const v2i wa = gather_vt<D, BITS>(s0, ct, lane);
+        const v2i wb = gather_vt<D, BITS>(s0 + ds, ct, lane);
+        if constexpr (BITS == 4) {
+            h8 lo, hi;
+            v_codes4((uint32_t)wa[0], (uint32_t)wa[1], lo, hi);
+            o[ct] = mfma16(lo, pwa, o[ct]);
+            o[ct + D / 32] = mfma16(hi, pwa, o[ct + D / 32]);
+            v_codes4((uint32_t)wb[0], (uint32_t)wb[1], lo, hi);
+            o[ct] = mfma16(lo, pwb, o[ct]);
+            o[ct + D / 32] = mfma16(hi, pwb, o[ct + D / 32]);
+        } else {
+            o[ct] = mfma16(int8_sub((uint32_t)wa[0], (uint32_t)wa[1]), pwa, o[ct]);
+            o[ct] = mfma16(int8_sub((uint32_t)wb[0], (uint32_t)wb[1]), pwb, o[ct]);
+        }
+    }
+    const _Float16 nh = __builtin_bit_cast(_Float16, (uint16_t)(0x8000u | (uint32_t)F::HALF));
+    vacc = mfma16(h8{nh, nh, nh, nh, nh, nh, nh, nh}, pw, vacc);   // column c sums its own P'
 }
 
 // Pages per window of the page loop: the block ids of a window sit in an LDS table.
@@ -365,22 +568,27 @@ struct AfterLoop {
     static constexpr int Q_OFF = 0, SC_OFF = 16 * D * 4, ML_OFF = SC_OFF + 16 * PAGE * 4;
 };
 
-// grid (S, Hkv, n_splits * ceil(G / 16)), block NW * 64.
+// grid (S, Hkv, n_splits * ceil(G / 16)), block NW * 64. ST = 2 (G <= 8): two page streams share the
+// MFMA columns (page A of each pair in columns 0-7, page B in 8-15); ST = 1: one page's 16 heads.
 // NS > 1: each workgroup writes its split's partials; with `sync` (one zeroed int32 per
 // (sequence, kv head, head chunk)), the last workgroup of a (sequence, kv head, head chunk) to
 // finish merges all splits into `out` and resets its counter, so no second launch is needed.
-template <int D, int BITS, typename IN, int NW>
+template <int D, int BITS, typename IN, int NW, int ST>
 __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     const IN* __restrict__ qg, IN* __restrict__ out, const uint8_t* __restrict__ cache, int64_t bs, int64_t hs,
     const IN* __restrict__ tail_k, const int32_t* __restrict__ tail_idx, const int32_t* __restrict__ block_table,
-    const int32_t* __restrict__ seq_lens, int64_t bt_stride, int H, int G, float sm_log2, int NS,
+    const int32_t* __restrict__ seq_lens, int64_t bt_stride, int H, int G, float p2, float rs, int NS,
     float* __restrict__ part_ml, float* __restrict__ part_o, int32_t* __restrict__ sync) {
     using F = Fmt<D, BITS>;
     using R = Ring<D, BITS>;
     constexpr int KSTEPS = D / 32;
     constexpr int DT = D / 16;
-    constexpr float TWO24 = 16777216.0f;
+    constexpr int NLO = BITS == 4 ? D / 32 : D / 16;          // O tiles in units of 2^-24 (the rest 2^-20)
+    constexpr float TWO24 = 16777216.0f, TWO20 = 1048576.0f;
+    constexpr bool QLO = std::is_same<IN, float>::value;      // q needs a low fp16 part
+    const float sm_log2 = p2 * rs;                            // exact: p2 is a power of two
     static_assert(NW == 2 || NW == 4 || NW == 8, "the tail splits 16 heads over 2 NW lane halves");
+    static_assert(ST == 1 || ST == 2, "one or two page streams");
     using AL = AfterLoop<D>;
     static_assert(2 * NW * R::SLOT >= AL::ML_OFF + 2 * NW * 16 * 4 + 16, "the after-loop scratch must fit");
     static_assert(2 * R::DMA <= 63, "vmcnt holds at most 63 loads");
@@ -421,7 +629,7 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
 #pragma unroll
     for (int i = 0; i < R::DMA; ++i) voff[i] = src_chunk<D, BITS>(R::chunk0(i) + lane) * 16u;
 
-    f4 o[DT];
+    f4 o[DT], vacc = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     float m_run = -__builtin_inff(), l_run = 0.0f, vb_run = 0.0f;
@@ -449,21 +657,29 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
         // in flight with the table loads, and converted before the barrier: no vector memory load of
         // the compiler's is outstanding once the page DMAs start. Lanes of heads past the chunk read
         // the chunk's last head and zero it.
-        const bool gv = r16 < Gc;
+        const int hq = ST == 2 ? (r16 & 7) : r16;                        // the head of this lane's column
+        const bool gv = hq < Gc;
         float qv[KSTEPS][8];
 #pragma unroll
-        for (int kk = 0; kk < KSTEPS; ++kk) load8(qg + qbase + (int64_t)min(r16, Gc - 1) * D + kdim<D, BITS>(kk, q, 0), qv[kk]);
+        for (int kk = 0; kk < KSTEPS; ++kk) load8(qg + qbase + (int64_t)min(hq, Gc - 1) * D + kdim<D, BITS>(kk, q, 0), qv[kk]);
         load_window();
-        h8 qh[KSTEPS], ql[KSTEPS];
+        // q' = q p2 as fp16 (+ its low part for fp32 q): qh, ql for the bias MFMAs; qa, qla the Q'
+        // sources, divided by 16 in the int4 K-steps of high nibbles
+        h8 qh[KSTEPS], ql[KSTEPS], qa[KSTEPS], qla[KSTEPS];
 #pragma unroll
         for (int kk = 0; kk < KSTEPS; ++kk)
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float xq = gv ? qv[kk][j] * sm_log2 : 0.0f;
+                const float xq = gv ? qv[kk][j] * p2 : 0.0f;
                 const _Float16 hi = (_Float16)xq;
+                const _Float16 lo = QLO ? (_Float16)(xq - (float)hi) : (_Float16)0.0f;
+                const bool hin = BITS == 4 && (kk & 1);
                 qh[kk][j] = hi;
-                ql[kk][j] = (_Float16)(xq - (float)hi);
+                ql[kk][j] = lo;
+                qa[kk][j] = hin ? (_Float16)((float)hi * 0.0625f) : hi;
+                qla[kk][j] = hin ? (_Float16)((float)lo * 0.0625f) : lo;
             }
+        const float sa = rs * TWO24;                             // x = sa s + kx
         int pa = w, pb = NW + w;                                         // the pairs in slots (0, 1), (2, 3)
         __syncthreads();
         KUSH_ISSUE_PAIR(sl0, sl1, pa)
@@ -480,16 +696,27 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
         KUSH_WAIT_VM(2 * R::DMA);                                                                  \
         int nx = 0;                                                                                \
         if (lane == 0) nx = (int)__builtin_amdgcn_atomic_inc32(&pair_ctr, ~0u, __ATOMIC_RELAXED, "workgroup"); \
-        float x[2][8];                                                                             \
-        page_scores<D, BITS>(SA, qh, ql, x[0], lane);                                              \
-        page_scores<D, BITS>(SB, qh, ql, x[1], lane);                                              \
-        if (2 * (P) + 1 >= wn) {                                                                   \
-            _Pragma("unroll") for (int jj = 0; jj < 8; ++jj) x[1][jj] = -__builtin_inff();         \
+        int2 id2;                                                                                  \
+        if constexpr (ST == 2) {                                                                   \
+            float sv[8], kx;                                                                       \
+            pair_scores2<D, BITS, QLO>(SA, qa, qla, qh, ql, sv, kx, rs, lane);                     \
+            if (2 * (P) + 1 >= wn && r16 >= 8) {                                                   \
+                _Pragma("unroll") for (int jj = 0; jj < 8; ++jj) sv[jj] = -__builtin_inff();       \
+            }                                                                                      \
+            nx = __builtin_amdgcn_readfirstlane(nx);                                               \
+            id2 = *reinterpret_cast<const int2*>(tbl + min(2 * nx, WIN - 2));                      \
+            consume2<D, BITS>(SA, R::SLOT, o, vacc, sv, sa, kx, m_run, l_run, vb_run, lane);       \
+        } else {                                                                                   \
+            const uint8_t* const sp[2] = {SA, SB};                                                 \
+            float sv[2][8], kx[2];                                                                 \
+            pair_scores<D, BITS, QLO>(SA, qa, qla, qh, ql, sv, kx, rs, lane);                      \
+            if (2 * (P) + 1 >= wn) {                                                               \
+                _Pragma("unroll") for (int jj = 0; jj < 8; ++jj) sv[1][jj] = -__builtin_inff();    \
+            }                                                                                      \
+            nx = __builtin_amdgcn_readfirstlane(nx);                                               \
+            id2 = *reinterpret_cast<const int2*>(tbl + min(2 * nx, WIN - 2));                      \
+            consume_pages<D, BITS, 2>(sp, o, vacc, sv, sa, kx, m_run, l_run, vb_run, lane);        \
         }                                                                                          \
-        nx = __builtin_amdgcn_readfirstlane(nx);                                                   \
-        const int2 id2 = *reinterpret_cast<const int2*>(tbl + min(2 * nx, WIN - 2));               \
-        const uint8_t* const sp[2] = {SA, SB};                                                     \
-        consume_pages<D, BITS, 2>(sp, o, x, m_run, l_run, vb_run, lane);                           \
         __builtin_amdgcn_s_waitcnt(0xC07F);                    /* lgkmcnt(0): slot reads done */    \
         issue_page<D, BITS>(SA, nx < pairs, __builtin_amdgcn_readfirstlane(id2.x), head_base, bs, voff);  \
         issue_page<D, BITS>(SB, 2 * nx + 1 < wn, __builtin_amdgcn_readfirstlane(id2.y), head_base, bs, voff); \
@@ -553,28 +780,36 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
         if (w == ow) {
             float x[1][8];
 #pragma unroll
-            for (int jj = 0; jj < 8; ++jj) x[0][jj] = sc[r16 * PAGE + tok(q, jj)];
+            for (int jj = 0; jj < 8; ++jj)
+                x[0][jj] = ST == 2 && r16 >= 8 ? -__builtin_inff() : sc[r16 * PAGE + tok(q, jj)];
             KUSH_WAIT_VM(0);
-            const uint8_t* const sp[1] = {tslot};
-            consume_pages<D, BITS, 1>(sp, o, x, m_run, l_run, vb_run, lane);
+            if constexpr (ST == 2) {                             // stream 0 takes the page
+                consume2<D, BITS>(tslot, 0, o, vacc, x[0], 1.0f, 0.0f, m_run, l_run, vb_run, lane);
+            } else {
+                const uint8_t* const sp[1] = {tslot};
+                const float b0[1] = {0.0f};
+                consume_pages<D, BITS, 1>(sp, o, vacc, x, 1.0f, b0, m_run, l_run, vb_run, lane);
+            }
         }
     }
 
-    // Merge the waves. Every wave rescales its O to the workgroup max and stores it in the idle rings
-    // (region of wave ww: 16 D floats, dims d as [d / 4][head][d % 4], one 16-byte store per lane and
-    // tile); after one barrier, wave w sums tiles w, w + NW, ... over the waves and writes them out.
+    // Merge the waves (and, ST = 2, the two streams of a head: columns c and c ^ 8). Every wave
+    // rescales its O to the workgroup max of its head and stores it in the idle rings (region of wave
+    // ww: 16 D floats, dims d as [d / 4][column][d % 4], one 16-byte store per lane and tile); after
+    // one barrier, wave w sums tiles w, w + NW, ... over the waves and writes them out.
     constexpr int OBYTES = 16 * D * 4;
     static_assert(NW * OBYTES <= 2 * NW * R::SLOT, "the merge needs 16 D floats per wave in the first array");
     l_run = rows_sum(l_run);
-    vb_run = rows_sum(vb_run);
+    vb_run = __builtin_fmaf(vacc[0], TWO24, rows_sum(vb_run));   // every row of vacc holds the head's sum
     if (q == 0) {
         m_l[w * 16 + r16] = m_run;
         l_l[w * 16 + r16] = l_run;
     }
     __syncthreads();                                             // rings idle, m_l / l_l complete
+    const int rx = ST == 2 ? (r16 ^ 8) : r16;                    // the other stream's column of this head
     float M = -__builtin_inff();
 #pragma unroll
-    for (int ww = 0; ww < NW; ++ww) M = __builtin_fmaxf(M, m_l[ww * 16 + r16]);
+    for (int ww = 0; ww < NW; ++ww) M = __builtin_fmaxf(M, __builtin_fmaxf(m_l[ww * 16 + r16], m_l[ww * 16 + rx]));
     {
         const float f = m_run == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m_run - M);
         uint8_t* reg = ringA + w * OBYTES;
@@ -582,7 +817,7 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
         for (int dt = 0; dt < DT; ++dt) {
             f4 v;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] = __builtin_fmaf(o[dt][i], TWO24, vb_run) * f;
+            for (int i = 0; i < 4; ++i) v[i] = __builtin_fmaf(o[dt][i], dt < NLO ? TWO24 : TWO20, vb_run) * f;
             *reinterpret_cast<f4*>(reg + (((4 * dt + q) * 16 + r16) * 4) * 4) = v;
         }
     }
@@ -592,6 +827,10 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
         for (int ww = 0; ww < NW; ++ww) {
             const float mw = m_l[ww * 16 + r16];
             if (mw > -__builtin_inff()) L += l_l[ww * 16 + r16] * __builtin_amdgcn_exp2f(mw - M);
+            if constexpr (ST == 2) {
+                const float mx = m_l[ww * 16 + rx];
+                if (mx > -__builtin_inff()) L += l_l[ww * 16 + rx] * __builtin_amdgcn_exp2f(mx - M);
+            }
         }
     }
     __syncthreads();
@@ -603,6 +842,7 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
         for (int ww = 0; ww < NW; ++ww) {
             const uint8_t* reg = ringA + ww * OBYTES;
             acc += *reinterpret_cast<const f4*>(reg + (((4 * dt + q) * 16 + r16) * 4) * 4);
+            if constexpr (ST == 2) acc += *reinterpret_cast<const f4*>(reg + (((4 * dt + q) * 16 + rx) * 4) * 4);
         }
         if (r16 < Gc) {
             const int d0 = 16 * dt + 4 * q;
@@ -685,11 +925,13 @@ __global__ __launch_bounds__(256) void combine_kernel(IN* __restrict__ out, cons
 template <int D, int BITS, typename IN, int NW>
 static int launch_decode(dim3 grid, hipStream_t stream, const void* q, void* out, const void* cache, int64_t bs,
                          int64_t hs, const void* tail_k, const int32_t* tail_idx, const int32_t* block_table,
-                         const int32_t* seq_lens, int64_t bt_stride, int hkv, int group, float sm_log2, int n_splits,
+                         const int32_t* seq_lens, int64_t bt_stride, int hkv, int group, float p2, float rs, int n_splits,
                          float* part_ml, float* part_o, int32_t* sync) {
-    decode_kernel<D, BITS, IN, NW><<<grid, dim3(NW * WAVE), 0, stream>>>(
+    // two page streams whenever the heads of a kv head fit in half the MFMA columns
+    auto kern = group <= 8 ? decode_kernel<D, BITS, IN, NW, 2> : decode_kernel<D, BITS, IN, NW, 1>;
+    kern<<<grid, dim3(NW * WAVE), 0, stream>>>(
         (const IN*)q, (IN*)out, (const uint8_t*)cache, bs, hs, (const IN*)tail_k, tail_idx, block_table, seq_lens,
-        bt_stride, hkv, group, sm_log2, n_splits, part_ml, part_o, sync);
+        bt_stride, hkv, group, p2, rs, n_splits, part_ml, part_o, sync);
     return kush_check_launch("kush_decode");
 }
 
@@ -714,7 +956,19 @@ extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const v
     if (waves != 2 && waves != 4 && waves != 8) return kush_fail(-2, "kush_decode: waves must be 0, 2, 4 or 8");
     const int n_gc = (group + 15) / 16;
     if ((int64_t)n_splits * n_gc > 65535) return kush_fail(-2, "kush_decode: n_splits %d too large", n_splits);
+    // scores in log2 units: scale log2 e = p2 rs with p2 a signed power of two (q p2 is exact in fp16
+    // for bf16 / fp16 q) and rs in [2^-0.5, 2^0.5] (a zero scale becomes 2^-120: x ~ 0, masks stay -inf)
     const float sm_log2 = (float)((double)scale * 1.4426950408889634);
+    float p2 = 1.0f, rs = 0x1p-120f;
+    if (!std::isfinite(sm_log2)) {
+        rs = sm_log2;
+    } else if (sm_log2 != 0.0f) {
+        int e2 = 0;
+        const float m = std::frexp(std::fabs(sm_log2), &e2);          // |sm_log2| = m 2^e2, m in [0.5, 1)
+        if (m < 0.70710678f) --e2;
+        p2 = std::copysign(std::ldexp(1.0f, e2), sm_log2);
+        rs = sm_log2 / p2;
+    }
     const dim3 grid(n_seqs, hkv, n_splits * n_gc);
     hipStream_t st = (hipStream_t)stream;
     return dispatch_shape(head_dim, bits, dtype, "kush_decode", [&](auto dd, auto bb, auto in) -> int {
@@ -722,7 +976,7 @@ extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const v
         using IN = decltype(in);
         if (n_seqs == 0) return 0;
 #define KUSH_DECODE_ARGS grid, st, q, out, cache, block_stride, head_stride, tail_k, tail_idx, block_table, seq_lens, \
-                         bt_stride, hkv, group, sm_log2, n_splits, part_ml, part_o, split_sync
+                         bt_stride, hkv, group, p2, rs, n_splits, part_ml, part_o, split_sync
         // the largest of the requested, 4 and 2 waves whose rings fit in LDS
         if (waves >= 8) {
             if constexpr (decode_fits<D, BITS, 8>()) return launch_decode<D, BITS, IN, 8>(KUSH_DECODE_ARGS);
