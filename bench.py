@@ -17,6 +17,16 @@ cache.
 Prints one JSON line (the driver's contract) with "roofline" (decode kernel: algorithmic bytes /
 its mean duration, from HIP events around the graph of decode kernels) and
 "cpu_baseline" (the C restatement of the reference CPU path, oracle/, on the host cores).
+
+--config selects the other measured configurations of the path (each prints its own JSON line; the
+default, c2, is the headline):
+  c3        Llama-3.1-8B decode step, 32 q / 8 kv heads, D 128, int8, batch 128 with ragged contexts
+            N_i ~ U[256, 8192] (seed 0): append of one token per sequence (pos_offset -1, the vLLM
+            convention) then decode over N_i + 1 tokens
+  c4        Qwen3-8B decode, 32 q / 8 kv heads, D 128, int4, batch 8 x 131,072 tokens (K bias sigma 4 on
+            5% of channels), split-K by the Ops.splits policy (--sweep adds NS 64, 128, 256 ...)
+  c4-write  the chunked-prefill write of 2,048 new tokens per sequence of that layer (8 x 2,048 tokens,
+            two ordered launches), quantize-and-pack bytes read + written
 """
 from __future__ import annotations
 
@@ -58,6 +68,8 @@ def parse_args(argv=None):
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="instead of the decode, run --steps device-to-device copies of MIB MiB: the plain copy "
                          "kernel of known size that scales rocprofv3's FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--config", default="c2", choices=("c2", "c3", "c4", "c4-write"),
+                    help="which configuration to measure (c2: the headline line)")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "decode_c2_traffic.md"),
                     help="rocprofv3 counter summary whose 'traffic_bytes_per_launch' fills roofline.traffic")
     return ap.parse_args(argv)
@@ -246,6 +258,198 @@ def copy_calibration(a) -> None:
                       "us_per_copy": round(dt * 1e6, 2), "GB/s": round(2 * n / dt / 1e9, 1)}), flush=True)
 
 
+# ---------------------------------------------------------------- other configurations (C3, C4)
+def time_graph(step, steps: int, warmup: int) -> float:
+    """Mean ms per call of step(i): `warmup` calls in a graph of their own, then exactly `steps`
+    calls captured in one graph, replayed once between HIP events on the replay stream."""
+    def capture(n):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                step(i)
+        torch.cuda.synchronize()
+        return g
+    for i in range(2):                       # eager calls first (lazy init outside the capture)
+        step(i)
+    torch.cuda.synchronize()
+    if warmup:
+        gw = capture(warmup)
+        gw.replay()
+        torch.cuda.synchronize()
+        del gw
+    g = capture(steps)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def ragged_cache(ops, lens, room: int, Hkv: int, bias_sigma: float, bias_frac: float, gen, dev):
+    """One pool of records for sequences of lens[i] tokens (pages for lens[i] + room), written by the
+    product's write kernel from seeded K = N(0,1) + per-channel bias (sigma bias_sigma on a seeded
+    bias_frac of the channels of each kv head) and V = N(0,1); pages placed by a seeded permutation."""
+    from kushkash_amd._ops import record_bytes
+    D, bits, dtype = ops.D, ops.bits, ops.dtype
+    B = len(lens)
+    pages = [-(-(n + room) // PAGE) for n in lens]
+    total, maxp = sum(pages), max(pages)
+    cache = torch.zeros(total, Hkv, record_bytes(D, bits), dtype=torch.uint8, device=dev)
+    perm = torch.randperm(total, generator=gen, device=dev).to(torch.int32)
+    table = torch.zeros(B, maxp, dtype=torch.int32, device=dev)
+    off = 0
+    for i, p in enumerate(pages):
+        table[i, :p] = perm[off:off + p]
+        off += p
+    tail_k = torch.zeros(B, Hkv, PAGE, D, dtype=dtype, device=dev)
+    tail_idx = torch.arange(B, dtype=torch.int32, device=dev)
+    seq_lens = torch.tensor(lens, dtype=torch.int32, device=dev)
+    n_bias = max(1, round(bias_frac * D))
+    bias = torch.zeros(Hkv, D, device=dev)
+    for h in range(Hkv):
+        ch = torch.randperm(D, generator=gen, device=dev)[:n_bias]
+        bias[h, ch] = bias_sigma * torch.randn(n_bias, generator=gen, device=dev)
+    s0 = 0
+    while s0 < B:                            # ~2^27 K elements per write call
+        s1, n_tok = s0, 0
+        while s1 < B and (s1 == s0 or n_tok + lens[s1] <= (1 << 27) // (Hkv * D)):
+            n_tok += lens[s1]
+            s1 += 1
+        k = (torch.randn(n_tok, Hkv, D, generator=gen, device=dev) + bias).to(dtype)
+        v = torch.randn(n_tok, Hkv, D, generator=gen, device=dev).to(dtype)
+        ln = lens[s0:s1]
+        qsl = torch.tensor([0] + list(torch.tensor(ln).cumsum(0)), dtype=torch.int32, device=dev)
+        js = torch.cat([torch.full((-(-n // PAGE),), i, dtype=torch.int32) for i, n in enumerate(ln)]).to(dev)
+        jp = torch.cat([torch.arange(-(-n // PAGE), dtype=torch.int32) for n in ln]).to(dev)
+        ops.write(k, v, qsl, seq_lens[s0:s1], tail_idx[s0:s1], js, jp, cache, table[s0:s1].contiguous(), tail_k)
+        del k, v
+        s0 = s1
+    torch.cuda.synchronize()
+    return cache, table, tail_k, tail_idx
+
+
+def _line(metric, us, alg, config, kernels, extra=None):
+    gbs = alg / (us * 1e-6) / 1e9
+    res = {"metric": metric, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "us_per_step": round(us, 2),
+           "pct_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "data": "synthetic (seeded, generated on the GPU)", "config": config,
+           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                        "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "kernel": kernels,
+                        "algorithmic_bytes": int(alg)}}
+    if extra:
+        res.update(extra)
+    print(json.dumps(res), flush=True)
+
+
+def bench_c3(a) -> None:
+    """C3: Llama-3.1-8B, int8, batch 128, ragged N_i ~ U[256, 8192]; one step = append + decode."""
+    from kushkash_amd._ops import Ops, record_bytes
+    dev = "cuda:0"
+    B, Hq, Hkv, D, bits = 128, 32, 8, 128, 8
+    G, dtype = Hq // Hkv, torch.bfloat16
+    lens = torch.randint(256, 8193, (B,), generator=torch.Generator().manual_seed(0)).tolist()
+    ops = Ops(torch.device(dev), D, bits, G, dtype)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    cache, table, tail_k, tail_idx = ragged_cache(ops, lens, 1, Hkv, 6.0, 0.10, gen, dev)
+    k_new = torch.randn(B, Hkv, D, generator=gen, device=dev).to(dtype)
+    v_new = torch.randn(B, Hkv, D, generator=gen, device=dev).to(dtype)
+    q = torch.randn(B, Hq, D, generator=gen, device=dev).to(dtype)
+    out = torch.empty_like(q)
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev) + 1        # counts the appended token
+    ns = a.splits or ops.splits(B, Hkv, max(n + 1 for n in lens) // PAGE)
+    work = torch.empty(max(1, B * Hkv * ns * G * (D + 2)), dtype=torch.float32, device=dev)
+    sm = 1.0 / math.sqrt(D)
+
+    def step(i):
+        ops.append(k_new, v_new, sl, tail_idx, cache, table, tail_k, pos_offset=-1, advance=False)
+        ops.decode(q, out, cache, table, sl, tail_idx, tail_k, sm, ns, work)
+
+    ms = time_graph(step, a.steps, a.warmup)
+    RB, DC = record_bytes(D, bits), (D if bits == 8 else D // 2)
+    n1 = [n + 1 for n in lens]
+    dec = sum((n // PAGE) * Hkv * RB + (n % PAGE) * Hkv * (2 * D + DC + 4) for n in n1)
+    qo = 2 * B * Hq * D * 2
+    app = B * Hkv * (2 * 2 * D + DC + 4 + 2 * D)                         # k, v rows in; V row, K tail row out
+    app += sum(Hkv * ((PAGE - 1) * 2 * D + PAGE * DC + 4 * D) for n in lens if n % PAGE == PAGE - 1)
+    alg = dec + qo + app + B * 4 * (table.shape[1] + 2)
+    _line("append + decode us/step + achieved HBM GB/s (% peak), int8, bs128 ragged U[256, 8192]", ms * 1e3, alg,
+          {"workload": f"C3 Llama-3.1-8B layer: {Hq} q / {Hkv} kv heads, D {D}, int{bits}, page 32, batch {B}, "
+                       f"N_i ~ U[256, 8192] (seed 0; sum {sum(lens)} tokens), append (pos_offset -1) + decode",
+           "global_batch": B, "split_k": ns, "tokens": sum(n1)},
+          f"append_kernel<{D},{bits},bf16> + decode_kernel<{D},{bits},bf16,4>")
+
+
+def bench_c4(a) -> None:
+    """C4 decode: Qwen3-8B, int4, batch 8 x 131,072 tokens, split-K."""
+    from kushkash_amd._ops import Ops, record_bytes
+    dev = "cuda:0"
+    B, Hq, Hkv, D, bits, N = 8, 32, 8, 128, 4, 131072
+    G, dtype = Hq // Hkv, torch.bfloat16
+    ops = Ops(torch.device(dev), D, bits, G, dtype)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    cache, table, tail_k, tail_idx = ragged_cache(ops, [N] * B, 0, Hkv, 4.0, 0.05, gen, dev)
+    q = torch.randn(B, Hq, D, generator=gen, device=dev).to(dtype)
+    out = torch.empty_like(q)
+    sl = torch.full((B,), N, dtype=torch.int32, device=dev)
+    sm = 1.0 / math.sqrt(D)
+    alg = B * Hkv * (N // PAGE) * record_bytes(D, bits) + 2 * B * Hq * D * 2 + B * 4 * (N // PAGE + 1)
+    policy = ops.splits(B, Hkv, N // PAGE)
+    nss = [a.splits or policy] + [int(x) for x in a.sweep.split(",") if x.strip() and ":" not in x]
+    for i, ns in enumerate(nss):
+        work = torch.empty(B * Hkv * ns * G * (D + 2), dtype=torch.float32, device=dev)
+        ms = time_graph(lambda j: ops.decode(q, out, cache, table, sl, tail_idx, tail_k, sm, ns, work),
+                        a.steps, a.warmup)
+        if i == 0:
+            _line("decode-attn us/step + achieved HBM GB/s (% peak), int4, bs8 x 131k ctx", ms * 1e3, alg,
+                  {"workload": f"C4 Qwen3-8B layer: {Hq} q / {Hkv} kv heads, D {D}, int{bits}, page 32, "
+                               f"batch {B} x {N} tokens", "global_batch": B, "seq_len": N, "split_k": ns},
+                  f"decode_kernel<{D},{bits},bf16,8> (split-K merged in the launch)")
+        else:
+            print(f"C4 splits {ns:4d}: {ms * 1e3:8.2f} us/step  {alg / ms / 1e6:7.1f} GB/s "
+                  f"({100 * alg / ms / 1e6 / PEAK_HBM_GBS:5.1f}% of peak)", file=sys.stderr, flush=True)
+
+
+def bench_c4_write(a) -> None:
+    """C4 chunked-prefill write: 2,048 new tokens for each of 8 sequences (fresh pages), 4 rotated
+    input / record sets (344 MB) so that the step reads and writes HBM, not the Infinity Cache."""
+    from kushkash_amd._ops import Ops, record_bytes
+    dev = "cuda:0"
+    B, Hq, Hkv, D, bits, T, P = 8, 32, 8, 128, 4, 2048, 4
+    G, dtype = Hq // Hkv, torch.bfloat16
+    ops = Ops(torch.device(dev), D, bits, G, dtype)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    pages = T // PAGE
+    RB = record_bytes(D, bits)
+    sets = []
+    for p in range(P):
+        cache = torch.zeros(B * pages, Hkv, RB, dtype=torch.uint8, device=dev)
+        table = torch.randperm(B * pages, generator=gen, device=dev).to(torch.int32).view(B, pages).contiguous()
+        k = torch.randn(B * T, Hkv, D, generator=gen, device=dev).to(dtype)
+        v = torch.randn(B * T, Hkv, D, generator=gen, device=dev).to(dtype)
+        sets.append((k, v, cache, table))
+    tail_k = torch.zeros(B, Hkv, PAGE, D, dtype=dtype, device=dev)
+    tail_idx = torch.arange(B, dtype=torch.int32, device=dev)
+    sl = torch.full((B,), T, dtype=torch.int32, device=dev)
+    qsl = torch.arange(B + 1, dtype=torch.int32, device=dev) * T
+    js = torch.arange(B, dtype=torch.int32, device=dev).repeat_interleave(pages)
+    jp = torch.arange(pages, dtype=torch.int32, device=dev).repeat(B)
+
+    def step(i):
+        k, v, cache, table = sets[i % P]
+        ops.write(k, v, qsl, sl, tail_idx, js, jp, cache, table, tail_k)
+
+    ms = time_graph(step, a.steps, a.warmup)
+    alg = 2 * B * T * Hkv * D * 2 + B * pages * Hkv * RB
+    _line("chunked-prefill write us/step + achieved HBM GB/s (% peak), int4, 8 x 2048 tokens", ms * 1e3, alg,
+          {"workload": f"C4 write: {B} x {T} new tokens, {Hkv} kv heads, D {D}, int{bits} (512 page jobs x {Hkv} "
+                       f"heads, two launches)", "global_batch": B, "tokens": B * T},
+          f"write_kernel<{D},{bits},bf16> x 2 (mode 0, mode 1)")
+
+
 def main(argv=None):
     a = parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -257,6 +461,9 @@ def main(argv=None):
     dev = "cuda:0"
     if a.calibrate_copy:
         copy_calibration(a)
+        return
+    if a.config != "c2":
+        {"c3": bench_c3, "c4": bench_c4, "c4-write": bench_c4_write}[a.config](a)
         return
     w = make_workload(a, dev)
     ns = a.splits or w["ops"].splits(w["B"], w["Hkv"], w["N"] // PAGE)

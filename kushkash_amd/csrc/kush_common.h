@@ -39,11 +39,42 @@ struct Fmt {
     static_assert(REC % 16 == 0, "records must stay 16-byte aligned");
 };
 
+// ------------------------------------------------------------------ vector types
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+
 // ------------------------------------------------------------------ input element types
 // The kernels take q, k, v, out and the exact K tail in one of three dtypes.
 struct bf16_t {
     uint16_t u;
 };
+
+// 8 consecutive elements as fp32: one or two 16-byte loads (p 16-byte aligned)
+__device__ __forceinline__ void load8(const float* p, float (&x)[8]) {
+    const f4 a = *reinterpret_cast<const f4*>(p), b = *reinterpret_cast<const f4*>(p + 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        x[j] = a[j];
+        x[j + 4] = b[j];
+    }
+}
+
+__device__ __forceinline__ void load8(const _Float16* p, float (&x)[8]) {
+    const h8 v = *reinterpret_cast<const h8*>(p);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = (float)v[j];
+}
+
+__device__ __forceinline__ void load8(const bf16_t* p, float (&x)[8]) {
+    const u4 v = *reinterpret_cast<const u4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        x[2 * i] = __uint_as_float(v[i] << 16);
+        x[2 * i + 1] = __uint_as_float(v[i] & 0xFFFF0000u);
+    }
+}
 
 __device__ __forceinline__ float to_f32(float x) { return x; }
 __device__ __forceinline__ float to_f32(_Float16 x) { return (float)x; }

@@ -31,12 +31,8 @@
 
 namespace kush {
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef float f4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
 constexpr float LOG2E = 1.4426950408889634f;
 
@@ -54,31 +50,6 @@ __device__ __forceinline__ int kdim(int kk, int q, int j) {
         return (kk & 1) * (D / 2) + q * (D / 8) + 8 * (kk >> 1) + j;
     else
         return q * (D / 4) + 8 * kk + j;
-}
-
-// 8 consecutive elements as fp32, one or two 16-byte loads (p 16-byte aligned)
-__device__ __forceinline__ void load8(const float* p, float (&x)[8]) {
-    const f4 a = *reinterpret_cast<const f4*>(p), b = *reinterpret_cast<const f4*>(p + 4);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        x[j] = a[j];
-        x[j + 4] = b[j];
-    }
-}
-
-__device__ __forceinline__ void load8(const _Float16* p, float (&x)[8]) {
-    const h8 v = *reinterpret_cast<const h8*>(p);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] = (float)v[j];
-}
-
-__device__ __forceinline__ void load8(const bf16_t* p, float (&x)[8]) {
-    const u4 v = *reinterpret_cast<const u4*>(p);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        x[2 * i] = __uint_as_float(v[i] << 16);
-        x[2 * i + 1] = __uint_as_float(v[i] & 0xFFFF0000u);
-    }
 }
 
 // Token of slot j of lane group q in the PV contraction: the token the QK^T accumulators of lane
@@ -545,7 +516,7 @@ __device__ __forceinline__ void consume2(const uint8_t* s0, int ds, f4 (&o)[D / 
 }
 
 // Pages per window of the page loop: the block ids of a window sit in an LDS table.
-constexpr int WIN = 2048;
+constexpr int WIN = 1024;
 
 // Static LDS of one decode workgroup: two arrays, each holding one page pair per wave (wave w at
 // 2 w SLOT), the window's block-id table and the pair counter. After the page loop the idle arrays
@@ -567,6 +538,15 @@ template <int D>
 struct AfterLoop {
     static constexpr int Q_OFF = 0, SC_OFF = 16 * D * 4, ML_OFF = SC_OFF + 16 * PAGE * 4;
 };
+
+// Split-K partials cross XCDs (separate L2s): stored write-through and read past the local L2, as
+// relaxed device-scope atomics (global_store / global_load with sc1).
+__device__ __forceinline__ void publish(float* p, float x) {
+    __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float fetch(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // grid (S, Hkv, n_splits * ceil(G / 16)), block NW * 64. ST = 2 (G <= 8): two page streams share the
 // MFMA columns (page A of each pair in columns 0-7, page B in 8-15); ST = 1: one page's 16 heads.
@@ -850,25 +830,28 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
 #pragma unroll
                 for (int i = 0; i < 4; ++i) out[qbase + r16 * D + d0 + i] = from_f32<IN>(acc[i] * inv_l);
             } else {
-                *reinterpret_cast<f4*>(part_o + pb * D + d0) = acc;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) publish(part_o + pb * D + d0 + i, acc[i]);
             }
         }
     }
     if (NS > 1 && w == 0 && q == 0 && r16 < Gc) {
-        part_ml[2 * pb] = M;
-        part_ml[2 * pb + 1] = L;
+        publish(part_ml + 2 * pb, M);
+        publish(part_ml + 2 * pb + 1, L);
     }
     if (NS == 1 || sync == nullptr) return;
 
     // split-K: the last workgroup of this (sequence, kv head, head chunk) merges every split. The
-    // barrier completes every wave's partial stores; one agent-scope release (L2 writeback) by thread
-    // 0 then publishes them before the counter moves, and the last workgroup's thread 0 acquires
-    // (L2 invalidate) before its waves read the other splits.
+    // partials went out as write-through stores (publish); once every wave has seen them complete
+    // (vmcnt 0, then the barrier), thread 0 counts the split in at the device's coherence point, and
+    // the last workgroup reads the other splits' partials past its own XCD's L2 (fetch). No L2-wide
+    // write-back or invalidate, which would stall every other workgroup streaming on the XCD.
+    KUSH_WAIT_VM(0);
     __syncthreads();
     if (threadIdx.x == 0) {
         const int n_gc = gridDim.z / NS;
         int32_t* ctr = sync + ((int64_t)s * H + h) * n_gc + gc;
-        const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         *last_flag = prev == NS - 1;
         if (prev == NS - 1) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -878,16 +861,16 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     for (int i = threadIdx.x; i < Gc * D; i += NW * WAVE) {
         const int g = g0 + i / D, d = i % D;
         float Mg = -__builtin_inff();
-        for (int zz = 0; zz < NS; ++zz) Mg = __builtin_fmaxf(Mg, part_ml[2 * ((base + zz) * G + g)]);
+        for (int zz = 0; zz < NS; ++zz) Mg = __builtin_fmaxf(Mg, fetch(part_ml + 2 * ((base + zz) * G + g)));
         float L = 0.0f, acc = 0.0f;
         if (Mg > -__builtin_inff()) {
             for (int zz = 0; zz < NS; ++zz) {
                 const int64_t pb = (base + zz) * G + g;
-                const float mz = part_ml[2 * pb];
+                const float mz = fetch(part_ml + 2 * pb);
                 if (mz > -__builtin_inff()) {
                     const float fz = __builtin_amdgcn_exp2f(mz - Mg);
-                    L += part_ml[2 * pb + 1] * fz;
-                    acc += fz * part_o[pb * D + d];
+                    L += fetch(part_ml + 2 * pb + 1) * fz;
+                    acc += fz * fetch(part_o + pb * D + d);
                 }
             }
         }

@@ -3,131 +3,240 @@
 // kushkash/_ops.py:66-101 (launch), arithmetic kushkash/kush/quant.mojo:25-50. Pages are
 // bit-identical to the reference CPU path (kushkash/kush/cpu.mojo:173-304).
 //
-// Work split on CDNA4 (wave64): a V token row is one wave (per-token range: wave min/max
-// reduction, then each lane packs the bytes of its dims); a K page is one workgroup that stages
-// the page's 32 x D values in LDS as fp32, reduces one channel per thread, and packs the codes
-// with consecutive lanes writing consecutive bytes.
+// Work split on CDNA4: one workgroup of 256 threads per (page, kv head). Thread t owns row
+// t / CG of the page (CG = D / 16 threads per row; D = 256 takes two passes) and the 16 dims
+// [8c, 8c + 8) and [D/2 + 8c, D/2 + 8c + 8), c = t % CG: exactly the dims whose codes make
+// bytes [8c, 8c + 8) of an int4 row (low nibble dim j, high nibble dim j + D/2), so rows are
+// loaded with 16-byte loads and stored with 8-byte stores, both coalesced. A V row's range is
+// reduced over the CG lanes of its row (xor shuffles); a K channel's range over the 32 rows goes
+// through an fp32 tile in LDS, one channel per thread.
 #include "kush_common.h"
 
 namespace kush {
 
 constexpr int WRITE_THREADS = 256;
 
-// V token row src[0:D] -> row t of a record (its final encoding: per-token range).
-template <int D, int BITS, typename IN>
-__device__ __forceinline__ void quantize_v_row(const IN* __restrict__ src, uint8_t* __restrict__ rec, int t, int lane) {
-    using F = Fmt<D, BITS>;
-    constexpr int R = D / WAVE;            // values per lane: 1, 2 or 4
-    float x[R];
-    float mn = __builtin_inff(), mx = -__builtin_inff();
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        x[r] = to_f32(src[lane + WAVE * r]);
-        mn = __builtin_fminf(mn, x[r]);
-        mx = __builtin_fmaxf(mx, x[r]);
-    }
-    mn = wave_min(mn);
-    mx = wave_max(mx);
-    float s, b, inv;
-    qparams<BITS>(mn, mx, s, b, inv);
-    if (lane == 0) {
-        reinterpret_cast<uint16_t*>(rec + F::OFF_VS)[t] = f16_bits(s);
-        reinterpret_cast<uint16_t*>(rec + F::OFF_VB)[t] = f16_bits(b);
-    }
-    uint8_t* dst = rec + F::OFF_VQ + t * F::DC;
-    if constexpr (BITS == 8) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) dst[lane + WAVE * r] = (uint8_t)qcode<8>(x[r], b, inv);
-    } else if constexpr (D == 64) {
-        // byte j < 32 pairs dim j (this lane) with dim j + 32 (lane j + 32)
-        float hi = __shfl_down(x[0], 32, WAVE);
-        if (lane < 32) dst[lane] = pack4(qcode<4>(x[0], b, inv), qcode<4>(hi, b, inv));
+template <int D>
+struct Rows {
+    static constexpr int CG = D / 16;                        // threads per row
+    static constexpr int RP = WRITE_THREADS / CG;            // rows per pass
+    static constexpr int PASSES = RP >= PAGE ? 1 : PAGE / RP;
+};
+
+// 8 consecutive elements as fp32: 16-byte loads when the rows are 16-byte aligned, else per element
+template <bool VEC, typename IN>
+__device__ __forceinline__ void get8(const IN* p, float (&x)[8]) {
+    if constexpr (VEC) {
+        load8(p, x);
     } else {
-        // byte j = lane + 64 r pairs dim j with dim j + D/2 = lane + 64 (r + R/2): same lane
 #pragma unroll
-        for (int r = 0; r < R / 2; ++r)
-            dst[lane + WAVE * r] = pack4(qcode<4>(x[r], b, inv), qcode<4>(x[r + R / 2], b, inv));
+        for (int j = 0; j < 8; ++j) x[j] = to_f32(p[j]);
     }
 }
 
-// K of one page by a workgroup: per-channel range over its 32 rows. Row t < split comes from
-// ka + t*sa (the exact tail), the rest from kb_src + (t - split)*skb (new rows). tile holds
-// PAGE*D + 2*D floats of LDS.
-template <int D, int BITS, typename IN, int NT>
-__device__ __forceinline__ void quantize_k_page(const IN* __restrict__ ka, int64_t sa, const IN* __restrict__ kb_src,
-                                                int64_t skb, int split, uint8_t* __restrict__ rec, float* tile) {
+template <bool VEC, typename IN>
+__device__ __forceinline__ void copy8(IN* dst, const IN* src) {
+    if constexpr (VEC && sizeof(IN) == 2) {
+        *reinterpret_cast<u4*>(dst) = *reinterpret_cast<const u4*>(src);
+    } else if constexpr (VEC) {
+        reinterpret_cast<u4*>(dst)[0] = reinterpret_cast<const u4*>(src)[0];
+        reinterpret_cast<u4*>(dst)[1] = reinterpret_cast<const u4*>(src)[1];
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dst[j] = src[j];
+    }
+}
+
+// codes of the 16 values of a thread (x[0..8): dims 8c.., x[8..16): dims D/2 + 8c..) -> the bytes
+// they make: int4 byte i = code(x[i]) | code(x[8 + i]) << 4 (row bytes 8c + i, in lo); int8 bytes in
+// dim order (row bytes 8c + i in lo, D/2 + 8c + i in hi)
+#pragma clang fp contract(off)
+template <int BITS>
+__device__ __forceinline__ void pack16(const float (&x)[16], const float (&b)[16], const float (&inv)[16], u2& lo,
+                                       u2& hi) {
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t c0 = (uint32_t)qcode<BITS>(x[i], b[i], inv[i]);
+        const uint32_t c1 = (uint32_t)qcode<BITS>(x[8 + i], b[8 + i], inv[8 + i]);
+        if constexpr (BITS == 4) {
+            w[i / 4] |= ((c0 & 0xFu) | ((c1 & 0xFu) << 4)) << (8 * (i % 4));
+        } else {
+            w[i / 4] |= (c0 & 0xFFu) << (8 * (i % 4));
+            w[2 + i / 4] |= (c1 & 0xFFu) << (8 * (i % 4));
+        }
+    }
+    lo = u2{w[0], w[1]};
+    hi = u2{w[2], w[3]};
+}
+#pragma clang fp contract(on)
+
+// One (page, kv head) by the workgroup: V rows [vlo, vhi) of the page (row t from
+// v_new + (t - vlo) * v_stride) and, when do_k, the K page: rows t < split from k_tail (stride D),
+// the others from k_new + (t - split) * k_stride. rec: the page's record. tile: LDS of
+// PAGE * D + 2 * D floats. Every thread of the workgroup calls this (it has barriers when do_k).
+template <int D, int BITS, typename IN, bool VEC>
+__device__ __forceinline__ void page_task(const IN* __restrict__ k_tail, const IN* __restrict__ k_new, int64_t k_stride,
+                                          int split, bool do_k, const IN* __restrict__ v_new, int64_t v_stride,
+                                          int vlo, int vhi, uint8_t* __restrict__ rec, float* tile) {
     using F = Fmt<D, BITS>;
+    using RW = Rows<D>;
+    constexpr int CG = RW::CG;
+    const int t = threadIdx.x, c = t % CG, r0 = t / CG;
+    float kx[RW::PASSES][16];
+#pragma unroll
+    for (int pp = 0; pp < RW::PASSES; ++pp) {
+        const int r = r0 + pp * RW::RP;
+        if (do_k && r < PAGE) {
+            const IN* row = r < split ? k_tail + r * D : k_new + (int64_t)(r - split) * k_stride;
+            float a[8], b[8];
+            get8<VEC>(row + 8 * c, a);
+            get8<VEC>(row + D / 2 + 8 * c, b);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                kx[pp][j] = a[j];
+                kx[pp][8 + j] = b[j];
+            }
+            float* tr = tile + r * D;
+            *reinterpret_cast<f4*>(tr + 8 * c) = f4{a[0], a[1], a[2], a[3]};
+            *reinterpret_cast<f4*>(tr + 8 * c + 4) = f4{a[4], a[5], a[6], a[7]};
+            *reinterpret_cast<f4*>(tr + D / 2 + 8 * c) = f4{b[0], b[1], b[2], b[3]};
+            *reinterpret_cast<f4*>(tr + D / 2 + 8 * c + 4) = f4{b[4], b[5], b[6], b[7]};
+        }
+        // V row r (its final encoding: per-token range over the CG threads of the row, which are
+        // consecutive lanes of one wave)
+        const bool vrow = r >= vlo && r < vhi && r < PAGE;
+        float x[16];
+        float mn = __builtin_inff(), mx = -__builtin_inff();
+        if (vrow) {
+            const IN* row = v_new + (int64_t)(r - vlo) * v_stride;
+            float a[8], b[8];
+            get8<VEC>(row + 8 * c, a);
+            get8<VEC>(row + D / 2 + 8 * c, b);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                x[j] = a[j];
+                x[8 + j] = b[j];
+                mn = __builtin_fminf(mn, __builtin_fminf(a[j], b[j]));
+                mx = __builtin_fmaxf(mx, __builtin_fmaxf(a[j], b[j]));
+            }
+        }
+#pragma unroll
+        for (int o = 1; o < CG; o <<= 1) {
+            mn = __builtin_fminf(mn, __shfl_xor(mn, o, WAVE));
+            mx = __builtin_fmaxf(mx, __shfl_xor(mx, o, WAVE));
+        }
+        if (vrow) {
+            float s, b, inv;
+            qparams<BITS>(mn, mx, s, b, inv);
+            float bb[16], ii[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                bb[j] = b;
+                ii[j] = inv;
+            }
+            u2 lo, hi;
+            pack16<BITS>(x, bb, ii, lo, hi);
+            uint8_t* dst = rec + F::OFF_VQ + r * F::DC + 8 * c;
+            *reinterpret_cast<u2*>(dst) = lo;
+            if constexpr (BITS == 8) *reinterpret_cast<u2*>(dst + D / 2) = hi;
+            if (c == 0) {
+                reinterpret_cast<uint16_t*>(rec + F::OFF_VS)[r] = f16_bits(s);
+                reinterpret_cast<uint16_t*>(rec + F::OFF_VB)[r] = f16_bits(b);
+            }
+        }
+    }
+    if (!do_k) return;
+
+    // K: per-channel range over the 32 rows (one channel per thread), then the codes
     float* kbias = tile + PAGE * D;
     float* kinv = kbias + D;
-    const int tid = threadIdx.x;
-    for (int i = tid; i < PAGE * D; i += NT) {
-        const int t = i / D, d = i % D;
-        const IN* row = t < split ? ka + t * sa : kb_src + (t - split) * skb;
-        tile[i] = to_f32(row[d]);
-    }
     __syncthreads();
-    for (int c = tid; c < D; c += NT) {
+    for (int ch = t; ch < D; ch += WRITE_THREADS) {
         float mn = __builtin_inff(), mx = -__builtin_inff();
 #pragma unroll 8
-        for (int t = 0; t < PAGE; ++t) {
-            const float x = tile[t * D + c];
+        for (int r = 0; r < PAGE; ++r) {
+            const float x = tile[r * D + ch];
             mn = __builtin_fminf(mn, x);
             mx = __builtin_fmaxf(mx, x);
         }
         float s, b, inv;
         qparams<BITS>(mn, mx, s, b, inv);
-        reinterpret_cast<uint16_t*>(rec + F::OFF_KS)[c] = f16_bits(s);
-        reinterpret_cast<uint16_t*>(rec + F::OFF_KB)[c] = f16_bits(b);
-        kbias[c] = b;
-        kinv[c] = inv;
+        reinterpret_cast<uint16_t*>(rec + F::OFF_KS)[ch] = f16_bits(s);
+        reinterpret_cast<uint16_t*>(rec + F::OFF_KB)[ch] = f16_bits(b);
+        kbias[ch] = b;
+        kinv[ch] = inv;
     }
     __syncthreads();
-    for (int i = tid; i < PAGE * F::DC; i += NT) {
-        const int t = i / F::DC, j = i % F::DC;
-        uint8_t byte;
-        if constexpr (BITS == 8) {
-            byte = (uint8_t)qcode<8>(tile[t * D + j], kbias[j], kinv[j]);
-        } else {
-            byte = pack4(qcode<4>(tile[t * D + j], kbias[j], kinv[j]),
-                         qcode<4>(tile[t * D + j + D / 2], kbias[j + D / 2], kinv[j + D / 2]));
+    float bb[16], ii[16];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        const f4 b0 = *reinterpret_cast<const f4*>(kbias + hh * (D / 2) + 8 * c);
+        const f4 b1 = *reinterpret_cast<const f4*>(kbias + hh * (D / 2) + 8 * c + 4);
+        const f4 i0 = *reinterpret_cast<const f4*>(kinv + hh * (D / 2) + 8 * c);
+        const f4 i1 = *reinterpret_cast<const f4*>(kinv + hh * (D / 2) + 8 * c + 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            bb[8 * hh + j] = b0[j];
+            bb[8 * hh + 4 + j] = b1[j];
+            ii[8 * hh + j] = i0[j];
+            ii[8 * hh + 4 + j] = i1[j];
         }
-        rec[t * F::DC + j] = byte;
     }
-    __syncthreads();   // tile is reused by the next call
+#pragma unroll
+    for (int pp = 0; pp < RW::PASSES; ++pp) {
+        const int r = r0 + pp * RW::RP;
+        if (r >= PAGE) continue;
+        u2 lo, hi;
+        pack16<BITS>(kx[pp], bb, ii, lo, hi);
+        uint8_t* dst = rec + r * F::DC + 8 * c;
+        *reinterpret_cast<u2*>(dst) = lo;
+        if constexpr (BITS == 8) *reinterpret_cast<u2*>(dst + D / 2) = hi;
+    }
+    __syncthreads();   // tile is free again
 }
 
-// grid (S), block 256. One token per sequence at position seq_lens[s] + pos_offset; negative
-// positions (padding rows) are skipped. K goes to the exact tail (quantized when its page
-// fills), V straight into its record row. Contract: gpu.mojo:207-238, cpu.mojo:248-270.
-template <int D, int BITS, typename IN>
+// n rows of D elements from src (row stride src_stride) to dst (row stride D)
+template <int D, typename IN, bool VEC>
+__device__ __forceinline__ void copy_rows(IN* __restrict__ dst, const IN* __restrict__ src, int64_t src_stride, int n) {
+    for (int i = threadIdx.x; i < n * (D / 8); i += WRITE_THREADS) {
+        const int r = i / (D / 8), j = 8 * (i % (D / 8));
+        copy8<VEC>(dst + r * D + j, src + (int64_t)r * src_stride + j);
+    }
+}
+
+// grid (S, Hkv), block 256: one (sequence, kv head). One token per sequence at position
+// seq_lens[s] + pos_offset; negative positions (padding rows) are skipped. K goes to the exact
+// tail (quantized when its page fills: rows 0..30 from the tail, row 31 this token, read from k),
+// V straight into its record row. Contract: gpu.mojo:207-238, cpu.mojo:248-270 (seq_lens
+// advances in advance_kernel, launched after this one).
+template <int D, int BITS, typename IN, bool VEC>
 __global__ __launch_bounds__(WRITE_THREADS) void append_kernel(
-    const IN* __restrict__ k, const IN* __restrict__ v, int64_t k_stride, int64_t v_stride, int32_t* seq_lens,
-    int pos_offset, int advance, const int32_t* __restrict__ tail_idx, uint8_t* __restrict__ cache, int64_t bs,
-    int64_t hs, IN* __restrict__ tail_k, const int32_t* __restrict__ block_table, int64_t bt_stride, int H) {
-    __shared__ float tile[PAGE * D + 2 * D];
-    const int s = blockIdx.x;
+    const IN* __restrict__ k, const IN* __restrict__ v, int64_t k_stride, int64_t v_stride,
+    const int32_t* __restrict__ seq_lens, int pos_offset, const int32_t* __restrict__ tail_idx,
+    uint8_t* __restrict__ cache, int64_t bs, int64_t hs, IN* __restrict__ tail_k,
+    const int32_t* __restrict__ block_table, int64_t bt_stride, int H) {
+    __shared__ __align__(16) float tile[PAGE * D + 2 * D];
+    const int s = blockIdx.x, h = blockIdx.y;
     const int pos = seq_lens[s] + pos_offset;
     if (pos < 0) return;
     const int slot = pos % PAGE;
     const int64_t blk = block_table[(int64_t)s * bt_stride + pos / PAGE];
-    const int64_t tb = (int64_t)tail_idx[s] * H * PAGE * D;
-    const IN* krow = k + (int64_t)s * k_stride;
-    const IN* vrow = v + (int64_t)s * v_stride;
-    for (int i = threadIdx.x; i < H * D; i += WRITE_THREADS) {
-        const int h = i / D, d = i % D;
-        tail_k[tb + ((int64_t)h * PAGE + slot) * D + d] = krow[(int64_t)h * D + d];
+    IN* tail = tail_k + ((int64_t)tail_idx[s] * H + h) * PAGE * D;
+    const IN* krow = k + (int64_t)s * k_stride + (int64_t)h * D;
+    uint8_t* rec = cache + blk * bs + (int64_t)h * hs;
+    copy_rows<D, IN, VEC>(tail + slot * D, krow, 0, 1);
+    page_task<D, BITS, IN, VEC>(tail, krow, 0, PAGE - 1, slot == PAGE - 1, v + (int64_t)s * v_stride + (int64_t)h * D,
+                                0, slot, slot + 1, rec, tile);
+}
+
+// seq_lens[s] = seq_lens[s] + pos_offset + 1 where that position is >= 0 (the appended token)
+__global__ __launch_bounds__(256) void advance_kernel(int32_t* seq_lens, int pos_offset, int S) {
+    const int s = blockIdx.x * 256 + threadIdx.x;
+    if (s < S) {
+        const int pos = seq_lens[s] + pos_offset;
+        if (pos >= 0) seq_lens[s] = pos + 1;
     }
-    const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-    for (int h = wave; h < H; h += WRITE_THREADS / WAVE)
-        quantize_v_row<D, BITS, IN>(vrow + (int64_t)h * D, cache + blk * bs + (int64_t)h * hs, slot, lane);
-    if (slot == PAGE - 1) {
-        // rows 0..30 were stashed in the tail by earlier steps; row 31 is this token
-        for (int h = 0; h < H; ++h)
-            quantize_k_page<D, BITS, IN, WRITE_THREADS>(tail_k + tb + (int64_t)h * PAGE * D, D, krow + (int64_t)h * D, 0,
-                                                        PAGE - 1, cache + blk * bs + (int64_t)h * hs, tile);
-    }
-    __syncthreads();   // every thread has read seq_lens[s]
-    if (advance && threadIdx.x == 0) seq_lens[s] = pos + 1;
 }
 
 // grid (n_jobs, Hkv), block 256. Job j covers logical page job_page[j] of sequence job_seq[j],
@@ -136,13 +245,13 @@ __global__ __launch_bounds__(WRITE_THREADS) void append_kernel(
 // the tail, newer from the chunk). mode 1: stash the new K rows of a still-partial page in the
 // tail. Launched as mode 0 then mode 1 so no tail is read and written by the same launch.
 // Contract: gpu.mojo:241-276, cpu.mojo:273-304.
-template <int D, int BITS, typename IN>
+template <int D, int BITS, typename IN, bool VEC>
 __global__ __launch_bounds__(WRITE_THREADS) void write_kernel(
     const IN* __restrict__ k, const IN* __restrict__ v, int64_t k_stride, int64_t v_stride,
     const int32_t* __restrict__ qsl, const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ tail_idx,
     const int32_t* __restrict__ job_seq, const int32_t* __restrict__ job_page, int mode, uint8_t* __restrict__ cache,
     int64_t bs, int64_t hs, IN* __restrict__ tail_k, const int32_t* __restrict__ block_table, int64_t bt_stride, int H) {
-    __shared__ float tile[PAGE * D + 2 * D];
+    __shared__ __align__(16) float tile[PAGE * D + 2 * D];
     const int j = blockIdx.x, h = blockIdx.y;
     const int s = job_seq[j];
     const int ps = job_page[j] * PAGE;
@@ -150,29 +259,29 @@ __global__ __launch_bounds__(WRITE_THREADS) void write_kernel(
     const int total = seq_lens[s];
     const int ctx = total - (qsl[s + 1] - q0);
     const bool complete = ps + PAGE <= total;
-    const int64_t tb = ((int64_t)tail_idx[s] * H + h) * PAGE * D;
-    const int lo = ps > ctx ? ps : ctx;
+    IN* tail = tail_k + ((int64_t)tail_idx[s] * H + h) * PAGE * D;
+    const int lo = ps > ctx ? ps : ctx;                     // first new position in the page
+    const int64_t hoff = (int64_t)h * D;
     if (mode == 0) {
         uint8_t* rec = cache + (int64_t)block_table[(int64_t)s * bt_stride + ps / PAGE] * bs + (int64_t)h * hs;
         const int hi = ps + PAGE < total ? ps + PAGE : total;
-        const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-        for (int t = lo + wave; t < hi; t += WRITE_THREADS / WAVE)
-            quantize_v_row<D, BITS, IN>(v + (int64_t)(q0 + t - ctx) * v_stride + (int64_t)h * D, rec, t - ps, lane);
-        if (complete) {
-            int split = ctx - ps;
-            split = split < 0 ? 0 : (split > PAGE ? PAGE : split);
-            quantize_k_page<D, BITS, IN, WRITE_THREADS>(tail_k + tb, D,
-                                                        k + (int64_t)(q0 + ps + split - ctx) * k_stride + (int64_t)h * D,
-                                                        k_stride, split, rec, tile);
-        }
-    } else {
-        if (complete) return;
-        const int n = total - lo;
-        for (int i = threadIdx.x; i < n * D; i += WRITE_THREADS) {
-            const int t = lo + i / D, d = i % D;
-            tail_k[tb + (int64_t)(t - ps) * D + d] = k[(int64_t)(q0 + t - ctx) * k_stride + (int64_t)h * D + d];
-        }
+        int split = ctx - ps;                               // K rows before it come from the tail
+        split = split < 0 ? 0 : (split > PAGE ? PAGE : split);
+        page_task<D, BITS, IN, VEC>(tail, k + (int64_t)(q0 + ps + split - ctx) * k_stride + hoff, k_stride, split,
+                                    complete, v + (int64_t)(q0 + lo - ctx) * v_stride + hoff, v_stride, lo - ps,
+                                    hi - ps, rec, tile);
+    } else if (!complete) {
+        copy_rows<D, IN, VEC>(tail + (lo - ps) * D, k + (int64_t)(q0 + lo - ctx) * k_stride + hoff, k_stride,
+                              total - lo);
     }
+}
+
+// 16-byte loads and stores when k / v rows (pointer and row stride) and tail_k are 16-byte aligned
+template <typename IN>
+static bool rows_aligned(const void* k, const void* v, int64_t k_stride, int64_t v_stride, const void* tail_k) {
+    const uint64_t e = sizeof(IN);
+    return (((uintptr_t)k | (uintptr_t)v | (uintptr_t)tail_k | (uint64_t)(k_stride * e) | (uint64_t)(v_stride * e)) &
+            15) == 0;
 }
 
 }  // namespace kush
@@ -189,9 +298,14 @@ extern "C" int kush_append(int head_dim, int bits, int dtype, const void* k, con
         constexpr int D = decltype(dd)::value, BITS = decltype(bb)::value;
         using IN = decltype(in);
         if (n_seqs == 0) return 0;
-        append_kernel<D, BITS, IN><<<dim3(n_seqs), dim3(WRITE_THREADS), 0, (hipStream_t)stream>>>(
-            (const IN*)k, (const IN*)v, k_stride, v_stride, seq_lens, pos_offset, advance, tail_idx, (uint8_t*)cache,
-            block_stride, head_stride, (IN*)tail_k, block_table, bt_stride, hkv);
+        hipStream_t st = (hipStream_t)stream;
+        auto kern = rows_aligned<IN>(k, v, k_stride, v_stride, tail_k) ? append_kernel<D, BITS, IN, true>
+                                                                         : append_kernel<D, BITS, IN, false>;
+        kern<<<dim3(n_seqs, hkv), dim3(WRITE_THREADS), 0, st>>>((const IN*)k, (const IN*)v, k_stride, v_stride,
+                                                                seq_lens, pos_offset, tail_idx, (uint8_t*)cache,
+                                                                block_stride, head_stride, (IN*)tail_k, block_table,
+                                                                bt_stride, hkv);
+        if (advance) advance_kernel<<<dim3((n_seqs + 255) / 256), dim3(256), 0, st>>>(seq_lens, pos_offset, n_seqs);
         return kush_check_launch("kush_append");
     });
 }
@@ -207,7 +321,9 @@ extern "C" int kush_write(int head_dim, int bits, int dtype, const void* k, cons
         constexpr int D = decltype(dd)::value, BITS = decltype(bb)::value;
         using IN = decltype(in);
         if (n_jobs == 0) return 0;
-        write_kernel<D, BITS, IN><<<dim3(n_jobs, hkv), dim3(WRITE_THREADS), 0, (hipStream_t)stream>>>(
+        auto kern = rows_aligned<IN>(k, v, k_stride, v_stride, tail_k) ? write_kernel<D, BITS, IN, true>
+                                                                         : write_kernel<D, BITS, IN, false>;
+        kern<<<dim3(n_jobs, hkv), dim3(WRITE_THREADS), 0, (hipStream_t)stream>>>(
             (const IN*)k, (const IN*)v, k_stride, v_stride, query_start_loc, seq_lens, tail_idx, job_seq, job_page,
             mode, (uint8_t*)cache, block_stride, head_stride, (IN*)tail_k, block_table, bt_stride, hkv);
         return kush_check_launch("kush_write");

@@ -151,3 +151,93 @@ def test_empty_and_short_sequences():
     got = out.float().cpu()
     assert torch.equal(got[0], torch.zeros_like(got[0]))
     assert (got - want).abs().max().item() <= out_tol(want, dtype)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_write_rows_any_stride(bits, dtype):
+    """k / v rows whose row stride breaks 16-byte alignment (a free row stride, as the reference's
+    _ops.py:6-15 allows) pack the same record bytes and tails as contiguous rows; chunks that start
+    mid-page and end mid-page (split K pages, mode-1 tails), then appends with pos_offset -1."""
+    torch.manual_seed(bits)
+    S, H, D = 3, 2, 128
+    ops = kk.Ops(torch.device(DEV), D, bits, 1, dtype)
+    pages = 4
+    RB = kk.record_bytes(D, bits)
+    bt = torch.randperm(S * pages, dtype=torch.int32).view(S, pages).to(DEV)
+    tail_idx = torch.arange(S, dtype=torch.int32, device=DEV)
+    lens0, lens1 = [20, 40, 64], [50, 75, 94]                       # two chunks per sequence
+    T = max(lens1)
+    kf = torch.randn(S * T, H, D) * 3
+    vf = torch.randn(S * T, H, D)
+    kf[..., 5] += 40
+
+    def packed(stride_pad: int):
+        cache = torch.zeros(S * pages, H, RB, dtype=torch.uint8, device=DEV)
+        tail_k = torch.zeros(S, H, PAGE, D, dtype=dtype, device=DEV)
+        big_k = torch.zeros(S * T, H * D + stride_pad, dtype=dtype, device=DEV)
+        big_v = torch.zeros(S * T, H * D + stride_pad, dtype=dtype, device=DEV)
+        big_k[:, :H * D] = kf.view(S * T, H * D).to(dtype).to(DEV)
+        big_v[:, :H * D] = vf.view(S * T, H * D).to(dtype).to(DEV)
+        k = big_k[:, :H * D].unflatten(1, (H, D))
+        v = big_v[:, :H * D].unflatten(1, (H, D))
+        done = [0] * S
+        for lens in (lens0, lens1):
+            n_new = [lens[s] - done[s] for s in range(S)]
+            rows = torch.cat([torch.arange(s * T + done[s], s * T + lens[s]) for s in range(S)]).to(DEV)
+            qsl = torch.tensor([0] + [sum(n_new[:i + 1]) for i in range(S)], dtype=torch.int32, device=DEV)
+            jobs = [(s, p) for s in range(S) for p in range(done[s] // PAGE, -(-lens[s] // PAGE))]
+            js = torch.tensor([j[0] for j in jobs], dtype=torch.int32, device=DEV)
+            jp = torch.tensor([j[1] for j in jobs], dtype=torch.int32, device=DEV)
+            kr, vr = k[rows], v[rows]                                    # gathered rows, same stride pattern
+            if stride_pad:
+                kb2 = torch.zeros(kr.shape[0], H * D + stride_pad, dtype=dtype, device=DEV)
+                vb2 = torch.zeros(kr.shape[0], H * D + stride_pad, dtype=dtype, device=DEV)
+                kb2[:, :H * D] = kr.flatten(1)
+                vb2[:, :H * D] = vr.flatten(1)
+                kr, vr = kb2[:, :H * D].unflatten(1, (H, D)), vb2[:, :H * D].unflatten(1, (H, D))
+            sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+            ops.write(kr, vr, qsl, sl, tail_idx, js, jp, cache, bt, tail_k)
+            done = list(lens)
+        # appends: one token per sequence at position seq_lens - 1 (vLLM convention)
+        for step in range(2):
+            sl = torch.tensor([n + 1 + step for n in lens1], dtype=torch.int32, device=DEV)
+            ka = torch.randn(S, H, D, generator=torch.Generator().manual_seed(step)).to(dtype)
+            va = torch.randn(S, H, D, generator=torch.Generator().manual_seed(10 + step)).to(dtype)
+            if stride_pad:
+                kb2 = torch.zeros(S, H * D + stride_pad, dtype=dtype, device=DEV)
+                vb2 = torch.zeros(S, H * D + stride_pad, dtype=dtype, device=DEV)
+                kb2[:, :H * D], vb2[:, :H * D] = ka.flatten(1).to(DEV), va.flatten(1).to(DEV)
+                ka, va = kb2[:, :H * D].unflatten(1, (H, D)), vb2[:, :H * D].unflatten(1, (H, D))
+            else:
+                ka, va = ka.to(DEV), va.to(DEV)
+            ops.append(ka, va, sl, tail_idx, cache, bt, tail_k, pos_offset=-1, advance=False)
+        torch.cuda.synchronize()
+        return cache.cpu(), tail_k.cpu()
+
+    c0, t0 = packed(0)
+    c1, t1 = packed(1)                                              # rows 2-byte (bf16) / 4-byte (fp32) off
+    assert torch.equal(c0, c1)
+    assert torch.equal(t0, t1)
+    # and the contiguous rows match the oracle's packing of the same writes
+    oc = OracleOps("cpu", D, bits, 1)
+    cache = torch.zeros(S * pages, H, RB, dtype=torch.uint8)
+    tail_k = torch.zeros(S, H, PAGE, D)
+    done = [0] * S
+    for lens in (lens0, lens1):
+        n_new = [lens[s] - done[s] for s in range(S)]
+        rows = torch.cat([torch.arange(s * T + done[s], s * T + lens[s]) for s in range(S)])
+        qsl = torch.tensor([0] + [sum(n_new[:i + 1]) for i in range(S)], dtype=torch.int32)
+        jobs = [(s, p) for s in range(S) for p in range(done[s] // PAGE, -(-lens[s] // PAGE))]
+        oc.write(kf.to(dtype).float()[rows].contiguous(), vf.to(dtype).float()[rows].contiguous(), qsl,
+                 torch.tensor(lens, dtype=torch.int32), tail_idx.cpu(),
+                 torch.tensor([j[0] for j in jobs], dtype=torch.int32),
+                 torch.tensor([j[1] for j in jobs], dtype=torch.int32), cache, bt.cpu(), tail_k)
+        done = list(lens)
+    for step in range(2):
+        sl = torch.tensor([n + 1 + step for n in lens1], dtype=torch.int32)
+        ka = torch.randn(S, H, D, generator=torch.Generator().manual_seed(step)).to(dtype).float()
+        va = torch.randn(S, H, D, generator=torch.Generator().manual_seed(10 + step)).to(dtype).float()
+        oc.append(ka, va, sl, tail_idx.cpu(), cache, bt.cpu(), tail_k, pos_offset=-1, advance=False)
+    assert torch.equal(c0, cache)
+    assert torch.equal(t0.float(), tail_k)
