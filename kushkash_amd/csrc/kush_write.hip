@@ -48,26 +48,36 @@ __device__ __forceinline__ void copy8(IN* dst, const IN* src) {
 }
 
 // codes of the 16 values of a thread (x[0..8): dims 8c.., x[8..16): dims D/2 + 8c..) -> the bytes
-// they make: int4 byte i = code(x[i]) | code(x[8 + i]) << 4 (row bytes 8c + i, in lo); int8 bytes in
-// dim order (row bytes 8c + i in lo, D/2 + 8c + i in hi)
+// they make: int4 byte i = code(x[i]) & 15 | (code(x[8 + i]) & 15) << 4 (row bytes 8c + i, in lo);
+// int8 bytes in dim order (row bytes 8c + i in lo, D/2 + 8c + i in hi). The codes stay floats
+// (exact small integers): an offset byte (code + 8 per nibble, code + 128) is inserted by
+// v_cvt_pk_u8_f32 and the offset taken out of the whole word by one xor.
 #pragma clang fp contract(off)
+template <int BITS>
+__device__ __forceinline__ float qcode_f(float x, float b, float inv) {
+    constexpr float HALF = float(1 << (BITS - 1));
+    const float r = __builtin_rintf((x - b) * inv);
+    return __builtin_fminf(__builtin_fmaxf(r, -HALF), HALF - 1.0f);
+}
+
 template <int BITS>
 __device__ __forceinline__ void pack16(const float (&x)[16], const float (&b)[16], const float (&inv)[16], u2& lo,
                                        u2& hi) {
     uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const uint32_t c0 = (uint32_t)qcode<BITS>(x[i], b[i], inv[i]);
-        const uint32_t c1 = (uint32_t)qcode<BITS>(x[8 + i], b[8 + i], inv[8 + i]);
+        const float c0 = qcode_f<BITS>(x[i], b[i], inv[i]);
+        const float c1 = qcode_f<BITS>(x[8 + i], b[8 + i], inv[8 + i]);
         if constexpr (BITS == 4) {
-            w[i / 4] |= ((c0 & 0xFu) | ((c1 & 0xFu) << 4)) << (8 * (i % 4));
+            w[i / 4] = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(c1, 16.0f, c0) + 136.0f, i % 4, w[i / 4]);
         } else {
-            w[i / 4] |= (c0 & 0xFFu) << (8 * (i % 4));
-            w[2 + i / 4] |= (c1 & 0xFFu) << (8 * (i % 4));
+            w[i / 4] = __builtin_amdgcn_cvt_pk_u8_f32(c0 + 128.0f, i % 4, w[i / 4]);
+            w[2 + i / 4] = __builtin_amdgcn_cvt_pk_u8_f32(c1 + 128.0f, i % 4, w[2 + i / 4]);
         }
     }
-    lo = u2{w[0], w[1]};
-    hi = u2{w[2], w[3]};
+    constexpr uint32_t OFF = BITS == 4 ? 0x88888888u : 0x80808080u;
+    lo = u2{w[0] ^ OFF, w[1] ^ OFF};
+    hi = u2{w[2] ^ OFF, w[3] ^ OFF};
 }
 #pragma clang fp contract(on)
 
@@ -83,50 +93,29 @@ __device__ __forceinline__ void page_task(const IN* __restrict__ k_tail, const I
     using RW = Rows<D>;
     constexpr int CG = RW::CG;
     const int t = threadIdx.x, c = t % CG, r0 = t / CG;
-    float kx[RW::PASSES][16];
+
+    // V rows: each row's final encoding, per-token range over the CG lanes of the row (consecutive
+    // lanes of one wave, all taking the same branch)
+    const auto v_rows = [&]() {
 #pragma unroll
-    for (int pp = 0; pp < RW::PASSES; ++pp) {
-        const int r = r0 + pp * RW::RP;
-        if (do_k && r < PAGE) {
-            const IN* row = r < split ? k_tail + r * D : k_new + (int64_t)(r - split) * k_stride;
-            float a[8], b[8];
-            get8<VEC>(row + 8 * c, a);
-            get8<VEC>(row + D / 2 + 8 * c, b);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                kx[pp][j] = a[j];
-                kx[pp][8 + j] = b[j];
-            }
-            float* tr = tile + r * D;
-            *reinterpret_cast<f4*>(tr + 8 * c) = f4{a[0], a[1], a[2], a[3]};
-            *reinterpret_cast<f4*>(tr + 8 * c + 4) = f4{a[4], a[5], a[6], a[7]};
-            *reinterpret_cast<f4*>(tr + D / 2 + 8 * c) = f4{b[0], b[1], b[2], b[3]};
-            *reinterpret_cast<f4*>(tr + D / 2 + 8 * c + 4) = f4{b[4], b[5], b[6], b[7]};
-        }
-        // V row r (its final encoding: per-token range over the CG threads of the row, which are
-        // consecutive lanes of one wave)
-        const bool vrow = r >= vlo && r < vhi && r < PAGE;
-        float x[16];
-        float mn = __builtin_inff(), mx = -__builtin_inff();
-        if (vrow) {
+        for (int pp = 0; pp < RW::PASSES; ++pp) {
+            const int r = r0 + pp * RW::RP;
+            if (r < vlo || r >= vhi || r >= PAGE) continue;
             const IN* row = v_new + (int64_t)(r - vlo) * v_stride;
-            float a[8], b[8];
-            get8<VEC>(row + 8 * c, a);
-            get8<VEC>(row + D / 2 + 8 * c, b);
+            float x[16];
+            get8<VEC>(row + 8 * c, reinterpret_cast<float(&)[8]>(x[0]));
+            get8<VEC>(row + D / 2 + 8 * c, reinterpret_cast<float(&)[8]>(x[8]));
+            float mn = x[0], mx = x[0];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                x[j] = a[j];
-                x[8 + j] = b[j];
-                mn = __builtin_fminf(mn, __builtin_fminf(a[j], b[j]));
-                mx = __builtin_fmaxf(mx, __builtin_fmaxf(a[j], b[j]));
+            for (int j = 1; j < 16; ++j) {
+                mn = __builtin_fminf(mn, x[j]);
+                mx = __builtin_fmaxf(mx, x[j]);
             }
-        }
 #pragma unroll
-        for (int o = 1; o < CG; o <<= 1) {
-            mn = __builtin_fminf(mn, __shfl_xor(mn, o, WAVE));
-            mx = __builtin_fmaxf(mx, __shfl_xor(mx, o, WAVE));
-        }
-        if (vrow) {
+            for (int o = 1; o < CG; o <<= 1) {
+                mn = __builtin_fminf(mn, __shfl_xor(mn, o, WAVE));
+                mx = __builtin_fmaxf(mx, __shfl_xor(mx, o, WAVE));
+            }
             float s, b, inv;
             qparams<BITS>(mn, mx, s, b, inv);
             float bb[16], ii[16];
@@ -145,8 +134,31 @@ __device__ __forceinline__ void page_task(const IN* __restrict__ k_tail, const I
                 reinterpret_cast<uint16_t*>(rec + F::OFF_VB)[r] = f16_bits(b);
             }
         }
+    };
+    if (!do_k) {
+        v_rows();
+        return;
     }
-    if (!do_k) return;
+
+    // K rows into registers and the fp32 tile (loads issued before the V work)
+    float kx[RW::PASSES][16];
+#pragma unroll
+    for (int pp = 0; pp < RW::PASSES; ++pp) {
+        const int r = r0 + pp * RW::RP;
+        if (r >= PAGE) continue;
+        const IN* row = r < split ? k_tail + r * D : k_new + (int64_t)(r - split) * k_stride;
+        get8<VEC>(row + 8 * c, reinterpret_cast<float(&)[8]>(kx[pp][0]));
+        get8<VEC>(row + D / 2 + 8 * c, reinterpret_cast<float(&)[8]>(kx[pp][8]));
+        float* tr = tile + r * D;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            *reinterpret_cast<f4*>(tr + hh * (D / 2) + 8 * c) =
+                f4{kx[pp][8 * hh], kx[pp][8 * hh + 1], kx[pp][8 * hh + 2], kx[pp][8 * hh + 3]};
+            *reinterpret_cast<f4*>(tr + hh * (D / 2) + 8 * c + 4) =
+                f4{kx[pp][8 * hh + 4], kx[pp][8 * hh + 5], kx[pp][8 * hh + 6], kx[pp][8 * hh + 7]};
+        }
+    }
+    v_rows();
 
     // K: per-channel range over the 32 rows (one channel per thread), then the codes
     float* kbias = tile + PAGE * D;
@@ -239,17 +251,17 @@ __global__ __launch_bounds__(256) void advance_kernel(int32_t* seq_lens, int pos
     }
 }
 
-// grid (n_jobs, Hkv), block 256. Job j covers logical page job_page[j] of sequence job_seq[j],
-// whose new rows [qsl[s], qsl[s+1]) sit at positions [ctx, seq_lens[s]).
-// mode 0: write the page's new V rows; if the page is complete, quantize its K (older rows from
-// the tail, newer from the chunk). mode 1: stash the new K rows of a still-partial page in the
-// tail. Launched as mode 0 then mode 1 so no tail is read and written by the same launch.
+// grid (n_jobs, Hkv), block 256: the write's mode 0. Job j covers logical page job_page[j] of
+// sequence job_seq[j], whose new rows [qsl[s], qsl[s+1]) sit at positions [ctx, seq_lens[s]):
+// write the page's new V rows and, if the page is complete, quantize its K (older rows from the
+// tail, newer from the chunk). Mode 1 (tail_kernel) then stashes the new K rows of still-partial
+// pages in the tail: two launches, so no tail is read and written by the same one.
 // Contract: gpu.mojo:241-276, cpu.mojo:273-304.
 template <int D, int BITS, typename IN, bool VEC>
 __global__ __launch_bounds__(WRITE_THREADS) void write_kernel(
     const IN* __restrict__ k, const IN* __restrict__ v, int64_t k_stride, int64_t v_stride,
     const int32_t* __restrict__ qsl, const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ tail_idx,
-    const int32_t* __restrict__ job_seq, const int32_t* __restrict__ job_page, int mode, uint8_t* __restrict__ cache,
+    const int32_t* __restrict__ job_seq, const int32_t* __restrict__ job_page, uint8_t* __restrict__ cache,
     int64_t bs, int64_t hs, IN* __restrict__ tail_k, const int32_t* __restrict__ block_table, int64_t bt_stride, int H) {
     __shared__ __align__(16) float tile[PAGE * D + 2 * D];
     const int j = blockIdx.x, h = blockIdx.y;
@@ -262,7 +274,7 @@ __global__ __launch_bounds__(WRITE_THREADS) void write_kernel(
     IN* tail = tail_k + ((int64_t)tail_idx[s] * H + h) * PAGE * D;
     const int lo = ps > ctx ? ps : ctx;                     // first new position in the page
     const int64_t hoff = (int64_t)h * D;
-    if (mode == 0) {
+    {
         uint8_t* rec = cache + (int64_t)block_table[(int64_t)s * bt_stride + ps / PAGE] * bs + (int64_t)h * hs;
         const int hi = ps + PAGE < total ? ps + PAGE : total;
         int split = ctx - ps;                               // K rows before it come from the tail
@@ -270,9 +282,33 @@ __global__ __launch_bounds__(WRITE_THREADS) void write_kernel(
         page_task<D, BITS, IN, VEC>(tail, k + (int64_t)(q0 + ps + split - ctx) * k_stride + hoff, k_stride, split,
                                     complete, v + (int64_t)(q0 + lo - ctx) * v_stride + hoff, v_stride, lo - ps,
                                     hi - ps, rec, tile);
-    } else if (!complete) {
-        copy_rows<D, IN, VEC>(tail + (lo - ps) * D, k + (int64_t)(q0 + lo - ctx) * k_stride + hoff, k_stride,
-                              total - lo);
+    }
+}
+
+// grid (ceil(n_jobs * Hkv / 4)), block 256: the write's mode 1, one wave per (job, kv head): stash
+// the new K rows of a still-partial page in the tail (a complete page's wave returns at once).
+template <int D, typename IN, bool VEC>
+__global__ __launch_bounds__(256) void tail_kernel(const IN* __restrict__ k, int64_t k_stride,
+                                                   const int32_t* __restrict__ qsl, const int32_t* __restrict__ seq_lens,
+                                                   const int32_t* __restrict__ tail_idx,
+                                                   const int32_t* __restrict__ job_seq,
+                                                   const int32_t* __restrict__ job_page, int n_jobs,
+                                                   IN* __restrict__ tail_k, int H) {
+    const int gw = blockIdx.x * 4 + (int)(threadIdx.x / WAVE), lane = threadIdx.x % WAVE;
+    const int j = gw / H, h = gw % H;
+    if (j >= n_jobs) return;
+    const int s = job_seq[j];
+    const int ps = job_page[j] * PAGE;
+    const int total = seq_lens[s];
+    if (ps + PAGE <= total) return;
+    const int q0 = qsl[s];
+    const int ctx = total - (qsl[s + 1] - q0);
+    const int lo = ps > ctx ? ps : ctx;
+    IN* dst = tail_k + (((int64_t)tail_idx[s] * H + h) * PAGE + (lo - ps)) * D;
+    const IN* src = k + (int64_t)(q0 + lo - ctx) * k_stride + (int64_t)h * D;
+    for (int i = lane; i < (total - lo) * (D / 8); i += WAVE) {
+        const int r = i / (D / 8), c = 8 * (i % (D / 8));
+        copy8<VEC>(dst + r * D + c, src + (int64_t)r * k_stride + c);
     }
 }
 
@@ -321,11 +357,18 @@ extern "C" int kush_write(int head_dim, int bits, int dtype, const void* k, cons
         constexpr int D = decltype(dd)::value, BITS = decltype(bb)::value;
         using IN = decltype(in);
         if (n_jobs == 0) return 0;
-        auto kern = rows_aligned<IN>(k, v, k_stride, v_stride, tail_k) ? write_kernel<D, BITS, IN, true>
-                                                                         : write_kernel<D, BITS, IN, false>;
-        kern<<<dim3(n_jobs, hkv), dim3(WRITE_THREADS), 0, (hipStream_t)stream>>>(
-            (const IN*)k, (const IN*)v, k_stride, v_stride, query_start_loc, seq_lens, tail_idx, job_seq, job_page,
-            mode, (uint8_t*)cache, block_stride, head_stride, (IN*)tail_k, block_table, bt_stride, hkv);
+        const bool vec = rows_aligned<IN>(k, v, k_stride, v_stride, tail_k);
+        hipStream_t st = (hipStream_t)stream;
+        if (mode == 0) {
+            auto kern = vec ? write_kernel<D, BITS, IN, true> : write_kernel<D, BITS, IN, false>;
+            kern<<<dim3(n_jobs, hkv), dim3(WRITE_THREADS), 0, st>>>(
+                (const IN*)k, (const IN*)v, k_stride, v_stride, query_start_loc, seq_lens, tail_idx, job_seq, job_page,
+                (uint8_t*)cache, block_stride, head_stride, (IN*)tail_k, block_table, bt_stride, hkv);
+        } else {
+            auto kern = vec ? tail_kernel<D, IN, true> : tail_kernel<D, IN, false>;
+            kern<<<dim3(((int64_t)n_jobs * hkv + 3) / 4), dim3(256), 0, st>>>(
+                (const IN*)k, k_stride, query_start_loc, seq_lens, tail_idx, job_seq, job_page, n_jobs, (IN*)tail_k, hkv);
+        }
         return kush_check_launch("kush_write");
     });
 }
