@@ -362,9 +362,13 @@ def bench_c3(a) -> None:
     work = torch.empty(max(1, B * Hkv * ns * G * (D + 2)), dtype=torch.float32, device=dev)
     sm = 1.0 / math.sqrt(D)
 
+    # longest sequences first (from the host-side lengths, as a serving engine's metadata builder has
+    # them): the ragged batch's long workgroups start first
+    order = torch.tensor(sorted(range(B), key=lambda i: -lens[i]), dtype=torch.int32, device=dev)
+
     def step(i):
         ops.append(k_new, v_new, sl, tail_idx, cache, table, tail_k, pos_offset=-1, advance=False)
-        ops.decode(q, out, cache, table, sl, tail_idx, tail_k, sm, ns, work)
+        ops.decode(q, out, cache, table, sl, tail_idx, tail_k, sm, ns, work, waves=a.waves or None, order=order)
 
     ms = time_graph(step, a.steps, a.warmup)
     RB, DC = record_bytes(D, bits), (D if bits == 8 else D // 2)
@@ -377,7 +381,8 @@ def bench_c3(a) -> None:
     _line("append + decode us/step + achieved HBM GB/s (% peak), int8, bs128 ragged U[256, 8192]", ms * 1e3, alg,
           {"workload": f"C3 Llama-3.1-8B layer: {Hq} q / {Hkv} kv heads, D {D}, int{bits}, page 32, batch {B}, "
                        f"N_i ~ U[256, 8192] (seed 0; sum {sum(lens)} tokens), append (pos_offset -1) + decode",
-           "global_batch": B, "split_k": ns, "tokens": sum(n1)},
+           "global_batch": B, "split_k": ns, "tokens": sum(n1), "sequence_order": "longest first",
+           "waves": a.waves or ops.waves(B, Hkv, ns, table.shape[1])},
           f"append_kernel<{D},{bits},bf16> + decode_kernel<{D},{bits},bf16,4>")
 
 
@@ -400,7 +405,8 @@ def bench_c4(a) -> None:
     nss = [a.splits or policy] + [int(x) for x in a.sweep.split(",") if x.strip() and ":" not in x]
     for i, ns in enumerate(nss):
         work = torch.empty(B * Hkv * ns * G * (D + 2), dtype=torch.float32, device=dev)
-        ms = time_graph(lambda j: ops.decode(q, out, cache, table, sl, tail_idx, tail_k, sm, ns, work),
+        ms = time_graph(lambda j: ops.decode(q, out, cache, table, sl, tail_idx, tail_k, sm, ns, work,
+                                            waves=a.waves or None),
                         a.steps, a.warmup)
         if i == 0:
             _line("decode-attn us/step + achieved HBM GB/s (% peak), int4, bs8 x 131k ctx", ms * 1e3, alg,
@@ -476,7 +482,7 @@ def main(argv=None):
         print(f"splits {sns:4d} waves {swv:3d}: {msx * 1e3:8.2f} us/step  {alg / msx / 1e6:7.1f} GB/s "
               f"({100 * alg / msx / 1e6 / PEAK_HBM_GBS:5.1f}% of peak)", file=sys.stderr, flush=True)
 
-    wv = a.waves or w["ops"].waves(w["B"], w["Hkv"], ns)
+    wv = a.waves or w["ops"].waves(w["B"], w["Hkv"], ns, w["pages"])
     ms = time_steps(w, ns, wv, a.steps, a.warmup)
     workload = (f"C2 Qwen2.5-7B decode layer: {a.hq} q / {a.hkv} kv heads, D {a.dim}, int{a.bits}, page 32, "
                 f"batch {a.batch} x {a.ctx} tokens")

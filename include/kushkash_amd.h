@@ -80,6 +80,8 @@ int kush_write(int head_dim, int bits, int dtype, const void* k, const void* v, 
  * resets its counter, so the buffer stays zero between calls; calls that share split_sync must
  * not overlap. Without it (NULL), run kush_combine afterwards. waves: 2, 4 or 8 waves per
  * workgroup (0 = 8; a configuration whose page ring does not fit in LDS falls back to fewer).
+ * seq_order: NULL, or int32 [n_seqs] holding a permutation of the sequences: their workgroups
+ * start in that order (longest first balances a ragged batch); the results do not depend on it.
  * q and tail_k must be 16-byte aligned.
  * Replaces kush_decode_tc / kush_decode (gpu.mojo:566-807, :840-1040) and, with split_sync, the
  * kush_combine launch (gpu.mojo:469-491) as issued by Ops.decode (_ops.py:191-213). */
@@ -87,7 +89,7 @@ int kush_decode(int head_dim, int bits, int group, int dtype, const void* q, voi
                 int64_t block_stride, int64_t head_stride, const void* tail_k, const int32_t* tail_idx,
                 const int32_t* block_table, const int32_t* seq_lens, int64_t bt_row_stride, int32_t hkv,
                 float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t* split_sync, int32_t waves,
-                int32_t n_seqs, void* stream);
+                const int32_t* seq_order, int32_t n_seqs, void* stream);
 
 /* Merge kush_decode's split partials into out [n_seqs][hkv*group][head_dim].
  * Replaces kush_combine (gpu.mojo:469-491) as launched by Ops.decode (_ops.py:212-213). */
@@ -98,7 +100,7 @@ int kush_combine(int head_dim, int group, int dtype, void* out, const float* par
  * reference raises the driver's error string directly (_cuda.py:39-43). */
 const char* kush_last_error(void);
 
-/* ABI revision of this header (2). No reference counterpart. */
+/* ABI revision of this header (3). No reference counterpart. */
 int kush_abi_version(void);
 
 #ifdef __cplusplus

@@ -558,7 +558,8 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     const IN* __restrict__ qg, IN* __restrict__ out, const uint8_t* __restrict__ cache, int64_t bs, int64_t hs,
     const IN* __restrict__ tail_k, const int32_t* __restrict__ tail_idx, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ seq_lens, int64_t bt_stride, int H, int G, float p2, float rs, int NS,
-    float* __restrict__ part_ml, float* __restrict__ part_o, int32_t* __restrict__ sync) {
+    float* __restrict__ part_ml, float* __restrict__ part_o, int32_t* __restrict__ sync,
+    const int32_t* __restrict__ seq_order) {
     using F = Fmt<D, BITS>;
     using R = Ring<D, BITS>;
     constexpr int KSTEPS = D / 32;
@@ -566,6 +567,7 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     constexpr int NLO = BITS == 4 ? D / 32 : D / 16;          // O tiles in units of 2^-24 (the rest 2^-20)
     constexpr float TWO24 = 16777216.0f, TWO20 = 1048576.0f;
     constexpr bool QLO = std::is_same<IN, float>::value;      // q needs a low fp16 part
+    constexpr bool DYN = NW == 8;                             // pairs from the LDS counter
     const float sm_log2 = p2 * rs;                            // exact: p2 is a power of two
     static_assert(NW == 2 || NW == 4 || NW == 8, "the tail splits 16 heads over 2 NW lane halves");
     static_assert(ST == 1 || ST == 2, "one or two page streams");
@@ -587,7 +589,14 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     const int lane = threadIdx.x & (WAVE - 1);
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);   // wave-uniform: scalar page loop
     const int r16 = lane & 15, q = lane >> 4;
-    const int s = blockIdx.x, h = blockIdx.y;
+    // with seq_order, workgroups go out sequence by sequence (all kv heads of one, then the next) in
+    // the given order: the hardware starts workgroups in linear order
+    int s = blockIdx.x, h = blockIdx.y;
+    if (seq_order != nullptr) {
+        const int L = blockIdx.x + gridDim.x * blockIdx.y;
+        s = seq_order[L / H];
+        h = L % H;
+    }
     const int z = blockIdx.z % NS, gc = blockIdx.z / NS, g0 = gc * 16;
     const int Gc = min(16, G - g0);
 
@@ -614,9 +623,12 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     for (int dt = 0; dt < DT; ++dt) o[dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     float m_run = -__builtin_inff(), l_run = 0.0f, vb_run = 0.0f;
 
-    // The split's pages go out in pairs (k: pages 2k, 2k + 1 of the window) from a counter in LDS,
-    // over windows of WIN pages whose block ids are first copied to an LDS table: waves the hardware
-    // runs more often simply take more pairs, and all waves finish together. A wave holds two pairs,
+    // The split's pages go out in pairs (k: pages 2k, 2k + 1 of the window), over windows of WIN pages
+    // whose block ids are first copied to an LDS table. With 8 waves (two per SIMD, which the hardware
+    // does not run at the same rate) the pairs come from a counter in LDS: the waves run more often
+    // simply take more pairs and all finish together, at the price of bitwise reproducibility (which
+    // wave accumulates which page varies from run to run; results agree to rounding). With 2 or 4
+    // waves, wave w takes pairs w, w + NW, ... (deterministic). A wave holds two pairs,
     // in slots (0, 1) and (2, 3): one is consumed while the other is in flight. A wave's pairs only
     // grow, so once the pair it would consume is past the window's end, so is the one in flight. Each
     // pair issue is 2 R::DMA instructions, also for a pair past the end (an empty buffer range: no
@@ -674,8 +686,8 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     {                                                                                              \
         if ((P) >= pairs) break;                                                                   \
         KUSH_WAIT_VM(2 * R::DMA);                                                                  \
-        int nx = 0;                                                                                \
-        if (lane == 0) nx = (int)__builtin_amdgcn_atomic_inc32(&pair_ctr, ~0u, __ATOMIC_RELAXED, "workgroup"); \
+        int nx = (P) + 2 * NW;                           /* static: this wave's pair after next */  \
+        if (DYN && lane == 0) nx = (int)__builtin_amdgcn_atomic_inc32(&pair_ctr, ~0u, __ATOMIC_RELAXED, "workgroup"); \
         int2 id2;                                                                                  \
         if constexpr (ST == 2) {                                                                   \
             float sv[8], kx;                                                                       \
@@ -909,12 +921,12 @@ template <int D, int BITS, typename IN, int NW>
 static int launch_decode(dim3 grid, hipStream_t stream, const void* q, void* out, const void* cache, int64_t bs,
                          int64_t hs, const void* tail_k, const int32_t* tail_idx, const int32_t* block_table,
                          const int32_t* seq_lens, int64_t bt_stride, int hkv, int group, float p2, float rs, int n_splits,
-                         float* part_ml, float* part_o, int32_t* sync) {
+                         float* part_ml, float* part_o, int32_t* sync, const int32_t* seq_order) {
     // two page streams whenever the heads of a kv head fit in half the MFMA columns
     auto kern = group <= 8 ? decode_kernel<D, BITS, IN, NW, 2> : decode_kernel<D, BITS, IN, NW, 1>;
     kern<<<grid, dim3(NW * WAVE), 0, stream>>>(
         (const IN*)q, (IN*)out, (const uint8_t*)cache, bs, hs, (const IN*)tail_k, tail_idx, block_table, seq_lens,
-        bt_stride, hkv, group, p2, rs, n_splits, part_ml, part_o, sync);
+        bt_stride, hkv, group, p2, rs, n_splits, part_ml, part_o, sync, seq_order);
     return kush_check_launch("kush_decode");
 }
 
@@ -926,7 +938,7 @@ extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const v
                            int64_t block_stride, int64_t head_stride, const void* tail_k, const int32_t* tail_idx,
                            const int32_t* block_table, const int32_t* seq_lens, int64_t bt_stride, int32_t hkv,
                            float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t* split_sync,
-                           int32_t waves, int32_t n_seqs, void* stream) {
+                           int32_t waves, const int32_t* seq_order, int32_t n_seqs, void* stream) {
     if (n_seqs < 0 || hkv <= 0 || group <= 0 || n_splits <= 0)
         return kush_fail(-2, "kush_decode: bad n_seqs %d / hkv %d / group %d / n_splits %d", n_seqs, hkv, group,
                          n_splits);
@@ -959,7 +971,7 @@ extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const v
         using IN = decltype(in);
         if (n_seqs == 0) return 0;
 #define KUSH_DECODE_ARGS grid, st, q, out, cache, block_stride, head_stride, tail_k, tail_idx, block_table, seq_lens, \
-                         bt_stride, hkv, group, p2, rs, n_splits, part_ml, part_o, split_sync
+                         bt_stride, hkv, group, p2, rs, n_splits, part_ml, part_o, split_sync, seq_order
         // the largest of the requested, 4 and 2 waves whose rings fit in LDS
         if (waves >= 8) {
             if constexpr (decode_fits<D, BITS, 8>()) return launch_decode<D, BITS, IN, 8>(KUSH_DECODE_ARGS);

@@ -241,3 +241,49 @@ def test_write_rows_any_stride(bits, dtype):
         oc.append(ka, va, sl, tail_idx.cpu(), cache, bt.cpu(), tail_k, pos_offset=-1, advance=False)
     assert torch.equal(c0, cache)
     assert torch.equal(t0.float(), tail_k)
+
+
+@pytest.mark.parametrize("ns", [1, 3])
+def test_sequence_order_does_not_change_results(ns):
+    """Decode with a start order for the sequences (longest first, and a random permutation) gives
+    the same bytes as the natural order, with and without split-K."""
+    torch.manual_seed(11)
+    lens = [5, 300, 64, 1000, 33, 0, 129, 700]
+    S, H, G, D, bits, dtype = len(lens), 2, 4, 128, 4, torch.bfloat16
+    ops = kk.Ops(torch.device(DEV), D, bits, G, dtype)
+    pages = -(-max(lens) // PAGE)
+    cache = torch.zeros(S * pages, H, kk.record_bytes(D, bits), dtype=torch.uint8, device=DEV)
+    bt = torch.randperm(S * pages, dtype=torch.int32).view(S, pages).to(DEV)
+    tail_k = torch.zeros(S, H, PAGE, D, dtype=dtype, device=DEV)
+    tail_idx = torch.arange(S, dtype=torch.int32, device=DEV)
+    n = sum(lens)
+    k = torch.randn(n, H, D, dtype=dtype, device=DEV)
+    v = torch.randn(n, H, D, dtype=dtype, device=DEV)
+    qsl = torch.tensor([0] + [sum(lens[:i + 1]) for i in range(S)], dtype=torch.int32, device=DEV)
+    seq_lens = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    jobs = [(s, p) for s in range(S) for p in range(-(-lens[s] // PAGE))]
+    js = torch.tensor([j[0] for j in jobs], dtype=torch.int32, device=DEV)
+    jp = torch.tensor([j[1] for j in jobs], dtype=torch.int32, device=DEV)
+    ops.write(k, v, qsl, seq_lens, tail_idx, js, jp, cache, bt, tail_k)
+    q = torch.randn(S, H * G, D, dtype=dtype, device=DEV)
+    work = torch.empty(S * H * ns * G * (D + 2), dtype=torch.float32, device=DEV)
+
+    def run(order):
+        out = torch.empty_like(q)
+        ops.decode(q, out, cache, bt, seq_lens, tail_idx, tail_k, D ** -0.5, ns, work, order=order)
+        torch.cuda.synchronize()
+        return out.cpu()
+
+    ref = run(None)                          # 4 waves by the policy: pages go to waves statically
+    longest = torch.tensor(sorted(range(S), key=lambda i: -lens[i]), dtype=torch.int32, device=DEV)
+    for order in (longest, torch.randperm(S).to(torch.int32).to(DEV)):
+        assert torch.equal(run(order), ref)
+    # 8 waves hand pairs out dynamically: equal to rounding, not bit for bit
+    out8 = torch.empty_like(q)
+    ops.decode(q, out8, cache, bt, seq_lens, tail_idx, tail_k, D ** -0.5, ns, work, waves=8, order=longest)
+    assert (out8.float().cpu() - ref.float()).abs().max().item() <= out_tol(ref.float(), dtype)
+    o = OracleOps("cpu", D, bits, G)
+    want = torch.empty(q.shape)
+    o.decode(q.float().cpu(), want, cache.cpu(), bt.cpu(), seq_lens.cpu(), tail_idx.cpu(), tail_k.float().cpu(),
+             D ** -0.5)
+    assert (ref.float() - want).abs().max().item() <= out_tol(want, dtype)
