@@ -91,6 +91,14 @@ int kush_decode(int head_dim, int bits, int group, int dtype, const void* q, voi
                 float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t* split_sync, int32_t waves,
                 const int32_t* seq_order, int32_t n_seqs, void* stream);
 
+/* Walsh-Hadamard rotation of rows of head_dim elements: y[r] = fwht(x[r]) for r < rows (row strides
+ * in elements; y may alias x), in the canonical order — butterflies at strides 1, 2, ..., D/2, then
+ * one fp32 multiply by 1/sqrt(D), rounded once to dtype — bit-identical to the reference's CPU
+ * and GPU rotation. bits is not a parameter (any record format).
+ * Replaces kush_fwht (gpu.mojo:95-112) as launched by Ops.fwht (_ops.py:104-126). */
+int kush_fwht(int head_dim, int dtype, const void* x, void* y, int64_t x_row_stride, int64_t y_row_stride,
+              int64_t rows, void* stream);
+
 /* Merge kush_decode's split partials into out [n_seqs][hkv*group][head_dim].
  * Replaces kush_combine (gpu.mojo:469-491) as launched by Ops.decode (_ops.py:212-213). */
 int kush_combine(int head_dim, int group, int dtype, void* out, const float* part_ml, const float* part_o,

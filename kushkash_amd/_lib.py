@@ -32,6 +32,8 @@ SIGNATURES = {
                     _P, _I32, _P, _I32, _P],
     # head_dim, group, dtype, out, part_ml, part_o, n_splits, hkv, n_seqs, stream
     "kush_combine": [_I32, _I32, _I32, _P, _P, _P, _I32, _I32, _I32, _P],
+    # head_dim, dtype, x, y, x_row_stride, y_row_stride, rows, stream
+    "kush_fwht": [_I32, _I32, _P, _P, _I64, _I64, _I64, _P],
     "kush_last_error": [],
     "kush_abi_version": [],
 }

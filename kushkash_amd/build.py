@@ -14,7 +14,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 LIB = PKG / "libkushhip.so"
-SOURCES = ("kush_capi.hip", "kush_write.hip", "kush_decode.hip")
+SOURCES = ("kush_capi.hip", "kush_write.hip", "kush_decode.hip", "kush_rotate.hip")
 ARCH = "gfx950"
 
 FLAGS = [

@@ -1,0 +1,46 @@
+"""The gfx950 Walsh-Hadamard rotation (needs an MI355X): bit-identical to the oracle's canonical
+order (the reference's CPU kernel, restated) for every head_dim and dtype, in place and out of
+place, and an involution up to rounding (reference: tests/test_gpu.py:203-218,
+tests/test_cpu.py:429-451)."""
+import pytest
+import torch
+
+import kushkash_amd as kk
+from kushkash_amd._ops import fwht_reference, hadamard
+from oracle.cpu_ops import OracleOps
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_fwht_gpu_matches_oracle(D, dtype):
+    g = torch.Generator().manual_seed(D)
+    # 1001 rows: a partial last workgroup; magnitudes 1e-3 .. 1e3 (inputs exact in dtype)
+    x = (torch.randn(1001, D, generator=g) * torch.logspace(-3, 3, 1001)[:, None]).to(dtype)
+    cpu = OracleOps("cpu", D, 4, 1).fwht(x.float().contiguous())
+    assert torch.equal(cpu, fwht_reference(x.float()))
+    ops = kk.Ops(torch.device(DEV), D, 4, 1, dtype)
+    y = ops.fwht(x.to(DEV)).cpu()
+    want = cpu.to(dtype)
+    bad = (y.float().view(torch.int32) != want.float().view(torch.int32)) if dtype == torch.float32 else (y != want)
+    assert not bad.any(), f"{bad.sum().item()} of {bad.numel()} values differ from the oracle"
+    xc = x.to(DEV)
+    assert torch.equal(ops.fwht(xc, out=xc).cpu(), y)                  # in place
+    assert ops.fwht(x[:0].to(DEV)).shape == (0, D)
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_fwht_gpu_is_the_hadamard_rotation(D):
+    ops = kk.Ops(torch.device(DEV), D, 4, 1, torch.float32)
+    x = torch.randn(3, 5, D, device=DEV)                               # any leading shape
+    y = ops.fwht(x)
+    dense = x.double().reshape(-1, D) @ hadamard(D, DEV).double()
+    assert ((y.reshape(-1, D).double() - dense).norm(dim=1) <= 1e-6 * dense.norm(dim=1)).all()
+    back = ops.fwht(y)
+    assert ((back - x).norm(dim=-1) <= 1e-6 * x.norm(dim=-1)).all()   # H @ H = I
+    with pytest.raises(ValueError):
+        ops.fwht(x.double())
+    with pytest.raises(ValueError):
+        ops.fwht(x.transpose(0, 1))
