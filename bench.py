@@ -27,6 +27,9 @@ default, c2, is the headline):
             5% of channels), split-K by the Ops.splits policy (--sweep adds NS 64, 128, 256 ...)
   c4-write  the chunked-prefill write of 2,048 new tokens per sequence of that layer (8 x 2,048 tokens,
             two ordered launches), quantize-and-pack bytes read + written
+  c4-unpack the packed-prefill unpack of one sequence of that layer (131,072 history tokens = 4,096
+            full pages dequantized, 2,048 new rows copied; kp / vp [133,120, 8, 128] bf16), records
+            read + rows written (--rot also rotates the history back)
 """
 from __future__ import annotations
 
@@ -68,7 +71,8 @@ def parse_args(argv=None):
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="instead of the decode, run --steps device-to-device copies of MIB MiB: the plain copy "
                          "kernel of known size that scales rocprofv3's FETCH_SIZE / WRITE_SIZE")
-    ap.add_argument("--config", default="c2", choices=("c2", "c3", "c4", "c4-write"),
+    ap.add_argument("--rot", action="store_true", help="c4-unpack: rotate history rows back (canonical FWHT)")
+    ap.add_argument("--config", default="c2", choices=("c2", "c3", "c4", "c4-write", "c4-unpack"),
                     help="which configuration to measure (c2: the headline line)")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "decode_c2_traffic.md"),
                     help="rocprofv3 counter summary whose 'traffic_bytes_per_launch' fills roofline.traffic")
@@ -456,6 +460,81 @@ def bench_c4_write(a) -> None:
           f"write_kernel<{D},{bits},bf16> x 2 (mode 0, mode 1)")
 
 
+def bench_c4_unpack(a) -> None:
+    """C4 packed-prefill unpack: the group of one sequence, [4,096 history pages | 2,048 new rows], as
+    the vLLM backend builds it before flash-attn (kushkash/vllm/backend.py:837-856). Two record pools
+    (310 MB) alternate across steps; kp / vp (545 MB) are rewritten every step."""
+    from kushkash_amd._ops import Ops, record_bytes
+    dev = "cuda:0"
+    Hkv, D, bits, N, T, P = 8, 128, 4, 131072, 2048, 2
+    dtype = torch.bfloat16
+    ops = Ops(torch.device(dev), D, bits, 1, dtype)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    pools = [ragged_cache(ops, [N], 0, Hkv, 4.0, 0.05, gen, dev) for _ in range(P)]
+    pages = N // PAGE
+    rows = N + T
+    page_dst = torch.arange(pages, dtype=torch.int32, device=dev) * PAGE
+    new_dst = torch.arange(N, rows, dtype=torch.int32, device=dev)
+    none = torch.zeros(0, dtype=torch.int32, device=dev)
+    k_new = torch.randn(T, Hkv, D, generator=gen, device=dev).to(dtype)
+    v_new = torch.randn(T, Hkv, D, generator=gen, device=dev).to(dtype)
+    kp = torch.empty(rows, Hkv, D, dtype=dtype, device=dev)
+    vp = torch.empty_like(kp)
+    blks = [p[1][0, :pages].contiguous() for p in pools]
+
+    def step(i):
+        cache, _, tail_k, _ = pools[i % P]
+        ops.unpack(cache, blks[i % P], page_dst, none, none, tail_k, k_new, v_new, new_dst, kp, vp, a.rot)
+
+    ops.validate = True                        # indices checked once, outside the timed graph
+    step(0)
+    ops.validate = False
+    ms = time_graph(step, a.steps, a.warmup)
+    RB = record_bytes(D, bits)
+    alg = pages * Hkv * RB + 2 * rows * Hkv * D * 2 + 2 * T * Hkv * D * 2
+    extra = None
+    if not a.no_cpu_baseline:
+        extra = {"cpu_baseline": cpu_baseline_unpack(pools[0], blks[0], k_new, v_new, D, bits, Hkv, a.rot,
+                                                     min(a.cpu_seconds, 10.0))}
+    _line("prefill-unpack us/step + achieved HBM GB/s (% peak), int4, 131k history + 2048 new", ms * 1e3, alg,
+          {"workload": f"C4 packed-prefill unpack: 1 x ({N} history + {T} new) tokens, {Hkv} kv heads, D {D}, "
+                       f"int{bits}, bf16 kp / vp, rot {int(a.rot)}", "global_batch": 1, "seq_len": rows},
+          f"unpack_kernel<{D},{bits},bf16,vec> ({pages} page items + {T // PAGE} new-row items) x {Hkv} heads",
+          extra)
+
+
+def cpu_baseline_unpack(pool, blk, k_new, v_new, D, bits, Hkv, rot, budget_s: float):
+    """The oracle's unpack (C restatement of the reference CPU kernel, fp32, one thread) over a
+    bounded sample of the same group: its first n history pages, no new rows."""
+    from kushkash_amd._ops import record_bytes
+    from oracle import cpu_ops
+    cache, _, tail_k, _ = pool
+    ops = cpu_ops.OracleOps("cpu", D, bits, 1)
+    cache_h, blk_h = cache.cpu(), blk.cpu()
+    tail_h = tail_k.float().cpu()
+    none = torch.zeros(0, dtype=torch.int32)
+    empty = torch.zeros(0, Hkv, D)
+
+    def run(n):
+        kp = torch.empty(n * PAGE, Hkv, D)
+        vp = torch.empty_like(kp)
+        dst = torch.arange(n, dtype=torch.int32) * PAGE
+        t0 = time.perf_counter()
+        ops.unpack(cache_h, blk_h[:n].contiguous(), dst, none, none, tail_h, empty, empty, none, kp, vp, rot)
+        return time.perf_counter() - t0
+
+    per_page = run(16) / 16
+    n = int(min(blk_h.numel(), max(16, budget_s / 4 / max(per_page, 1e-9))))
+    run(n)
+    reps = max(1, min(10, int(budget_s / max(per_page * n, 1e-9))))
+    med = sorted(run(n) for _ in range(reps))[reps // 2]
+    alg = n * Hkv * record_bytes(D, bits) + 2 * n * PAGE * Hkv * D * 4
+    return {"value": round(alg / med / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{n} of {blk_h.numel()} history pages of the same group (all {Hkv} kv heads, fp32 kp / vp, "
+                      f"rot {int(rot)}), median of {reps} runs after 1 warm-up; {med * 1e6 / n:.1f} us per page"}
+
+
 def main(argv=None):
     a = parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -469,7 +548,7 @@ def main(argv=None):
         copy_calibration(a)
         return
     if a.config != "c2":
-        {"c3": bench_c3, "c4": bench_c4, "c4-write": bench_c4_write}[a.config](a)
+        {"c3": bench_c3, "c4": bench_c4, "c4-write": bench_c4_write, "c4-unpack": bench_c4_unpack}[a.config](a)
         return
     w = make_workload(a, dev)
     ns = a.splits or w["ops"].splits(w["B"], w["Hkv"], w["N"] // PAGE)

@@ -99,6 +99,22 @@ int kush_decode(int head_dim, int bits, int group, int dtype, const void* q, voi
 int kush_fwht(int head_dim, int dtype, const void* x, void* y, int64_t x_row_stride, int64_t y_row_stride,
               int64_t rows, void* stream);
 
+/* Build one packed-prefill group's keys and values, kp / vp [rows][hkv][head_dim] in dtype
+ * (contiguous), in one launch: full history pages (record of block page_blk[i] -> rows
+ * page_dst[i] + 0..31), partial pages (tail_info[3i..3i+2] = first row, tokens 1..32, tail slot:
+ * K rows from tail_k [slots][hkv][32][head_dim], V rows from the record of block tail_blk[i]) and
+ * the new chunk (row j of k_new / v_new, element row strides k_stride / v_stride, head stride
+ * head_dim -> row new_dst[j]). Dequantization is fma(code, scale, bias) in fp32; rot != 0 rotates
+ * history rows back (canonical Walsh-Hadamard) before the one rounding to dtype; new rows are
+ * copied. Rows no entry names are left untouched. Indices are not bounds-checked (the caller's
+ * contract, as in the reference).
+ * Replaces kush_unpack (gpu.mojo:303-375) as launched by Ops.unpack (_ops.py:128-180). */
+int kush_unpack(int head_dim, int bits, int dtype, const void* cache, int64_t block_stride, int64_t head_stride,
+                int32_t hkv, const int32_t* page_blk, const int32_t* page_dst, int64_t n_pages,
+                const int32_t* tail_blk, const int32_t* tail_info, int64_t n_tail, const void* tail_k,
+                const void* k_new, const void* v_new, int64_t k_stride, int64_t v_stride, const int32_t* new_dst,
+                int64_t n_new, void* kp, void* vp, int32_t rot, void* stream);
+
 /* Merge kush_decode's split partials into out [n_seqs][hkv*group][head_dim].
  * Replaces kush_combine (gpu.mojo:469-491) as launched by Ops.decode (_ops.py:212-213). */
 int kush_combine(int head_dim, int group, int dtype, void* out, const float* part_ml, const float* part_o,
@@ -108,7 +124,7 @@ int kush_combine(int head_dim, int group, int dtype, void* out, const float* par
  * reference raises the driver's error string directly (_cuda.py:39-43). */
 const char* kush_last_error(void);
 
-/* ABI revision of this header (3). No reference counterpart. */
+/* ABI revision of this header (4). No reference counterpart. */
 int kush_abi_version(void);
 
 #ifdef __cplusplus

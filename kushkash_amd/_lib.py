@@ -14,7 +14,7 @@ from pathlib import Path
 import torch   # noqa: F401  -- loads torch's HIP runtime first; the library binds to it (same soname)
 
 LIB = Path(__file__).resolve().parent / "libkushhip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _P, _I32, _I64, _F = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float
 SIGNATURES = {
@@ -34,6 +34,8 @@ SIGNATURES = {
     "kush_combine": [_I32, _I32, _I32, _P, _P, _P, _I32, _I32, _I32, _P],
     # head_dim, dtype, x, y, x_row_stride, y_row_stride, rows, stream
     "kush_fwht": [_I32, _I32, _P, _P, _I64, _I64, _I64, _P],
+    "kush_unpack": [_I32, _I32, _I32, _P, _I64, _I64, _I32, _P, _P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _I64, _P,
+                    _I64, _P, _P, _I32, _P],
     "kush_last_error": [],
     "kush_abi_version": [],
 }

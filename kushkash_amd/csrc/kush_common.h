@@ -86,12 +86,63 @@ template <>
 __device__ __forceinline__ float from_f32<float>(float x) { return x; }
 template <>
 __device__ __forceinline__ _Float16 from_f32<_Float16>(float x) { return (_Float16)x; }   // RNE
+// RNE to bf16 (overflow to infinity, NaN stays NaN): gfx950's v_cvt_pk_bf16_f32, which converts
+// two values per instruction when two conversions meet in one 32-bit word
 template <>
 __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) {
-    uint32_t u = __float_as_uint(x);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return bf16_t{(uint16_t)((u >> 16) | 0x40u)};   // quiet NaN
-    u += 0x7fffu + ((u >> 16) & 1u);                                                     // RNE
-    return bf16_t{(uint16_t)(u >> 16)};
+    return bf16_t{__builtin_bit_cast(uint16_t, (__bf16)x)};
+}
+
+// 8 consecutive elements as fp32: 16-byte loads when the rows are 16-byte aligned, else per element
+template <bool VEC, typename IN>
+__device__ __forceinline__ void get8(const IN* p, float (&x)[8]) {
+    if constexpr (VEC) {
+        load8(p, x);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = to_f32(p[j]);
+    }
+}
+
+template <bool VEC, typename IN>
+__device__ __forceinline__ void copy8(IN* dst, const IN* src) {
+    if constexpr (VEC && sizeof(IN) == 2) {
+        *reinterpret_cast<u4*>(dst) = *reinterpret_cast<const u4*>(src);
+    } else if constexpr (VEC) {
+        reinterpret_cast<u4*>(dst)[0] = reinterpret_cast<const u4*>(src)[0];
+        reinterpret_cast<u4*>(dst)[1] = reinterpret_cast<const u4*>(src)[1];
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dst[j] = src[j];
+    }
+}
+
+// 8 fp32 values rounded to IN at dst: 16-byte stores when dst is 16-byte aligned, else per element.
+// The opaque copy keeps the compiler from folding a preceding fp32 multiply or fma into an fp16
+// conversion (v_fma_mix*_f16 round once, straight to fp16; these kernels round to fp32 first, then
+// to IN, as the reference does, and at fp16 ties the two differ).
+template <typename IN>
+__device__ __forceinline__ IN store_rounded(float x) {
+    asm volatile("" : "+v"(x));
+    return from_f32<IN>(x);
+}
+
+template <bool VEC, typename IN>
+__device__ __forceinline__ void put8(IN* dst, const float* x) {
+    if constexpr (VEC && sizeof(IN) == 4) {
+        reinterpret_cast<f4*>(dst)[0] = f4{x[0], x[1], x[2], x[3]};
+        reinterpret_cast<f4*>(dst)[1] = f4{x[4], x[5], x[6], x[7]};
+    } else if constexpr (VEC) {
+        u4 w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            w[i] = (uint32_t)__builtin_bit_cast(uint16_t, store_rounded<IN>(x[2 * i])) |
+                   ((uint32_t)__builtin_bit_cast(uint16_t, store_rounded<IN>(x[2 * i + 1])) << 16);
+        *reinterpret_cast<u4*>(dst) = w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dst[j] = store_rounded<IN>(x[j]);
+    }
 }
 
 __device__ __forceinline__ uint16_t f16_bits(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }

@@ -23,30 +23,6 @@ struct Rows {
     static constexpr int PASSES = RP >= PAGE ? 1 : PAGE / RP;
 };
 
-// 8 consecutive elements as fp32: 16-byte loads when the rows are 16-byte aligned, else per element
-template <bool VEC, typename IN>
-__device__ __forceinline__ void get8(const IN* p, float (&x)[8]) {
-    if constexpr (VEC) {
-        load8(p, x);
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = to_f32(p[j]);
-    }
-}
-
-template <bool VEC, typename IN>
-__device__ __forceinline__ void copy8(IN* dst, const IN* src) {
-    if constexpr (VEC && sizeof(IN) == 2) {
-        *reinterpret_cast<u4*>(dst) = *reinterpret_cast<const u4*>(src);
-    } else if constexpr (VEC) {
-        reinterpret_cast<u4*>(dst)[0] = reinterpret_cast<const u4*>(src)[0];
-        reinterpret_cast<u4*>(dst)[1] = reinterpret_cast<const u4*>(src)[1];
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) dst[j] = src[j];
-    }
-}
-
 // codes of the 16 values of a thread (x[0..8): dims 8c.., x[8..16): dims D/2 + 8c..) -> the bytes
 // they make: int4 byte i = code(x[i]) & 15 | (code(x[8 + i]) & 15) << 4 (row bytes 8c + i, in lo);
 // int8 bytes in dim order (row bytes 8c + i in lo, D/2 + 8c + i in hi). The codes stay floats

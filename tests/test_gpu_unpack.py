@@ -1,0 +1,105 @@
+"""The gfx950 packed-prefill unpack (needs an MI355X): bit-identical to the oracle's CPU kernel
+(the reference's, restated) rounded to the output dtype, for every head_dim, bits, dtype and rot,
+with rows no entry names left untouched (reference: tests/test_gpu.py:221-240). Also a large
+group across all the shape classes a serving step makes (hundreds of shuffled pages, several kv
+heads, partial pages of every length, a ragged new chunk), the per-element path for unaligned
+rows, and index validation before any launch."""
+import pytest
+import torch
+
+import kushkash_amd as kk
+from _unpack_fixture import INDEX_NAMES, make_group
+from oracle.cpu_ops import OracleOps
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+BITS_OF = {torch.float32: torch.int32, torch.float16: torch.int16, torch.bfloat16: torch.int16}
+
+
+def oracle_unpack(c, D, bits, rot, dtype):
+    """The oracle's fp32 kp, vp rounded once to dtype (the kernels round fp32 -> dtype once)."""
+    shape = (c["rows"], c["H"], D)
+    kp, vp = torch.full(shape, float("nan")), torch.full(shape, float("nan"))
+    args = [c[n].float() if n in ("tail_k", "k_new", "v_new") else c[n] for n in INDEX_NAMES]
+    OracleOps("cpu", D, bits, 1).unpack(c["records"], *args, kp, vp, rot)
+    return kp.to(dtype), vp.to(dtype)
+
+
+def gpu_unpack(c, D, bits, rot, dtype, k_new=None, v_new=None, kp=None, vp=None):
+    shape = (c["rows"], c["H"], D)
+    kp = torch.full(shape, float("nan"), dtype=dtype, device=DEV) if kp is None else kp
+    vp = torch.full(shape, float("nan"), dtype=dtype, device=DEV) if vp is None else vp
+    args = {n: c[n].to(DEV) for n in INDEX_NAMES}
+    if k_new is not None:
+        args["k_new"], args["v_new"] = k_new, v_new
+    kk.Ops(torch.device(DEV), D, bits, 1, dtype).unpack(c["records"].to(DEV), *[args[n] for n in INDEX_NAMES],
+                                                        kp, vp, rot)
+    return kp.cpu(), vp.cpu()
+
+
+def assert_same(c, got, want, dtype):
+    written = torch.ones(c["rows"], dtype=torch.bool)
+    written[torch.tensor(c["gaps"])] = False
+    for g, w in zip(got, want):
+        a, b = g[written].view(BITS_OF[dtype]), w[written].view(BITS_OF[dtype])
+        assert torch.equal(a, b), f"{(a != b).sum().item()} of {a.numel()} values differ from the oracle"
+        assert g[~written].isnan().all(), "a row no entry names was written"
+
+
+@pytest.mark.parametrize("D,bits", [(64, 4), (128, 4), (256, 4), (64, 8), (128, 8), (256, 8)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rot", [False, True])
+def test_unpack_gpu_matches_oracle(D, bits, dtype, rot):
+    c = make_group(D, bits, dtype, seed=D + bits)
+    assert_same(c, gpu_unpack(c, D, bits, rot, dtype), oracle_unpack(c, D, bits, rot, dtype), dtype)
+
+
+@pytest.mark.parametrize("rot", [False, True])
+def test_unpack_gpu_large_group(rot):
+    """8 kv heads, 300 shuffled full pages, partial pages of 1..31 tokens, 700 new rows in runs."""
+    D, bits, dtype = 128, 4, torch.bfloat16
+    c = make_group(D, bits, dtype, seed=11, H=8, n_pages=300, tail_tokens=tuple(range(1, 32, 2)),
+                   new_runs=(1, 31, 32, 33, 603), slots=24)
+    assert_same(c, gpu_unpack(c, D, bits, rot, dtype), oracle_unpack(c, D, bits, rot, dtype), dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_unpack_gpu_unaligned_rows(dtype):
+    """k_new / v_new rows one element apart from 16-byte alignment, kp / vp starting one element
+    into their buffer: the per-element path gives the same bits."""
+    D, bits = 128, 8
+    c = make_group(D, bits, dtype, seed=5, H=4)
+    n, H, rows = c["k_new"].shape[0], c["H"], c["rows"]
+
+    def odd_rows(x):                                   # [n, H, D] with row stride H * D + 1
+        buf = torch.empty(n, H * D + 1, dtype=dtype, device=DEV)
+        buf[:, :H * D] = x.reshape(n, H * D).to(DEV)
+        return buf[:, :H * D].view(n, H, D)
+
+    def offset_out():
+        buf = torch.full((rows * H * D + 1,), float("nan"), dtype=dtype, device=DEV)
+        return buf[1:].view(rows, H, D)
+
+    k_new, v_new = odd_rows(c["k_new"]), odd_rows(c["v_new"])
+    assert k_new.stride(0) == H * D + 1
+    got = gpu_unpack(c, D, bits, True, dtype, k_new, v_new, offset_out(), offset_out())
+    assert_same(c, got, oracle_unpack(c, D, bits, True, dtype), dtype)
+
+
+def test_unpack_gpu_validates_indices_before_launch():
+    D, bits, dtype = 64, 4, torch.bfloat16
+    c = make_group(D, bits, dtype)
+    ops = kk.Ops(torch.device(DEV), D, bits, 1, dtype, validate=True)
+    shape = (c["rows"], c["H"], D)
+    kp = torch.zeros(shape, dtype=dtype, device=DEV)
+    args = {n: c[n].to(DEV) for n in INDEX_NAMES}
+    args["page_blk"] = args["page_blk"] + c["records"].shape[0]
+    with pytest.raises(ValueError, match="page_blk"):
+        ops.unpack(c["records"].to(DEV), *[args[n] for n in INDEX_NAMES], kp, kp.clone(), False)
+    assert not kp.any()
+    empty = torch.zeros(0, dtype=torch.int32, device=DEV)             # nothing to do: no launch
+    none = torch.zeros(0, c["H"], D, dtype=dtype, device=DEV)
+    ops.unpack(c["records"].to(DEV), empty, empty, empty, empty, args["tail_k"], none, none, empty, kp, kp, False)
+    with pytest.raises(ValueError, match="must be torch.bfloat16"):
+        ops.unpack(c["records"].to(DEV), *[args[n] if n != "k_new" else args[n].float() for n in INDEX_NAMES],
+                   kp, kp.clone(), False)
