@@ -30,6 +30,8 @@ default, c2, is the headline):
   c4-unpack the packed-prefill unpack of one sequence of that layer (131,072 history tokens = 4,096
             full pages dequantized, 2,048 new rows copied; kp / vp [133,120, 8, 128] bf16), records
             read + rows written (--rot also rotates the history back)
+  c4-fwht   the Walsh-Hadamard rotation (Ops.fwht) of that group's keys in place: 133,120 tokens x 8
+            kv heads = 1,064,960 rows of D 128 bf16, read and written
 """
 from __future__ import annotations
 
@@ -72,7 +74,7 @@ def parse_args(argv=None):
                     help="instead of the decode, run --steps device-to-device copies of MIB MiB: the plain copy "
                          "kernel of known size that scales rocprofv3's FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--rot", action="store_true", help="c4-unpack: rotate history rows back (canonical FWHT)")
-    ap.add_argument("--config", default="c2", choices=("c2", "c3", "c4", "c4-write", "c4-unpack"),
+    ap.add_argument("--config", default="c2", choices=("c2", "c3", "c4", "c4-write", "c4-unpack", "c4-fwht"),
                     help="which configuration to measure (c2: the headline line)")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "decode_c2_traffic.md"),
                     help="rocprofv3 counter summary whose 'traffic_bytes_per_launch' fills roofline.traffic")
@@ -500,7 +502,8 @@ def bench_c4_unpack(a) -> None:
     _line("prefill-unpack us/step + achieved HBM GB/s (% peak), int4, 131k history + 2048 new", ms * 1e3, alg,
           {"workload": f"C4 packed-prefill unpack: 1 x ({N} history + {T} new) tokens, {Hkv} kv heads, D {D}, "
                        f"int{bits}, bf16 kp / vp, rot {int(a.rot)}", "global_batch": 1, "seq_len": rows},
-          f"unpack_kernel<{D},{bits},bf16,vec> ({pages} page items + {T // PAGE} new-row items) x {Hkv} heads",
+          f"unpack_kernel<{D},{bits},bf16,vec> ({pages} page items + {T // PAGE} new-row items) x {Hkv} heads, "
+          f"4 tasks per workgroup",
           extra)
 
 
@@ -535,6 +538,23 @@ def cpu_baseline_unpack(pool, blk, k_new, v_new, D, bits, Hkv, rot, budget_s: fl
                       f"rot {int(rot)}), median of {reps} runs after 1 warm-up; {med * 1e6 / n:.1f} us per page"}
 
 
+def bench_c4_fwht(a) -> None:
+    """Ops.fwht over one C4 packed group's keys, in place (two alternating 272 MB buffers)."""
+    from kushkash_amd._ops import Ops
+    dev = "cuda:0"
+    Hkv, D, rows = 8, 128, 131072 + 2048
+    dtype = torch.bfloat16
+    ops = Ops(torch.device(dev), D, 4, 1, dtype)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    xs = [torch.randn(rows * Hkv, D, generator=gen, device=dev).to(dtype) for _ in range(2)]
+    ms = time_graph(lambda i: ops.fwht(xs[i % 2], out=xs[i % 2]), a.steps, a.warmup)
+    alg = 2 * rows * Hkv * D * 2
+    _line("fwht us/step + achieved HBM GB/s (% peak), 1,064,960 rows of D 128 bf16", ms * 1e3, alg,
+          {"workload": f"C4 key rotation: {rows} tokens x {Hkv} kv heads, D {D}, bf16, in place", "rows": rows * Hkv},
+          f"fwht_kernel<{D},bf16> (one wave per row)")
+
+
 def main(argv=None):
     a = parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -548,7 +568,8 @@ def main(argv=None):
         copy_calibration(a)
         return
     if a.config != "c2":
-        {"c3": bench_c3, "c4": bench_c4, "c4-write": bench_c4_write, "c4-unpack": bench_c4_unpack}[a.config](a)
+        {"c3": bench_c3, "c4": bench_c4, "c4-write": bench_c4_write, "c4-unpack": bench_c4_unpack,
+         "c4-fwht": bench_c4_fwht}[a.config](a)
         return
     w = make_workload(a, dev)
     ns = a.splits or w["ops"].splits(w["B"], w["Hkv"], w["N"] // PAGE)

@@ -2,11 +2,10 @@
 // (kushkash/kush/quant.mojo:90-110, GPU butterflies gpu.mojo:57-93): butterflies at strides
 // 1, 2, ..., D/2 in that order (of each pair, the element with the stride bit set becomes
 // partner - self, the other self + partner), then one fp32 multiply by 1/sqrt(D). Every add is an
-// exact-order fp32 add, so any data layout that keeps the stage order gives the same bits; two
-// layouts are used:
-//   fwht_wave: one wave64 per row, lane l holds dims l + 64 i (i < D / 64);
-//   fwht_runs: D / 16 consecutive lanes per row, lane c of the row holds two runs of 8 dims,
-//              x[j] = dim 8c + j and x[8 + j] = dim D/2 + 8c + j (the record's int4 byte order).
+// exact-order fp32 add, so any data layout that keeps the stage order gives the same bits. The
+// layout here (fwht_runs): D / 16 consecutive lanes per row, lane c of the row holds two runs of 8
+// dims, x[j] = dim 8c + j and x[8 + j] = dim D/2 + 8c + j (the record's int4 byte order); strides
+// 1..4 stay in a run, 8..D/4 cross lanes (DPP within 16-lane rows), D/2 pairs the two runs.
 #pragma once
 
 #include "kush_common.h"
@@ -49,37 +48,6 @@ __device__ __forceinline__ void butterfly_lanes(float (&x)[N], int l) {
     const uint32_t sign = (l & M) ? 0x80000000u : 0u;
 #pragma unroll
     for (int i = 0; i < N; ++i) x[i] = lane_xor<M>(x[i]) + __uint_as_float(__float_as_uint(x[i]) ^ sign);
-}
-
-template <int D>
-__device__ __forceinline__ void fwht_wave(float (&v)[D / WAVE], int lane) {
-    constexpr int R = D / WAVE;
-    butterfly_lanes<1>(v, lane);                      // strides 1 .. 8: DPP within 16-lane rows
-    butterfly_lanes<2>(v, lane);
-    butterfly_lanes<4>(v, lane);
-    butterfly_lanes<8>(v, lane);
-#pragma unroll
-    for (int h = 16; h < WAVE; h <<= 1) {             // strides 16, 32: across rows
-        const bool upper = (lane & h) != 0;
-#pragma unroll
-        for (int i = 0; i < R; ++i) {
-            const float other = __shfl_xor(v[i], h, WAVE);
-            v[i] = upper ? other - v[i] : v[i] + other;
-        }
-    }
-#pragma unroll
-    for (int hb = 1; hb < R; hb <<= 1) {              // stride 64 hb: register bit hb
-#pragma unroll
-        for (int i = 0; i < R; ++i) {
-            if (i & hb) continue;
-            const float a = v[i], b = v[i + hb];
-            v[i] = a + b;
-            v[i + hb] = a - b;
-        }
-    }
-    const float sc = fwht_scale<D>();
-#pragma unroll
-    for (int i = 0; i < R; ++i) v[i] = v[i] * sc;
 }
 
 // c = the lane's index within its row's D / 16 lanes (those lanes are consecutive and aligned)

@@ -5,25 +5,29 @@
 // gpu.mojo:57-93), order kushkash/kush/quant.mojo:95-110, launched by Ops.fwht
 // (kushkash/_ops.py:104-126); bit-identical to the reference CPU path (cpu.mojo:83-107).
 //
-// One wave64 per row (fwht_wave): lane l holds row[l + 64 i], i < D / 64.
+// A streaming kernel (each row read once, written once): a row is D / 16 consecutive lanes, each
+// holding two runs of 8 dims (fwht_runs) moved with 16-byte accesses when the rows are 16-byte
+// aligned, so a 256-thread workgroup covers 4096 elements per pass.
 #include "kush_fwht.h"
 
 namespace kush {
 
-// grid (ceil(rows / 4)), block 256: one wave per row; y may alias x (a wave reads its whole row first)
-template <int D, typename IN>
+// grid (ceil(rows / (256 / (D / 16)))), block 256; y may alias x (a row's lanes read it whole
+// before any of them writes)
+template <int D, typename IN, bool VEC>
 __global__ __launch_bounds__(256) void fwht_kernel(const IN* x, IN* y, int64_t x_stride, int64_t y_stride,
                                                    int64_t rows) {
-    const int lane = threadIdx.x % WAVE;
-    const int64_t r = (int64_t)blockIdx.x * 4 + threadIdx.x / WAVE;
-    if (r >= rows) return;
-    constexpr int R = D / WAVE;
-    float v[R];
-#pragma unroll
-    for (int i = 0; i < R; ++i) v[i] = to_f32(x[r * x_stride + lane + WAVE * i]);
-    fwht_wave<D>(v, lane);
-#pragma unroll
-    for (int i = 0; i < R; ++i) y[r * y_stride + lane + WAVE * i] = store_rounded<IN>(v[i]);
+    constexpr int CG = D / 16, RPB = 256 / CG;
+    const int c = threadIdx.x % CG;
+    const int64_t r = (int64_t)blockIdx.x * RPB + threadIdx.x / CG;
+    if (r >= rows) return;                            // a row's lanes leave together
+    const int lo = 8 * c, hi = D / 2 + 8 * c;
+    float v[16];
+    get8<VEC>(x + r * x_stride + lo, reinterpret_cast<float(&)[8]>(v[0]));
+    get8<VEC>(x + r * x_stride + hi, reinterpret_cast<float(&)[8]>(v[8]));
+    fwht_runs<D>(v, c);
+    put8<VEC>(y + r * y_stride + lo, v);
+    put8<VEC>(y + r * y_stride + hi, v + 8);
 }
 
 }  // namespace kush
@@ -37,10 +41,15 @@ extern "C" int kush_fwht(int head_dim, int dtype, const void* x, void* y, int64_
         constexpr int D = decltype(dd)::value;
         using IN = decltype(in);
         if (rows == 0) return 0;
-        const int64_t blocks = (rows + 3) / 4;
+        constexpr int RPB = 256 / (D / 16);
+        const int64_t blocks = (rows + RPB - 1) / RPB;
         if (blocks > 0x7fffffff) return kush_fail(-2, "kush_fwht: %lld rows is too many", (long long)rows);
-        fwht_kernel<D, IN><<<dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream>>>(
-            (const IN*)x, (IN*)y, x_row_stride, y_row_stride, rows);
+        const uint64_t e = sizeof(IN);
+        const bool vec = (((uintptr_t)x | (uintptr_t)y | (uint64_t)(x_row_stride * e) | (uint64_t)(y_row_stride * e)) &
+                          15) == 0;
+        auto kern = vec ? fwht_kernel<D, IN, true> : fwht_kernel<D, IN, false>;
+        kern<<<dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream>>>((const IN*)x, (IN*)y, x_row_stride,
+                                                                             y_row_stride, rows);
         return kush_check_launch("kush_fwht");
     });
 }

@@ -29,6 +29,10 @@ def test_fwht_gpu_matches_oracle(D, dtype):
     xc = x.to(DEV)
     assert torch.equal(ops.fwht(xc, out=xc).cpu(), y)                  # in place
     assert ops.fwht(x[:0].to(DEV)).shape == (0, D)
+    buf = torch.empty(x.numel() + 1, dtype=dtype, device=DEV)          # rows off 16-byte alignment:
+    xo = buf[1:].view(x.shape)                                         # the per-element path
+    xo.copy_(x.to(DEV))
+    assert torch.equal(ops.fwht(xo).cpu(), y)
 
 
 @pytest.mark.parametrize("D", [64, 128, 256])
