@@ -233,7 +233,7 @@ def cpu_baseline(w, budget_s: float):
 
 
 def measured_traffic(path: str, workload: str):
-    """HBM bytes per decode launch from a committed counter summary (FETCH_SIZE + WRITE_SIZE of the
+    """HBM bytes per launch of a configuration's main kernel from a committed counter summary (FETCH_SIZE + WRITE_SIZE of the
     same workload, each scaled by the copy-kernel calibration), or None."""
     try:
         text = Path(path).read_text()
@@ -335,13 +335,14 @@ def ragged_cache(ops, lens, room: int, Hkv: int, bias_sigma: float, bias_frac: f
     return cache, table, tail_k, tail_idx
 
 
-def _line(metric, us, alg, config, kernels, extra=None):
+def _line(metric, us, alg, config, kernels, extra=None, traffic_md=None):
     gbs = alg / (us * 1e-6) / 1e9
+    traffic = measured_traffic(str(ROOT / "profiles" / traffic_md), config["workload"]) if traffic_md else None
     res = {"metric": metric, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "us_per_step": round(us, 2),
            "pct_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "data": "synthetic (seeded, generated on the GPU)", "config": config,
            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                        "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "kernel": kernels,
+                        "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic, "kernel": kernels,
                         "algorithmic_bytes": int(alg)}}
     if extra:
         res.update(extra)
@@ -504,7 +505,7 @@ def bench_c4_unpack(a) -> None:
                        f"int{bits}, bf16 kp / vp, rot {int(a.rot)}", "global_batch": 1, "seq_len": rows},
           f"unpack_kernel<{D},{bits},bf16,vec> ({pages} page items + {T // PAGE} new-row items) x {Hkv} heads, "
           f"4 tasks per workgroup",
-          extra)
+          extra, traffic_md="unpack_c4_traffic.md")
 
 
 def cpu_baseline_unpack(pool, blk, k_new, v_new, D, bits, Hkv, rot, budget_s: float):
@@ -552,7 +553,7 @@ def bench_c4_fwht(a) -> None:
     alg = 2 * rows * Hkv * D * 2
     _line("fwht us/step + achieved HBM GB/s (% peak), 1,064,960 rows of D 128 bf16", ms * 1e3, alg,
           {"workload": f"C4 key rotation: {rows} tokens x {Hkv} kv heads, D {D}, bf16, in place", "rows": rows * Hkv},
-          f"fwht_kernel<{D},bf16> (one wave per row)")
+          f"fwht_kernel<{D},bf16,vec> ({D // 16} lanes per row)", traffic_md="fwht_c4_traffic.md")
 
 
 def main(argv=None):
