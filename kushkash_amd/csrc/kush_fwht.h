@@ -19,27 +19,6 @@ __device__ __forceinline__ float fwht_scale() {
 }
 
 #pragma clang fp contract(off)
-// x of lane (l ^ m) for m in {1, 2, 4, 8}, by DPP within each 16-lane row: quad_perm swaps for 1
-// and 2; 4 and 8 compose two mirrors (half-row mirror l -> l ^ 7 and quad reversal l -> l ^ 3
-// give l ^ 4; row mirror l -> l ^ 15 and half-row mirror give l ^ 8)
-template <int M>
-__device__ __forceinline__ float lane_xor(float x) {
-    static_assert(M == 1 || M == 2 || M == 4 || M == 8, "DPP xor within a 16-lane row");
-    int v = __float_as_int(x);
-    if constexpr (M == 1) {
-        v = __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);       // quad_perm [1, 0, 3, 2]
-    } else if constexpr (M == 2) {
-        v = __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, true);       // quad_perm [2, 3, 0, 1]
-    } else if constexpr (M == 4) {
-        v = __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, true);      // row_half_mirror
-        v = __builtin_amdgcn_mov_dpp(v, 0x1B, 0xF, 0xF, true);       // quad_perm [3, 2, 1, 0]
-    } else {
-        v = __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, true);      // row_mirror
-        v = __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, true);      // row_half_mirror
-    }
-    return __int_as_float(v);
-}
-
 // one butterfly stage across lanes (lane bit M of l): the lower lane keeps self + partner, the upper
 // one partner - self, written partner + (-self) (the same IEEE result) so that every lane does one
 // sign xor and one add, into which the compiler folds the DPP move

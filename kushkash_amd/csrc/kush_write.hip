@@ -3,24 +3,74 @@
 // kushkash/_ops.py:66-101 (launch), arithmetic kushkash/kush/quant.mojo:25-50. Pages are
 // bit-identical to the reference CPU path (kushkash/kush/cpu.mojo:173-304).
 //
-// Work split on CDNA4: one workgroup of 256 threads per (page, kv head). Thread t owns row
-// t / CG of the page (CG = D / 16 threads per row; D = 256 takes two passes) and the 16 dims
-// [8c, 8c + 8) and [D/2 + 8c, D/2 + 8c + 8), c = t % CG: exactly the dims whose codes make
-// bytes [8c, 8c + 8) of an int4 row (low nibble dim j, high nibble dim j + D/2), so rows are
-// loaded with 16-byte loads and stored with 8-byte stores, both coalesced. A V row's range is
-// reduced over the CG lanes of its row (xor shuffles); a K channel's range over the 32 rows goes
-// through an fp32 tile in LDS, one channel per thread.
+// Work split on CDNA4: one workgroup per (page, kv head), of 256 threads for the append and of
+// 128 (D <= 128) or 256 threads for the chunk write, small enough in threads and LDS that a CU
+// holds 16 of them: a chunk's pages then mostly run as one round, all their row loads in flight
+// together. Thread t owns row t / CG of each pass over the page (CG = D / 16 threads per row)
+// and the 16 dims [8c, 8c + 8) and [D/2 + 8c, D/2 + 8c + 8), c = t % CG: exactly the dims whose
+// codes make bytes [8c, 8c + 8) of an int4 row (low nibble dim j, high nibble dim j + D/2), so
+// rows are loaded with 16-byte loads and stored with 8-byte stores, both coalesced. A V row's
+// range is reduced over the CG lanes of its row (xor shuffles); a K channel's range over the 32
+// rows goes through a tile of the K rows in LDS, kept in the input dtype (exact), one channel
+// per thread.
 #include "kush_common.h"
 
 namespace kush {
 
 constexpr int WRITE_THREADS = 256;
 
+// threads of a chunk-write workgroup
 template <int D>
+constexpr int write_threads() { return D == 256 ? 256 : 128; }
+
+template <int D, int THREADS>
 struct Rows {
     static constexpr int CG = D / 16;                        // threads per row
-    static constexpr int RP = WRITE_THREADS / CG;            // rows per pass
+    static constexpr int RP = THREADS / CG;                  // rows per pass
     static constexpr int PASSES = RP >= PAGE ? 1 : PAGE / RP;
+};
+
+// LDS of a page task: the K tile (PAGE x D in the input dtype), then the channels' fp32 bias and
+// reciprocal scale
+template <int D, typename IN>
+constexpr int tile_bytes() { return PAGE * D * (int)sizeof(IN) + 2 * D * 4; }
+
+// A thread's 16 values of one row (two runs of 8: dims 8c.. and D/2 + 8c..) as loaded, in 16-byte
+// words (2 for 16-bit inputs, 4 for fp32): half the registers of fp32 values for bf16 / fp16
+template <typename IN, bool VEC>
+struct Row16 {
+    static constexpr int W = (int)sizeof(IN) * 16 / 16;
+    u4 w[W];
+    __device__ __forceinline__ void load(const IN* row, int lo, int hi) {
+        if constexpr (VEC) {
+#pragma unroll
+            for (int i = 0; i < W / 2; ++i) {
+                w[i] = reinterpret_cast<const u4*>(row + lo)[i];
+                w[W / 2 + i] = reinterpret_cast<const u4*>(row + hi)[i];
+            }
+        } else {
+            IN v[16];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                v[j] = row[lo + j];
+                v[8 + j] = row[hi + j];
+            }
+            __builtin_memcpy(w, v, sizeof(w));
+        }
+    }
+    __device__ __forceinline__ void floats(float (&x)[16]) const {
+        const IN* v = reinterpret_cast<const IN*>(w);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) x[j] = to_f32(v[j]);
+    }
+    // both runs into the tile row (16-byte aligned)
+    __device__ __forceinline__ void store(IN* row, int lo, int hi) const {
+#pragma unroll
+        for (int i = 0; i < W / 2; ++i) {
+            reinterpret_cast<u4*>(row + lo)[i] = w[i];
+            reinterpret_cast<u4*>(row + hi)[i] = w[W / 2 + i];
+        }
+    }
 };
 
 // codes of the 16 values of a thread (x[0..8): dims 8c.., x[8..16): dims D/2 + 8c..) -> the bytes
@@ -57,18 +107,36 @@ __device__ __forceinline__ void pack16(const float (&x)[16], const float (&b)[16
 }
 #pragma clang fp contract(on)
 
-// One (page, kv head) by the workgroup: V rows [vlo, vhi) of the page (row t from
-// v_new + (t - vlo) * v_stride) and, when do_k, the K page: rows t < split from k_tail (stride D),
-// the others from k_new + (t - split) * k_stride. rec: the page's record. tile: LDS of
-// PAGE * D + 2 * D floats. Every thread of the workgroup calls this (it has barriers when do_k).
-template <int D, int BITS, typename IN, bool VEC>
+// min / max over the CG consecutive lanes of a row (xor butterflies by DPP within 16-lane rows)
+template <int CG>
+__device__ __forceinline__ void row_range(float& mn, float& mx) {
+    mn = __builtin_fminf(mn, lane_xor<1>(mn));
+    mx = __builtin_fmaxf(mx, lane_xor<1>(mx));
+    mn = __builtin_fminf(mn, lane_xor<2>(mn));
+    mx = __builtin_fmaxf(mx, lane_xor<2>(mx));
+    if constexpr (CG > 4) {
+        mn = __builtin_fminf(mn, lane_xor<4>(mn));
+        mx = __builtin_fmaxf(mx, lane_xor<4>(mx));
+    }
+    if constexpr (CG > 8) {
+        mn = __builtin_fminf(mn, lane_xor<8>(mn));
+        mx = __builtin_fmaxf(mx, lane_xor<8>(mx));
+    }
+}
+
+// One (page, kv head) by the workgroup of THREADS threads: V rows [vlo, vhi) of the page (row t
+// from v_new + (t - vlo) * v_stride) and, when do_k, the K page: rows t < split from k_tail
+// (stride D), the others from k_new + (t - split) * k_stride. rec: the page's record. lds:
+// tile_bytes<D, IN>() bytes. Every thread of the workgroup calls this (it has barriers when do_k).
+template <int D, int BITS, typename IN, bool VEC, int THREADS>
 __device__ __forceinline__ void page_task(const IN* __restrict__ k_tail, const IN* __restrict__ k_new, int64_t k_stride,
                                           int split, bool do_k, const IN* __restrict__ v_new, int64_t v_stride,
-                                          int vlo, int vhi, uint8_t* __restrict__ rec, float* tile) {
+                                          int vlo, int vhi, uint8_t* __restrict__ rec, uint8_t* lds) {
     using F = Fmt<D, BITS>;
-    using RW = Rows<D>;
+    using RW = Rows<D, THREADS>;
     constexpr int CG = RW::CG;
     const int t = threadIdx.x, c = t % CG, r0 = t / CG;
+    const auto has_v = [&](int r) { return r >= vlo && r < vhi && r < PAGE; };
 
     // V rows: each row's final encoding, per-token range over the CG lanes of the row (consecutive
     // lanes of one wave, all taking the same branch)
@@ -76,22 +144,18 @@ __device__ __forceinline__ void page_task(const IN* __restrict__ k_tail, const I
 #pragma unroll
         for (int pp = 0; pp < RW::PASSES; ++pp) {
             const int r = r0 + pp * RW::RP;
-            if (r < vlo || r >= vhi || r >= PAGE) continue;
-            const IN* row = v_new + (int64_t)(r - vlo) * v_stride;
+            if (!has_v(r)) continue;
+            Row16<IN, VEC> vr;
+            vr.load(v_new + (int64_t)(r - vlo) * v_stride, 8 * c, D / 2 + 8 * c);
             float x[16];
-            get8<VEC>(row + 8 * c, reinterpret_cast<float(&)[8]>(x[0]));
-            get8<VEC>(row + D / 2 + 8 * c, reinterpret_cast<float(&)[8]>(x[8]));
+            vr.floats(x);
             float mn = x[0], mx = x[0];
 #pragma unroll
             for (int j = 1; j < 16; ++j) {
                 mn = __builtin_fminf(mn, x[j]);
                 mx = __builtin_fmaxf(mx, x[j]);
             }
-#pragma unroll
-            for (int o = 1; o < CG; o <<= 1) {
-                mn = __builtin_fminf(mn, __shfl_xor(mn, o, WAVE));
-                mx = __builtin_fmaxf(mx, __shfl_xor(mx, o, WAVE));
-            }
+            row_range<CG>(mn, mx);
             float s, b, inv;
             qparams<BITS>(mn, mx, s, b, inv);
             float bb[16], ii[16];
@@ -116,35 +180,27 @@ __device__ __forceinline__ void page_task(const IN* __restrict__ k_tail, const I
         return;
     }
 
-    // K rows into registers and the fp32 tile (loads issued before the V work)
-    float kx[RW::PASSES][16];
+    // K rows into registers as loaded and into the tile (loads issued before the V work)
+    IN* const tile = reinterpret_cast<IN*>(lds);
+    Row16<IN, VEC> kr[RW::PASSES];
 #pragma unroll
     for (int pp = 0; pp < RW::PASSES; ++pp) {
         const int r = r0 + pp * RW::RP;
         if (r >= PAGE) continue;
-        const IN* row = r < split ? k_tail + r * D : k_new + (int64_t)(r - split) * k_stride;
-        get8<VEC>(row + 8 * c, reinterpret_cast<float(&)[8]>(kx[pp][0]));
-        get8<VEC>(row + D / 2 + 8 * c, reinterpret_cast<float(&)[8]>(kx[pp][8]));
-        float* tr = tile + r * D;
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-            *reinterpret_cast<f4*>(tr + hh * (D / 2) + 8 * c) =
-                f4{kx[pp][8 * hh], kx[pp][8 * hh + 1], kx[pp][8 * hh + 2], kx[pp][8 * hh + 3]};
-            *reinterpret_cast<f4*>(tr + hh * (D / 2) + 8 * c + 4) =
-                f4{kx[pp][8 * hh + 4], kx[pp][8 * hh + 5], kx[pp][8 * hh + 6], kx[pp][8 * hh + 7]};
-        }
+        kr[pp].load(r < split ? k_tail + r * D : k_new + (int64_t)(r - split) * k_stride, 8 * c, D / 2 + 8 * c);
+        kr[pp].store(tile + r * D, 8 * c, D / 2 + 8 * c);
     }
     v_rows();
 
     // K: per-channel range over the 32 rows (one channel per thread), then the codes
-    float* kbias = tile + PAGE * D;
+    float* kbias = reinterpret_cast<float*>(lds + PAGE * D * sizeof(IN));
     float* kinv = kbias + D;
     __syncthreads();
-    for (int ch = t; ch < D; ch += WRITE_THREADS) {
+    for (int ch = t; ch < D; ch += THREADS) {
         float mn = __builtin_inff(), mx = -__builtin_inff();
 #pragma unroll 8
         for (int r = 0; r < PAGE; ++r) {
-            const float x = tile[r * D + ch];
+            const float x = to_f32(tile[r * D + ch]);
             mn = __builtin_fminf(mn, x);
             mx = __builtin_fmaxf(mx, x);
         }
@@ -175,8 +231,10 @@ __device__ __forceinline__ void page_task(const IN* __restrict__ k_tail, const I
     for (int pp = 0; pp < RW::PASSES; ++pp) {
         const int r = r0 + pp * RW::RP;
         if (r >= PAGE) continue;
+        float kx[16];
+        kr[pp].floats(kx);
         u2 lo, hi;
-        pack16<BITS>(kx[pp], bb, ii, lo, hi);
+        pack16<BITS>(kx, bb, ii, lo, hi);
         uint8_t* dst = rec + r * F::DC + 8 * c;
         *reinterpret_cast<u2*>(dst) = lo;
         if constexpr (BITS == 8) *reinterpret_cast<u2*>(dst + D / 2) = hi;
@@ -204,7 +262,7 @@ __global__ __launch_bounds__(WRITE_THREADS) void append_kernel(
     const int32_t* __restrict__ seq_lens, int pos_offset, const int32_t* __restrict__ tail_idx,
     uint8_t* __restrict__ cache, int64_t bs, int64_t hs, IN* __restrict__ tail_k,
     const int32_t* __restrict__ block_table, int64_t bt_stride, int H) {
-    __shared__ __align__(16) float tile[PAGE * D + 2 * D];
+    __shared__ __align__(16) uint8_t lds[tile_bytes<D, IN>()];
     const int s = blockIdx.x, h = blockIdx.y;
     const int pos = seq_lens[s] + pos_offset;
     if (pos < 0) return;
@@ -214,8 +272,8 @@ __global__ __launch_bounds__(WRITE_THREADS) void append_kernel(
     const IN* krow = k + (int64_t)s * k_stride + (int64_t)h * D;
     uint8_t* rec = cache + blk * bs + (int64_t)h * hs;
     copy_rows<D, IN, VEC>(tail + slot * D, krow, 0, 1);
-    page_task<D, BITS, IN, VEC>(tail, krow, 0, PAGE - 1, slot == PAGE - 1, v + (int64_t)s * v_stride + (int64_t)h * D,
-                                0, slot, slot + 1, rec, tile);
+    page_task<D, BITS, IN, VEC, WRITE_THREADS>(tail, krow, 0, PAGE - 1, slot == PAGE - 1,
+                                               v + (int64_t)s * v_stride + (int64_t)h * D, 0, slot, slot + 1, rec, lds);
 }
 
 // seq_lens[s] = seq_lens[s] + pos_offset + 1 where that position is >= 0 (the appended token)
@@ -227,19 +285,19 @@ __global__ __launch_bounds__(256) void advance_kernel(int32_t* seq_lens, int pos
     }
 }
 
-// grid (n_jobs, Hkv), block 256: the write's mode 0. Job j covers logical page job_page[j] of
+// grid (n_jobs, Hkv), block write_threads<D>(): the write's mode 0. Job j covers logical page job_page[j] of
 // sequence job_seq[j], whose new rows [qsl[s], qsl[s+1]) sit at positions [ctx, seq_lens[s]):
 // write the page's new V rows and, if the page is complete, quantize its K (older rows from the
 // tail, newer from the chunk). Mode 1 (tail_kernel) then stashes the new K rows of still-partial
 // pages in the tail: two launches, so no tail is read and written by the same one.
 // Contract: gpu.mojo:241-276, cpu.mojo:273-304.
 template <int D, int BITS, typename IN, bool VEC>
-__global__ __launch_bounds__(WRITE_THREADS) void write_kernel(
+__global__ __launch_bounds__(write_threads<D>()) void write_kernel(
     const IN* __restrict__ k, const IN* __restrict__ v, int64_t k_stride, int64_t v_stride,
     const int32_t* __restrict__ qsl, const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ tail_idx,
     const int32_t* __restrict__ job_seq, const int32_t* __restrict__ job_page, uint8_t* __restrict__ cache,
     int64_t bs, int64_t hs, IN* __restrict__ tail_k, const int32_t* __restrict__ block_table, int64_t bt_stride, int H) {
-    __shared__ __align__(16) float tile[PAGE * D + 2 * D];
+    __shared__ __align__(16) uint8_t lds[tile_bytes<D, IN>()];
     const int j = blockIdx.x, h = blockIdx.y;
     const int s = job_seq[j];
     const int ps = job_page[j] * PAGE;
@@ -255,9 +313,10 @@ __global__ __launch_bounds__(WRITE_THREADS) void write_kernel(
         const int hi = ps + PAGE < total ? ps + PAGE : total;
         int split = ctx - ps;                               // K rows before it come from the tail
         split = split < 0 ? 0 : (split > PAGE ? PAGE : split);
-        page_task<D, BITS, IN, VEC>(tail, k + (int64_t)(q0 + ps + split - ctx) * k_stride + hoff, k_stride, split,
-                                    complete, v + (int64_t)(q0 + lo - ctx) * v_stride + hoff, v_stride, lo - ps,
-                                    hi - ps, rec, tile);
+        page_task<D, BITS, IN, VEC, write_threads<D>()>(tail, k + (int64_t)(q0 + ps + split - ctx) * k_stride + hoff,
+                                                        k_stride, split, complete,
+                                                        v + (int64_t)(q0 + lo - ctx) * v_stride + hoff, v_stride,
+                                                        lo - ps, hi - ps, rec, lds);
     }
 }
 
@@ -337,7 +396,7 @@ extern "C" int kush_write(int head_dim, int bits, int dtype, const void* k, cons
         hipStream_t st = (hipStream_t)stream;
         if (mode == 0) {
             auto kern = vec ? write_kernel<D, BITS, IN, true> : write_kernel<D, BITS, IN, false>;
-            kern<<<dim3(n_jobs, hkv), dim3(WRITE_THREADS), 0, st>>>(
+            kern<<<dim3(n_jobs, hkv), dim3(write_threads<D>()), 0, st>>>(
                 (const IN*)k, (const IN*)v, k_stride, v_stride, query_start_loc, seq_lens, tail_idx, job_seq, job_page,
                 (uint8_t*)cache, block_stride, head_stride, (IN*)tail_k, block_table, bt_stride, hkv);
         } else {
