@@ -9,7 +9,11 @@ fp32 on the CPU. With rotation, q goes in and the output comes back through bf16
 magnitude.
 
 test_attend_chunk_over_history: a chunk of new queries over the cached history plus the chunk
-itself, causal (cache.py:185-201), against fp32 attention over [dequantized history | chunk]."""
+itself, causal (cache.py:185-201), against fp32 attention over [dequantized history | chunk].
+
+The reference's rotation tests on the GPU: rotate() rounds once (tests/test_gpu.py:65-84), a
+rotated cache attends like the CPU one (:87-97), and rotation lowers the int4 attention error
+(tests/test_cpu.py:369-393)."""
 import pytest
 import torch
 import torch.nn.functional as F
@@ -66,3 +70,49 @@ def test_attend_chunk_over_history(n_hist, T):
     ref = F.scaled_dot_product_attention(q.float(), keys, vals, attn_mask=mask, enable_gqa=True)
     err = (out - ref).abs().max().item()
     assert err <= _bound(ref, 3), err
+
+
+def test_rotate_rounds_once_gpu():
+    """rotate() on the GPU (one torch GEMM with the +-1 matrix and alpha 1/sqrt(D), fp32
+    accumulation): within one rounding of the exact product for every dtype and head_dim, and the
+    out= form gives the same bits (tests/test_gpu.py:65-84)."""
+    from kushkash_amd._ops import hadamard, rotate
+    unit = {torch.float32: 2.0 ** -24, torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8}
+    for dt, u in unit.items():
+        for D in (64, 128, 256):
+            h = hadamard(D, DEV)
+            x = torch.randn(6, 8, D, device=DEV).to(dt)[:, ::2]
+            y = rotate(x, h)
+            ref = x.double() @ h.double()
+            tol = u * ref.abs() + 1e-5
+            assert y.dtype == dt and bool(((y.double() - ref).abs() <= tol).all()), (dt, D)
+            buf = torch.full((8, 4, D), float("nan"), device=DEV, dtype=dt)
+            rotate(x, h, out=buf[:6])
+            assert torch.equal(buf[:6], y) and bool(buf[6:].isnan().all()), (dt, D)
+
+
+def test_rotated_cache_gpu_matches_oracle():
+    """Rotation on, fp32: GPU and CPU-oracle caches attend alike (pages may differ in rare rounding
+    flips of the rotated inputs, the outputs must not; tests/test_gpu.py:87-97)."""
+    from _harness import oracle_cache
+    torch.manual_seed(0)
+    B, H, G, D, T = 2, 2, 4, 128, 3 * 32 + 5
+    K, V, q = torch.randn(B, H, T, D) * 2, torch.randn(B, H, T, D), torch.randn(B, H * G, D)
+    K[..., 1] += 50
+    outs = []
+    cpu = oracle_cache(1, H, H * G, D, batch_size=B, bits=4, rotate=True)
+    cpu.write(0, K, V)
+    outs.append(cpu.attend(0, q))
+    gpu = kk.KushCache(1, H, H * G, D, batch_size=B, bits=4, device=DEV, dtype=torch.float32, rotate=True)
+    gpu.write(0, K.to(DEV), V.to(DEV))
+    outs.append(gpu.attend(0, q.to(DEV)).cpu())
+    assert (outs[0] - outs[1]).norm() / outs[0].norm() < 3e-3
+
+
+def test_rotation_lowers_attention_error_gpu():
+    """With outlier channels in K and V, decode and chunk attention over the int4 cache land closer
+    to exact attention when the cache rotates (tests/test_cpu.py:369-393), on the GPU path."""
+    from _rotation_case import rotation_errors
+    err = rotation_errors(lambda rot: kk.KushCache(1, 2, 8, 128, batch_size=1, bits=4, device=DEV,
+                                                   dtype=torch.float32, rotate=rot), DEV)
+    assert err[True][0] < 0.9 * err[False][0] and err[True][1] < 0.9 * err[False][1], err

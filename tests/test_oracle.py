@@ -265,3 +265,12 @@ def test_ragged_mixed_batches(bits, D, G):
         if not dec + chk:
             continue
         sim.step(dec + chk, [1] * len(dec) + [rng.randint(2, 40) for _ in chk])
+
+
+def test_rotation_lowers_attention_error():
+    """The point of the rotation: with outlier channels in K and V, decode and chunk attention over
+    the int4 cache (oracle backend) land closer to exact attention when the cache rotates
+    (tests/test_cpu.py:369-393)."""
+    from _rotation_case import rotation_errors
+    err = rotation_errors(lambda rot: oracle_cache(1, 2, 8, 128, batch_size=1, bits=4, rotate=rot), "cpu")
+    assert err[True][0] < 0.9 * err[False][0] and err[True][1] < 0.9 * err[False][1], err
