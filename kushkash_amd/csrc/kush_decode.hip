@@ -813,34 +813,58 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
             *reinterpret_cast<f4*>(reg + (((4 * dt + q) * 16 + r16) * 4) * 4) = v;
         }
     }
-    float L = 0.0f;                                              // softmax denominator of head r16
+    // softmax denominator of head r16: every wave's (and stream's) l at the workgroup max. A column
+    // that saw no token holds m = -inf and l = 0, and exp2(-inf) = 0, so no term needs a branch and
+    // all the LDS reads go out together (the sum keeps its order)
+    float L = 0.0f;
     if (M > -__builtin_inff()) {
+        float mv[NW][ST], lv[NW][ST];
 #pragma unroll
-        for (int ww = 0; ww < NW; ++ww) {
-            const float mw = m_l[ww * 16 + r16];
-            if (mw > -__builtin_inff()) L += l_l[ww * 16 + r16] * __builtin_amdgcn_exp2f(mw - M);
-            if constexpr (ST == 2) {
-                const float mx = m_l[ww * 16 + rx];
-                if (mx > -__builtin_inff()) L += l_l[ww * 16 + rx] * __builtin_amdgcn_exp2f(mx - M);
+        for (int ww = 0; ww < NW; ++ww)
+#pragma unroll
+            for (int c2 = 0; c2 < ST; ++c2) {
+                mv[ww][c2] = m_l[ww * 16 + (c2 ? rx : r16)];
+                lv[ww][c2] = l_l[ww * 16 + (c2 ? rx : r16)];
             }
-        }
+#pragma unroll
+        for (int ww = 0; ww < NW; ++ww)
+#pragma unroll
+            for (int c2 = 0; c2 < ST; ++c2) L += lv[ww][c2] * __builtin_amdgcn_exp2f(mv[ww][c2] - M);
     }
     __syncthreads();
     const float inv_l = L > 0.0f ? 1.0f / L : 0.0f;
     const int64_t pb = (((int64_t)s * H + h) * NS + z) * G + g0 + r16;   // partials row of head r16
+    const bool out_vec = (((uintptr_t)out) & 15) == 0;
     for (int dt = w; dt < DT; dt += NW) {
+        f4 part[NW][ST];                                         // every wave's piece, read together
+#pragma unroll
+        for (int ww = 0; ww < NW; ++ww)
+#pragma unroll
+            for (int c2 = 0; c2 < ST; ++c2)
+                part[ww][c2] = *reinterpret_cast<const f4*>(ringA + ww * OBYTES +
+                                                            (((4 * dt + q) * 16 + (c2 ? rx : r16)) * 4) * 4);
         f4 acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int ww = 0; ww < NW; ++ww) {
-            const uint8_t* reg = ringA + ww * OBYTES;
-            acc += *reinterpret_cast<const f4*>(reg + (((4 * dt + q) * 16 + r16) * 4) * 4);
-            if constexpr (ST == 2) acc += *reinterpret_cast<const f4*>(reg + (((4 * dt + q) * 16 + rx) * 4) * 4);
-        }
+        for (int ww = 0; ww < NW; ++ww)
+#pragma unroll
+            for (int c2 = 0; c2 < ST; ++c2) acc += part[ww][c2];
         if (r16 < Gc) {
             const int d0 = 16 * dt + 4 * q;
             if (NS == 1) {
+                IN* dst = out + qbase + r16 * D + d0;
+                if (out_vec) {                                   // one 8- or 16-byte store
+                    IN v4[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) out[qbase + r16 * D + d0 + i] = from_f32<IN>(acc[i] * inv_l);
+                    for (int i = 0; i < 4; ++i) v4[i] = from_f32<IN>(acc[i] * inv_l);
+                    if constexpr (sizeof(IN) == 2) {
+                        *reinterpret_cast<u2*>(dst) = __builtin_bit_cast(u2, v4);
+                    } else {
+                        *reinterpret_cast<f4*>(dst) = __builtin_bit_cast(f4, v4);
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) dst[i] = from_f32<IN>(acc[i] * inv_l);
+                }
             } else {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) publish(part_o + pb * D + d0 + i, acc[i]);
