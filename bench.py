@@ -372,10 +372,11 @@ def bench_c3(a) -> None:
     # longest sequences first (from the host-side lengths, as a serving engine's metadata builder has
     # them): the ragged batch's long workgroups start first
     order = torch.tensor(sorted(range(B), key=lambda i: -lens[i]), dtype=torch.int32, device=dev)
+    wv = a.waves or ops.waves(B, Hkv, ns, max(n1 for n1 in lens) // PAGE + 1)
 
     def step(i):
         ops.append(k_new, v_new, sl, tail_idx, cache, table, tail_k, pos_offset=-1, advance=False)
-        ops.decode(q, out, cache, table, sl, tail_idx, tail_k, sm, ns, work, waves=a.waves or None, order=order)
+        ops.decode(q, out, cache, table, sl, tail_idx, tail_k, sm, ns, work, waves=wv, order=order)
 
     ms = time_graph(step, a.steps, a.warmup)
     RB, DC = record_bytes(D, bits), (D if bits == 8 else D // 2)
@@ -389,8 +390,8 @@ def bench_c3(a) -> None:
           {"workload": f"C3 Llama-3.1-8B layer: {Hq} q / {Hkv} kv heads, D {D}, int{bits}, page 32, batch {B}, "
                        f"N_i ~ U[256, 8192] (seed 0; sum {sum(lens)} tokens), append (pos_offset -1) + decode",
            "global_batch": B, "split_k": ns, "tokens": sum(n1), "sequence_order": "longest first",
-           "waves": a.waves or ops.waves(B, Hkv, ns, table.shape[1])},
-          f"append_kernel<{D},{bits},bf16> + decode_kernel<{D},{bits},bf16,4>")
+           "waves": wv},
+          f"append_kernel<{D},{bits},bf16> + decode_kernel<{D},{bits},bf16,{wv}>")
 
 
 def bench_c4(a) -> None:
@@ -412,14 +413,15 @@ def bench_c4(a) -> None:
     nss = [a.splits or policy] + [int(x) for x in a.sweep.split(",") if x.strip() and ":" not in x]
     for i, ns in enumerate(nss):
         work = torch.empty(B * Hkv * ns * G * (D + 2), dtype=torch.float32, device=dev)
-        ms = time_graph(lambda j: ops.decode(q, out, cache, table, sl, tail_idx, tail_k, sm, ns, work,
-                                            waves=a.waves or None),
+        wv = a.waves or ops.waves(B, Hkv, ns, N // PAGE)
+        ms = time_graph(lambda j: ops.decode(q, out, cache, table, sl, tail_idx, tail_k, sm, ns, work, waves=wv),
                         a.steps, a.warmup)
         if i == 0:
             _line("decode-attn us/step + achieved HBM GB/s (% peak), int4, bs8 x 131k ctx", ms * 1e3, alg,
                   {"workload": f"C4 Qwen3-8B layer: {Hq} q / {Hkv} kv heads, D {D}, int{bits}, page 32, "
-                               f"batch {B} x {N} tokens", "global_batch": B, "seq_len": N, "split_k": ns},
-                  f"decode_kernel<{D},{bits},bf16,8> (split-K merged in the launch)")
+                               f"batch {B} x {N} tokens", "global_batch": B, "seq_len": N, "split_k": ns,
+                   "waves": wv},
+                  f"decode_kernel<{D},{bits},bf16,{wv}> (split-K merged in the launch)")
         else:
             print(f"C4 splits {ns:4d}: {ms * 1e3:8.2f} us/step  {alg / ms / 1e6:7.1f} GB/s "
                   f"({100 * alg / ms / 1e6 / PEAK_HBM_GBS:5.1f}% of peak)", file=sys.stderr, flush=True)

@@ -161,13 +161,16 @@ class KushCache:
             raise RuntimeError("attend() on an empty cache")
         q = rotate(q, self.rot, self.kdtype).contiguous()
         out = torch.empty_like(q)
-        ns = self._frozen_ns or self.ops.splits(self.B, self.H, self._len[layer] // PAGE)
+        pages = (self._capacity if self._frozen_ns else self._len[layer]) // PAGE
+        ns = self._frozen_ns or self.ops.splits(self.B, self.H, pages)
         if ns > 1:
             need = self.B * self.H * ns * self.G * (2 + self.D)
             if self._work.numel() < need:
                 self._work = torch.empty(need, dtype=torch.float32, device=self.device)
+        # GPU: the waves per workgroup from the cached length (the block table may be wider)
+        kw = {"waves": self.ops.waves(self.B, self.H, ns, pages)} if self.gpu else {}
         self.ops.decode(q, out, self.pool[layer], self.block_table, self.seq_lens[layer], self.tail_idx,
-                        self.tail_k[layer], self.scale, ns, self._work)
+                        self.tail_k[layer], self.scale, ns, self._work, **kw)
         return rotate(out, self.rot, self.dtype)
 
     def attend_chunk(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
