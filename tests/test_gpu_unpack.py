@@ -3,7 +3,8 @@
 with rows no entry names left untouched (reference: tests/test_gpu.py:221-240). Also a large
 group across all the shape classes a serving step makes (hundreds of shuffled pages, several kv
 heads, partial pages of every length, a ragged new chunk), the per-element path for unaligned
-rows, and index validation before any launch."""
+rows, index validation before any launch, and the unpack in its use: a packed-prefill group built
+from a KushCache, attended per sequence, against attend_chunk."""
 import pytest
 import torch
 
@@ -103,3 +104,50 @@ def test_unpack_gpu_validates_indices_before_launch():
     with pytest.raises(ValueError, match="must be torch.bfloat16"):
         ops.unpack(c["records"].to(DEV), *[args[n] if n != "k_new" else args[n].float() for n in INDEX_NAMES],
                    kp, kp.clone(), False)
+
+
+def test_packed_prefill_matches_attend_chunk():
+    """The unpack in its use (the vLLM packed prefill, kushkash/vllm/backend.py:837-856): a group
+    built from a KushCache's own block table, records and K tail -- each sequence's history (two
+    full pages and a partial one, K from the tail slot) followed by its new chunk -- unpacks to the
+    exact dequantization of those records (bit for bit, the fp64 restatement), and attention per
+    sequence over its packed rows, causal from the history's end, agrees with attend_chunk over the
+    same cache. attend_chunk dequantizes with the reference's torch path, in bf16 (code * scale and
+    + bias each rounded), so the two differ by that rounding: max-abs within 2e-2."""
+    import torch.nn.functional as F
+    from _unpack_fixture import unpack_torch
+    from kushkash_amd._ops import PAGE
+    B, Hkv, G, D, hist, T = 2, 2, 4, 128, 70, 33
+    dt = torch.bfloat16
+    g = torch.Generator().manual_seed(7)
+    c = kk.KushCache(1, Hkv, Hkv * G, D, batch_size=B, bits=4, device=DEV, dtype=dt, rotate=False)
+    c.write(0, torch.randn(B, Hkv, hist, D, generator=g).to(dt).to(DEV),
+            torch.randn(B, Hkv, hist, D, generator=g).to(dt).to(DEV))
+    q = torch.randn(B, Hkv * G, T, D, generator=g).to(dt)
+    k = torch.randn(B, Hkv, T, D, generator=g).to(dt)
+    v = torch.randn(B, Hkv, T, D, generator=g).to(dt)
+    bt, ti = c.block_table.cpu(), c.tail_idx.cpu()
+    full, rem = divmod(hist, PAGE)
+    L = hist + T                                                          # packed rows per sequence
+    i32 = lambda x: torch.tensor(x, dtype=torch.int32)
+    group = dict(records=c.pool[0].cpu(), H=Hkv, rows=B * L, gaps=[],
+                 page_blk=i32([int(bt[i, p]) for i in range(B) for p in range(full)]),
+                 page_dst=i32([i * L + p * PAGE for i in range(B) for p in range(full)]),
+                 tail_blk=i32([int(bt[i, full]) for i in range(B)]),
+                 tail_info=i32([x for i in range(B) for x in (i * L + full * PAGE, rem, int(ti[i]))]),
+                 tail_k=c.tail_k[0].cpu(), k_new=k.permute(0, 2, 1, 3).reshape(B * T, Hkv, D),
+                 v_new=v.permute(0, 2, 1, 3).reshape(B * T, Hkv, D),
+                 new_dst=i32([i * L + hist + t for i in range(B) for t in range(T)]))
+    kp = torch.zeros(B * L, Hkv, D, dtype=dt, device=DEV)
+    vp = torch.zeros_like(kp)
+    c.ops.unpack(c.pool[0], *[group[n].to(DEV) for n in INDEX_NAMES], kp, vp, False)
+    want_k, want_v = unpack_torch(group, D, 4, False, dt)
+    assert torch.equal(kp.cpu().view(torch.int16), want_k.view(torch.int16))
+    assert torch.equal(vp.cpu().view(torch.int16), want_v.view(torch.int16))
+    keys = kp.view(B, L, Hkv, D).permute(0, 2, 1, 3).float().cpu()
+    vals = vp.view(B, L, Hkv, D).permute(0, 2, 1, 3).float().cpu()
+    mask = torch.ones(T, L, dtype=torch.bool).tril(hist)                  # query t sees hist + t + 1 rows
+    out = F.scaled_dot_product_attention(q.float(), keys, vals, attn_mask=mask, enable_gqa=True)
+    ref = c.attend_chunk(0, q.to(DEV), k.to(DEV), v.to(DEV)).float().cpu()
+    err = (out - ref).abs().max().item()
+    assert err < 2e-2, err
