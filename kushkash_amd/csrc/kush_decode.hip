@@ -786,9 +786,10 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     }
 
     // Merge the waves (and, ST = 2, the two streams of a head: columns c and c ^ 8). Every wave
-    // rescales its O to the workgroup max of its head and stores it in the idle rings (region of wave
-    // ww: 16 D floats, dims d as [d / 4][column][d % 4], one 16-byte store per lane and tile); after
-    // one barrier, wave w sums tiles w, w + NW, ... over the waves and writes them out.
+    // rescales its O to the workgroup max of its head, adds a head's two stream columns (one DPP
+    // move; columns 0-7 then hold the sums) and stores it in the idle rings (region of wave ww: 16 D
+    // floats, dims d as [d / 4][column][d % 4], one 16-byte store per lane and tile); after one
+    // barrier, wave w sums tiles w, w + NW, ... over the waves and writes them out.
     constexpr int OBYTES = 16 * D * 4;
     static_assert(NW * OBYTES <= 2 * NW * R::SLOT, "the merge needs 16 D floats per wave in the first array");
     l_run = rows_sum(l_run);
@@ -809,8 +810,11 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
         for (int dt = 0; dt < DT; ++dt) {
             f4 v;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] = __builtin_fmaf(o[dt][i], dt < NLO ? TWO24 : TWO20, vb_run) * f;
-            *reinterpret_cast<f4*>(reg + (((4 * dt + q) * 16 + r16) * 4) * 4) = v;
+            for (int i = 0; i < 4; ++i) {
+                v[i] = __builtin_fmaf(o[dt][i], dt < NLO ? TWO24 : TWO20, vb_run) * f;
+                if constexpr (ST == 2) v[i] += lane_xor<8>(v[i]);   // the head's two streams (column c ^ 8)
+            }
+            if (ST == 1 || r16 < 8) *reinterpret_cast<f4*>(reg + (((4 * dt + q) * 16 + r16) * 4) * 4) = v;
         }
     }
     // softmax denominator of head r16: every wave's (and stream's) l at the workgroup max. A column
@@ -835,19 +839,15 @@ __global__ __launch_bounds__(NW * WAVE) void decode_kernel(
     const float inv_l = L > 0.0f ? 1.0f / L : 0.0f;
     const int64_t pb = (((int64_t)s * H + h) * NS + z) * G + g0 + r16;   // partials row of head r16
     const bool out_vec = (((uintptr_t)out) & 15) == 0;
+    const int hcol = ST == 2 ? (r16 & 7) : r16;                  // the column holding head r16's sum
     for (int dt = w; dt < DT; dt += NW) {
-        f4 part[NW][ST];                                         // every wave's piece, read together
+        f4 part[NW];                                             // every wave's piece, read together
 #pragma unroll
         for (int ww = 0; ww < NW; ++ww)
-#pragma unroll
-            for (int c2 = 0; c2 < ST; ++c2)
-                part[ww][c2] = *reinterpret_cast<const f4*>(ringA + ww * OBYTES +
-                                                            (((4 * dt + q) * 16 + (c2 ? rx : r16)) * 4) * 4);
+            part[ww] = *reinterpret_cast<const f4*>(ringA + ww * OBYTES + (((4 * dt + q) * 16 + hcol) * 4) * 4);
         f4 acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int ww = 0; ww < NW; ++ww)
-#pragma unroll
-            for (int c2 = 0; c2 < ST; ++c2) acc += part[ww][c2];
+        for (int ww = 0; ww < NW; ++ww) acc += part[ww];
         if (r16 < Gc) {
             const int d0 = 16 * dt + 4 * q;
             if (NS == 1) {
