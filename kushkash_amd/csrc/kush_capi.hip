@@ -1,6 +1,6 @@
 // C-ABI plumbing shared by every entry point: error codes and the last error message.
-// The entry points themselves live next to their kernels (kush_write.hip, kush_decode.hip) and
-// are declared in include/kushkash_amd.h.
+// The entry points themselves live next to their kernels (kush_write.hip, kush_decode.hip,
+// kush_rotate.hip, kush_unpack.hip) and are declared in include/kushkash_amd.h.
 #include <stdarg.h>
 #include <stdio.h>
 

@@ -1,6 +1,6 @@
 // Shared definitions for the gfx950 kernels of the compressed-KV hot path: the page-record
 // format (kushkash/kush/quant.mojo:16-87), the quantization arithmetic (quant.mojo:25-50), input
-// dtype conversions and wave64 reductions.
+// dtype conversions, row loads and stores, and lane exchange.
 //
 // Page record of one (block, kv head), D channels, BITS in {4, 8}, DC = row bytes:
 //   [ kq: 32*DC | vq: 32*DC | ks: D fp16 | kb: D fp16 | vs: 32 fp16 | vb: 32 fp16 ]
@@ -174,19 +174,6 @@ __device__ __forceinline__ int qcode(float x, float b, float inv) {
 __device__ __forceinline__ uint8_t pack4(int lo, int hi) { return (uint8_t)((lo & 0xF) | ((hi & 0xF) << 4)); }
 
 #pragma clang fp contract(on)
-
-// ------------------------------------------------------------------ wave64 reductions
-__device__ __forceinline__ float wave_min(float x) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x = __builtin_fminf(x, __shfl_xor(x, o, WAVE));
-    return x;
-}
-
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x = __builtin_fmaxf(x, __shfl_xor(x, o, WAVE));
-    return x;
-}
 
 // ------------------------------------------------------------------ lane exchange
 // x of lane (l ^ m) for m in {1, 2, 4, 8}, by DPP within each 16-lane row: quad_perm swaps for 1

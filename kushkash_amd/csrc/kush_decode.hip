@@ -3,22 +3,27 @@
 // :418-491 (split ranges, merge, combine), kushkash/_ops.py:182-213 (launch), arithmetic of the
 // reference CPU path kushkash/kush/cpu.mojo:320-451.
 //
-// Mapping onto CDNA4. One workgroup = NW waves for one (sequence, kv head, split, 16-head
-// chunk); its waves take the split's pages round-robin, each keeping its own online-softmax
-// state, and merge through LDS at the end. Per page a wave:
-//   1. loads its K code slice straight into registers (lane (t, q): row t of a 16-token tile,
-//      bytes [q*DC/4, (q+1)*DC/4): the 64 lanes read 16 contiguous rows) and copies the V codes
-//      and the page's scales / biases into a wave-private LDS stage with 16-byte loads;
-//   2. turns codes into exact fp16 with v_perm (byte under the fp16 exponent of 1024) and one
-//      packed subtract, and computes S^T = K . Q'^T on MFMA 16x16x32 f16, where
-//      Q' = fp16(q * sm * log2 e) * k_scale (fp16) and the K bias dot stays fp32 (v_dot2 on a
-//      hi/lo fp16 split of q);
-//   3. runs a page-granular online softmax in base 2 (wave shuffles over the 4 lane groups);
-//   4. reads V codes column-wise from LDS (8 tokens per lane) into V^T operands and
-//      accumulates O^T += V^T . P'^T on MFMA, with P' = e * v_scale in fp16 and the V bias
-//      folded into one scalar per head.
-// The partial last page takes K from the exact tail (fp32 dot products) and V rows from its
-// record, masked beyond the tail length.
+// Mapping onto CDNA4. One workgroup = NW waves (2, 4 or 8) for one (sequence, kv head, split,
+// 16-head chunk). The split's pages go out in pairs over windows of up to 1,024 pages whose block
+// ids sit in an LDS table; with 8 waves a counter in LDS hands out the pairs, with 2 or 4 waves
+// wave w takes pairs w, w + NW, ... Per pair a wave:
+//   1. has both records staged in its private LDS ring by buffer-to-LDS DMA (whole records, 1 KB
+//      per instruction, issued one pair ahead and waited on with explicit vmcnt counts);
+//   2. reads K code rows from the ring and turns them into exact subnormal fp16 operands (one
+//      v_perm and one v_bitop3 per pair of codes), and computes the scores S^T = K . Q'^T on MFMA
+//      16x16x32 f16 with Q' = q' * k_scale as an fp16 pair (q' = q times a power of two; the rest
+//      of scale * log2 e multiplies the fp32 scores); the K-bias and -HALF * k_scale terms come
+//      from two more MFMAs per K-step;
+//   3. runs a page-granular online softmax in base 2 per MFMA column (with G <= 8 two page
+//      streams share the 16 columns: page A in 0-7, page B in 8-15), moving the running max only
+//      when a page exceeds it by more than 2^3;
+//   4. gathers V codes column-wise from the ring (ds_read_b64_tr_b8) into V^T operands and
+//      accumulates O^T += V^T . P'^T on MFMA, with P' = fp16(e * v_scale); -HALF * sum P' comes
+//      from one MFMA and the V bias sum e * v_bias stays in fp32.
+// The partial last page takes exact fp32 K . q scores from the tail (spread over all waves) and V
+// rows from its record. The waves (and streams) merge through the idle ring at the end; with
+// split-K, partials are published write-through and the last workgroup of a (sequence, kv head)
+// merges them in the same launch.
 //
 // MFMA 16x16x32 f16 operand layout used throughout (lane l, r = l % 16, q = l / 16):
 //   A: row r, 8 contraction slots of lane group q;  B: column r, the same 8 slots;
@@ -32,11 +37,6 @@
 namespace kush {
 
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-
-constexpr float LOG2E = 1.4426950408889634f;
-
-__device__ __forceinline__ h2 as_h2(uint32_t x) { return __builtin_bit_cast(h2, x); }
 
 __device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
 
