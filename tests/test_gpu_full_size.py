@@ -1,0 +1,92 @@
+"""Decode at the benchmark configurations' full sizes (needs an MI355X), built exactly as bench.py
+builds them: the outputs match the reference's own dequant-attention -- fp32 attention over the
+records dequantized by the torch reference path (cached_kv, kushkash/_ops.py:295-306; the partial
+page with its exact K tail) -- within max-abs 2e-3 plus half an output ulp, bf16 out and fp32
+accumulation (the acceptance bound of the compressed-KV decode).
+
+C2: Qwen2.5-7B layer, int4, 64 x 4096 tokens (the headline line's workload).
+C3: Llama-3.1-8B layer, int8, 128 ragged sequences U[256, 8192] with one appended token each and
+    the longest-first order, 2 waves.
+C4: Qwen3-8B layer, int4, 8 x 131,072 tokens with split-K merged in the launch, 8 waves."""
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import bench
+from _harness import out_tol
+from kushkash_amd._ops import PAGE, cached_kv
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def reference(q, cache, table, n, tail_k, D, bits):
+    """fp32 attention of q [B, Hq, D] over the n cached tokens of every sequence of the batch."""
+    k, v = cached_kv(cache, table, n, tail_k, D, bits, torch.float32)
+    return F.scaled_dot_product_attention(q[:, :, None].float(), k, v, enable_gqa=True)[:, :, 0]
+
+
+def check(out, ref, what):
+    err = (out.float() - ref).abs().max().item()
+    tol = out_tol(ref, torch.bfloat16)
+    assert err <= tol, f"{what}: max-abs {err:.3e} > {tol:.3e}"
+
+
+def test_c2_full_size():
+    a = bench.parse_args(["--pools", "1"])
+    w = bench.make_workload(a, DEV)
+    ops, D = w["ops"], w["D"]
+    ns = ops.splits(w["B"], w["Hkv"], w["pages"])
+    out = torch.empty_like(w["q"])
+    ops.decode(w["q"], out, w["cache"], w["tables"][0], w["seq_lens"], w["tail_idx"], w["tail_k"],
+               1.0 / math.sqrt(D), ns, None, waves=ops.waves(w["B"], w["Hkv"], ns, w["pages"]))
+    check(out, reference(w["q"], w["cache"], w["tables"][0], w["N"], w["tail_k"], D, w["bits"]), "C2")
+
+
+def test_c3_full_size():
+    from kushkash_amd._ops import Ops
+    B, Hq, Hkv, D, bits = 128, 32, 8, 128, 8
+    G, dtype = Hq // Hkv, torch.bfloat16
+    lens = torch.randint(256, 8193, (B,), generator=torch.Generator().manual_seed(0)).tolist()
+    ops = Ops(torch.device(DEV), D, bits, G, dtype)
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(0)
+    cache, table, tail_k, tail_idx = bench.ragged_cache(ops, lens, 1, Hkv, 6.0, 0.10, gen, DEV)
+    k_new = torch.randn(B, Hkv, D, generator=gen, device=DEV).to(dtype)
+    v_new = torch.randn(B, Hkv, D, generator=gen, device=DEV).to(dtype)
+    q = torch.randn(B, Hq, D, generator=gen, device=DEV).to(dtype)
+    sl = torch.tensor(lens, dtype=torch.int32, device=DEV) + 1
+    ops.append(k_new, v_new, sl, tail_idx, cache, table, tail_k, pos_offset=-1, advance=False)
+    ns = ops.splits(B, Hkv, max(lens) // PAGE + 1)
+    work = torch.empty(max(1, B * Hkv * ns * G * (D + 2)), dtype=torch.float32, device=DEV)
+    order = torch.tensor(sorted(range(B), key=lambda i: -lens[i]), dtype=torch.int32, device=DEV)
+    out = torch.empty_like(q)
+    ops.decode(q, out, cache, table, sl, tail_idx, tail_k, 1.0 / math.sqrt(D), ns, work,
+               waves=ops.waves(B, Hkv, ns, max(lens) // PAGE + 1), order=order)
+    for i in range(B):                                         # ragged: one sequence at a time
+        t = int(tail_idx[i])
+        ref = reference(q[i:i + 1], cache, table[i:i + 1], lens[i] + 1, tail_k[t:t + 1], D, bits)
+        check(out[i:i + 1], ref, f"C3 sequence {i} ({lens[i] + 1} tokens)")
+
+
+def test_c4_full_size():
+    from kushkash_amd._ops import Ops
+    B, Hq, Hkv, D, bits, N = 8, 32, 8, 128, 4, 131072
+    G, dtype = Hq // Hkv, torch.bfloat16
+    ops = Ops(torch.device(DEV), D, bits, G, dtype)
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(0)
+    cache, table, tail_k, tail_idx = bench.ragged_cache(ops, [N] * B, 0, Hkv, 4.0, 0.05, gen, DEV)
+    q = torch.randn(B, Hq, D, generator=gen, device=DEV).to(dtype)
+    sl = torch.full((B,), N, dtype=torch.int32, device=DEV)
+    ns = ops.splits(B, Hkv, N // PAGE)
+    assert ns > 1
+    work = torch.empty(B * Hkv * ns * G * (D + 2), dtype=torch.float32, device=DEV)
+    out = torch.empty_like(q)
+    ops.decode(q, out, cache, table, sl, tail_idx, tail_k, 1.0 / math.sqrt(D), ns, work,
+               waves=ops.waves(B, Hkv, ns, N // PAGE))
+    for s0 in range(0, B, 2):                                  # the fp32 reference two sequences at a time
+        ref = reference(q[s0:s0 + 2], cache, table[s0:s0 + 2], N, tail_k[s0:s0 + 2], D, bits)
+        check(out[s0:s0 + 2], ref, f"C4 sequences {s0}-{s0 + 1}")
