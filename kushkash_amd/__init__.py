@@ -1,12 +1,23 @@
 """kushkash_amd: the compressed-KV hot path of kushkash (paged int4 / int8 KV cache with fused
 dequant decode attention) as hand-written HIP kernels for AMD Instinct MI355X (gfx950).
 
-Drop-in for the reference's kushkash.KushCache / kushkash._ops.Ops on one GPU."""
+Drop-in for the reference's kushkash.KushCache / kushkash._ops.Ops on one GPU, and for its Hugging
+Face entry points (KushHFCache, enable, generate; transformers is imported on first use)."""
 from ._ops import PAGE, Ops, record_bytes
 from .cache import KushCache, MemoryStats
 
-__all__ = ["KushCache", "MemoryStats", "PAGE", "Ops", "record_bytes", "build"]
+__all__ = ["KushCache", "MemoryStats", "PAGE", "Ops", "record_bytes", "KushHFCache", "enable", "generate", "build"]
 __version__ = "0.1.0"
+
+
+def __getattr__(name):
+    if name in ("KushHFCache", "enable"):
+        from . import hf
+        return getattr(hf, name)
+    if name == "generate":
+        from ._generate import generate
+        return generate
+    raise AttributeError(name)
 
 
 def build(verbose: bool = False):
