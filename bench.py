@@ -74,6 +74,8 @@ def parse_args(argv=None):
                     help="instead of the decode, run --steps device-to-device copies of MIB MiB: the plain copy "
                          "kernel of known size that scales rocprofv3's FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--rot", action="store_true", help="c4-unpack: rotate history rows back (canonical FWHT)")
+    ap.add_argument("--two-launch", action="store_true",
+                    help="c4-write: the reference's two launches (mode 0, mode 1) instead of one fused launch")
     ap.add_argument("--config", default="c2", choices=("c2", "c3", "c4", "c4-write", "c4-unpack", "c4-fwht"),
                     help="which configuration to measure (c2: the headline line)")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "decode_c2_traffic.md"),
@@ -455,14 +457,15 @@ def bench_c4_write(a) -> None:
 
     def step(i):
         k, v, cache, table = sets[i % P]
-        ops.write(k, v, qsl, sl, tail_idx, js, jp, cache, table, tail_k)
+        ops.write(k, v, qsl, sl, tail_idx, js, jp, cache, table, tail_k, fused=not a.two_launch)
 
     ms = time_graph(step, a.steps, a.warmup)
     alg = 2 * B * T * Hkv * D * 2 + B * pages * Hkv * RB
+    launches = "two launches: mode 0, mode 1" if a.two_launch else "one launch: mode 2"
     _line("chunked-prefill write us/step + achieved HBM GB/s (% peak), int4, 8 x 2048 tokens", ms * 1e3, alg,
           {"workload": f"C4 write: {B} x {T} new tokens, {Hkv} kv heads, D {D}, int{bits} (512 page jobs x {Hkv} "
-                       f"heads, two launches)", "global_batch": B, "tokens": B * T},
-          f"write_kernel<{D},{bits},bf16> x 2 (mode 0, mode 1)")
+                       f"heads, {launches})", "global_batch": B, "tokens": B * T},
+          f"write_kernel<{D},{bits},bf16> ({launches})")
 
 
 def bench_c4_unpack(a) -> None:

@@ -62,7 +62,9 @@ int kush_append(int head_dim, int bits, int dtype, const void* k, const void* v,
  * [query_start_loc[s], query_start_loc[s+1]) at positions ending at seq_lens[s] (already
  * counting them); job j covers logical page job_page[j] of sequence job_seq[j]. mode 0 writes V
  * rows and quantizes pages the chunk completes; mode 1 stashes the K rows of still-partial pages
- * in the tail. Call mode 0 for all jobs, then mode 1, on the same stream.
+ * in the tail. Call mode 0 for all jobs, then mode 1, on the same stream. mode 2 (no counterpart
+ * in the reference) does both in one launch; it needs a job for every page each sequence's chunk
+ * touches (the job list every caller of the reference builds, _ops.py:342-344).
  * Replaces kush_write (gpu.mojo:241-276) as launched by Ops.write (_ops.py:82-101). */
 int kush_write(int head_dim, int bits, int dtype, const void* k, const void* v, int64_t k_row_stride,
                int64_t v_row_stride, const int32_t* query_start_loc, const int32_t* seq_lens,

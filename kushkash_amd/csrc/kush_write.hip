@@ -242,10 +242,10 @@ __device__ __forceinline__ void page_task(const IN* __restrict__ k_tail, const I
     __syncthreads();   // tile is free again
 }
 
-// n rows of D elements from src (row stride src_stride) to dst (row stride D)
-template <int D, typename IN, bool VEC>
+// n rows of D elements from src (row stride src_stride) to dst (row stride D), by THREADS threads
+template <int D, typename IN, bool VEC, int THREADS = WRITE_THREADS>
 __device__ __forceinline__ void copy_rows(IN* __restrict__ dst, const IN* __restrict__ src, int64_t src_stride, int n) {
-    for (int i = threadIdx.x; i < n * (D / 8); i += WRITE_THREADS) {
+    for (int i = threadIdx.x; i < n * (D / 8); i += THREADS) {
         const int r = i / (D / 8), j = 8 * (i % (D / 8));
         copy8<VEC>(dst + r * D + j, src + (int64_t)r * src_stride + j);
     }
@@ -290,8 +290,13 @@ __global__ __launch_bounds__(256) void advance_kernel(int32_t* seq_lens, int pos
 // write the page's new V rows and, if the page is complete, quantize its K (older rows from the
 // tail, newer from the chunk). Mode 1 (tail_kernel) then stashes the new K rows of still-partial
 // pages in the tail: two launches, so no tail is read and written by the same one.
+// FUSE (mode 2): mode 1 in the same launch. A sequence's tail is read only by the job of its first
+// touched page (page ctx / 32, when ctx % 32 != 0 and the page completes) and written only for its
+// last page (seq_lens / 32, when left partial). When both happen on different pages, the first
+// page's job writes the tail after its own reads (same workgroup, behind page_task's last barrier);
+// otherwise the partial page's job does. Needs a job for every page the chunk touches.
 // Contract: gpu.mojo:241-276, cpu.mojo:273-304.
-template <int D, int BITS, typename IN, bool VEC>
+template <int D, int BITS, typename IN, bool VEC, bool FUSE>
 __global__ __launch_bounds__(write_threads<D>()) void write_kernel(
     const IN* __restrict__ k, const IN* __restrict__ v, int64_t k_stride, int64_t v_stride,
     const int32_t* __restrict__ qsl, const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ tail_idx,
@@ -317,6 +322,16 @@ __global__ __launch_bounds__(write_threads<D>()) void write_kernel(
                                                         k_stride, split, complete,
                                                         v + (int64_t)(q0 + lo - ctx) * v_stride + hoff, v_stride,
                                                         lo - ps, hi - ps, rec, lds);
+    }
+    if constexpr (FUSE) {
+        const int last = total / PAGE, first = ctx / PAGE;
+        const int owner = (ctx % PAGE != 0 && last != first) ? first : last;
+        if (total % PAGE != 0 && ps / PAGE == owner) {
+            const int pl = last * PAGE;
+            const int lo2 = pl > ctx ? pl : ctx;
+            copy_rows<D, IN, VEC, write_threads<D>()>(tail + (lo2 - pl) * D, k + (int64_t)(q0 + lo2 - ctx) * k_stride + hoff,
+                                                      k_stride, total - lo2);
+        }
     }
 }
 
@@ -386,7 +401,7 @@ extern "C" int kush_write(int head_dim, int bits, int dtype, const void* k, cons
                           const int32_t* tail_idx, const int32_t* job_seq, const int32_t* job_page, int32_t n_jobs,
                           int32_t mode, void* cache, int64_t block_stride, int64_t head_stride, void* tail_k,
                           const int32_t* block_table, int64_t bt_stride, int32_t hkv, void* stream) {
-    if (n_jobs < 0 || hkv <= 0 || (mode != 0 && mode != 1))
+    if (n_jobs < 0 || hkv <= 0 || mode < 0 || mode > 2)
         return kush_fail(-2, "kush_write: bad n_jobs %d / hkv %d / mode %d", n_jobs, hkv, mode);
     return dispatch_shape(head_dim, bits, dtype, "kush_write", [&](auto dd, auto bb, auto in) -> int {
         constexpr int D = decltype(dd)::value, BITS = decltype(bb)::value;
@@ -394,8 +409,9 @@ extern "C" int kush_write(int head_dim, int bits, int dtype, const void* k, cons
         if (n_jobs == 0) return 0;
         const bool vec = rows_aligned<IN>(k, v, k_stride, v_stride, tail_k);
         hipStream_t st = (hipStream_t)stream;
-        if (mode == 0) {
-            auto kern = vec ? write_kernel<D, BITS, IN, true> : write_kernel<D, BITS, IN, false>;
+        if (mode != 1) {
+            auto kern = mode == 2 ? (vec ? write_kernel<D, BITS, IN, true, true> : write_kernel<D, BITS, IN, false, true>)
+                                  : (vec ? write_kernel<D, BITS, IN, true, false> : write_kernel<D, BITS, IN, false, false>);
             kern<<<dim3(n_jobs, hkv), dim3(write_threads<D>()), 0, st>>>(
                 (const IN*)k, (const IN*)v, k_stride, v_stride, query_start_loc, seq_lens, tail_idx, job_seq, job_page,
                 (uint8_t*)cache, block_stride, head_stride, (IN*)tail_k, block_table, bt_stride, hkv);

@@ -153,12 +153,16 @@ def test_empty_and_short_sequences():
     assert (got - want).abs().max().item() <= out_tol(want, dtype)
 
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_write_rows_any_stride(bits, dtype):
+def test_write_rows_any_stride(bits, dtype, fused):
     """k / v rows whose row stride breaks 16-byte alignment (a free row stride, as the reference's
     _ops.py:6-15 allows) pack the same record bytes and tails as contiguous rows; chunks that start
-    mid-page and end mid-page (split K pages, mode-1 tails), then appends with pos_offset -1."""
+    mid-page and end mid-page (split K pages, mode-1 tails), then appends with pos_offset -1. The
+    second chunks of sequences 0 and 1 complete a page that reads the tail and leave a later page
+    partial (the case where the one-launch write's first-page job writes the tail after reading it);
+    fused=False runs the reference's two launches."""
     torch.manual_seed(bits)
     S, H, D = 3, 2, 128
     ops = kk.Ops(torch.device(DEV), D, bits, 1, dtype)
@@ -197,7 +201,7 @@ def test_write_rows_any_stride(bits, dtype):
                 vb2[:, :H * D] = vr.flatten(1)
                 kr, vr = kb2[:, :H * D].unflatten(1, (H, D)), vb2[:, :H * D].unflatten(1, (H, D))
             sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
-            ops.write(kr, vr, qsl, sl, tail_idx, js, jp, cache, bt, tail_k)
+            ops.write(kr, vr, qsl, sl, tail_idx, js, jp, cache, bt, tail_k, fused=fused)
             done = list(lens)
         # appends: one token per sequence at position seq_lens - 1 (vLLM convention)
         for step in range(2):
