@@ -29,6 +29,8 @@ FLAGS = [
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     # no packed-fp32 VALU forms (v_pk_fma_f32 / v_pk_mul_f32 / v_pk_add_f32) anywhere
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the decode kernels then need no v_accvgpr moves in their page loop
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wno-pass-failed",
 ]
 

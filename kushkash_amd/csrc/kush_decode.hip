@@ -548,13 +548,16 @@ __device__ __forceinline__ float fetch(const float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// grid (S, Hkv, n_splits * ceil(G / 16)), block NW * 64. ST = 2 (G <= 8): two page streams share the
+// grid (S, Hkv, n_splits * ceil(G / 16)), block NW * 64. Registers are budgeted for two waves per SIMD
+// (amdgpu_waves_per_eu(2); the library is built with MFMA accumulators in VGPRs): with a 512-register
+// budget the 4-wave variant used 236 VGPRs + 76 AGPRs and spent 46 v_accvgpr moves per page in its
+// loop; at <= 256 it needs none, and two 4-wave workgroups fit on one CU. ST = 2 (G <= 8): two page streams share the
 // MFMA columns (page A of each pair in columns 0-7, page B in 8-15); ST = 1: one page's 16 heads.
 // NS > 1: each workgroup writes its split's partials; with `sync` (one zeroed int32 per
 // (sequence, kv head, head chunk)), the last workgroup of a (sequence, kv head, head chunk) to
 // finish merges all splits into `out` and resets its counter, so no second launch is needed.
 template <int D, int BITS, typename IN, int NW, int ST>
-__global__ __launch_bounds__(NW * WAVE) void decode_kernel(
+__global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) void decode_kernel(
     const IN* __restrict__ qg, IN* __restrict__ out, const uint8_t* __restrict__ cache, int64_t bs, int64_t hs,
     const IN* __restrict__ tail_k, const int32_t* __restrict__ tail_idx, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ seq_lens, int64_t bt_stride, int H, int G, float p2, float rs, int NS,
