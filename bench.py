@@ -465,7 +465,7 @@ def bench_c4_write(a) -> None:
     _line("chunked-prefill write us/step + achieved HBM GB/s (% peak), int4, 8 x 2048 tokens", ms * 1e3, alg,
           {"workload": f"C4 write: {B} x {T} new tokens, {Hkv} kv heads, D {D}, int{bits} (512 page jobs x {Hkv} "
                        f"heads, {launches})", "global_batch": B, "tokens": B * T},
-          f"write_kernel<{D},{bits},bf16> ({launches})")
+          f"write_kernel<{D},{bits},bf16> ({launches})", traffic_md="write_c4_traffic.md")
 
 
 def bench_c4_unpack(a) -> None:
