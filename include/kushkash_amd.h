@@ -84,13 +84,17 @@ int kush_write(int head_dim, int bits, int dtype, const void* k, const void* v, 
  * workgroup (0 = 8; a configuration whose page ring does not fit in LDS falls back to fewer).
  * seq_order: NULL, or int32 [n_seqs] holding a permutation of the sequences: their workgroups
  * start in that order (longest first balances a ragged batch); the results do not depend on it.
+ * bt_cols: entries per block_table row that may be read (the table's column count), or 0 when
+ * unknown; with it the first block ids of split 0 are fetched before seq_lens is read (a shorter
+ * dependent chain at the start of every workgroup), with 0 only entries below seq_lens are read.
  * q and tail_k must be 16-byte aligned.
  * Replaces kush_decode_tc / kush_decode (gpu.mojo:566-807, :840-1040) and, with split_sync, the
  * kush_combine launch (gpu.mojo:469-491) as issued by Ops.decode (_ops.py:191-213). */
 int kush_decode(int head_dim, int bits, int group, int dtype, const void* q, void* out, const void* cache,
                 int64_t block_stride, int64_t head_stride, const void* tail_k, const int32_t* tail_idx,
-                const int32_t* block_table, const int32_t* seq_lens, int64_t bt_row_stride, int32_t hkv,
-                float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t* split_sync, int32_t waves,
+                const int32_t* block_table, const int32_t* seq_lens, int64_t bt_row_stride, int32_t bt_cols,
+                int32_t hkv, float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t* split_sync,
+                int32_t waves,
                 const int32_t* seq_order, int32_t n_seqs, void* stream);
 
 /* Walsh-Hadamard rotation of rows of head_dim elements: y[r] = fwht(x[r]) for r < rows (row strides
@@ -126,7 +130,7 @@ int kush_combine(int head_dim, int group, int dtype, void* out, const float* par
  * reference raises the driver's error string directly (_cuda.py:39-43). */
 const char* kush_last_error(void);
 
-/* ABI revision of this header (4). No reference counterpart. */
+/* ABI revision of this header (5). No reference counterpart. */
 int kush_abi_version(void);
 
 #ifdef __cplusplus

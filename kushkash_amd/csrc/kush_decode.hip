@@ -560,7 +560,7 @@ template <int D, int BITS, typename IN, int NW, int ST>
 __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) void decode_kernel(
     const IN* __restrict__ qg, IN* __restrict__ out, const uint8_t* __restrict__ cache, int64_t bs, int64_t hs,
     const IN* __restrict__ tail_k, const int32_t* __restrict__ tail_idx, const int32_t* __restrict__ block_table,
-    const int32_t* __restrict__ seq_lens, int64_t bt_stride, int H, int G, float p2, float rs, int NS,
+    const int32_t* __restrict__ seq_lens, int64_t bt_stride, int bt_cols, int H, int G, float p2, float rs, int NS,
     float* __restrict__ part_ml, float* __restrict__ part_o, int32_t* __restrict__ sync,
     const int32_t* __restrict__ seq_order) {
     using F = Fmt<D, BITS>;
@@ -603,13 +603,32 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     const int z = blockIdx.z % NS, gc = blockIdx.z / NS, g0 = gc * 16;
     const int Gc = min(16, G - g0);
 
+    const int32_t* bt = block_table + (int64_t)s * bt_stride;
+    const int64_t qbase = ((int64_t)s * H + h) * G * D + (int64_t)g0 * D;
+    // Issued before the length is read, which neither depends on: this lane's q head (B column r16)
+    // over its contraction dims (8 consecutive dims per K-step; lanes of heads past the chunk read
+    // the chunk's last head and zero it later) and, for split 0 (whose pages start at 0), the first
+    // window's block ids up to the table's column count bt_cols (entries past the length are never
+    // used). The length then arrives with them instead of before them.
+    const int hq = ST == 2 ? (r16 & 7) : r16;                            // the head of this lane's column
+    const bool gv = hq < Gc;
+    float qv[KSTEPS][8];
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) load8(qg + qbase + (int64_t)min(hq, Gc - 1) * D + kdim<D, BITS>(kk, q, 0), qv[kk]);
+    constexpr int PRE = WIN / (NW * WAVE);                               // prefetched ids per thread
+    const int npre = z == 0 ? min(WIN, bt_cols) : 0;
+    int pre[PRE];
+#pragma unroll
+    for (int k = 0; k < PRE; ++k) {
+        const int i = (int)threadIdx.x + k * NW * WAVE;
+        pre[k] = i < npre ? bt[i] : 0;
+    }
+
     const int n = seq_lens[s];
     const int full = n / PAGE, tail_n = n % PAGE;
     const int pps = (full + NS - 1) / NS;
     const int p0 = min(full, z * pps), p1 = min(full, p0 + pps);
-    const int32_t* bt = block_table + (int64_t)s * bt_stride;
     const uint8_t* head_base = cache + (int64_t)h * hs;
-    const int64_t qbase = ((int64_t)s * H + h) * G * D + (int64_t)g0 * D;
     const bool has_tail = tail_n > 0 && z == NS - 1;
     uint8_t* const sl0 = ringA + 2 * w * R::SLOT;
     uint8_t* const sl1 = sl0 + R::SLOT;
@@ -639,7 +658,15 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     if (p1 > p0) {
         int wb = p0, wn = min(WIN, p1 - p0), pairs = (wn + 1) / 2;
         const auto load_window = [&]() {
-            for (int i = threadIdx.x; i < wn; i += NW * WAVE) tbl[i] = bt[wb + i];
+            if (wb == 0 && wn <= npre) {                                 // split 0's first window, prefetched
+#pragma unroll
+                for (int k = 0; k < PRE; ++k) {
+                    const int i = (int)threadIdx.x + k * NW * WAVE;
+                    if (i < wn) tbl[i] = pre[k];
+                }
+            } else {
+                for (int i = threadIdx.x; i < wn; i += NW * WAVE) tbl[i] = bt[wb + i];
+            }
             if (threadIdx.x == 0) pair_ctr = 2 * NW;
         };
 #define KUSH_ISSUE_PAIR(SA, SB, P)                                                                 \
@@ -648,15 +675,8 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         issue_page<D, BITS>(SA, (P) < pairs, __builtin_amdgcn_readfirstlane(id2.x), head_base, bs, voff);  \
         issue_page<D, BITS>(SB, 2 * (P) + 1 < wn, __builtin_amdgcn_readfirstlane(id2.y), head_base, bs, voff); \
     }
-        // this lane's q head (B column r16) over its contraction dims (8 consecutive dims per K-step),
-        // in flight with the table loads, and converted before the barrier: no vector memory load of
-        // the compiler's is outstanding once the page DMAs start. Lanes of heads past the chunk read
-        // the chunk's last head and zero it.
-        const int hq = ST == 2 ? (r16 & 7) : r16;                        // the head of this lane's column
-        const bool gv = hq < Gc;
-        float qv[KSTEPS][8];
-#pragma unroll
-        for (int kk = 0; kk < KSTEPS; ++kk) load8(qg + qbase + (int64_t)min(hq, Gc - 1) * D + kdim<D, BITS>(kk, q, 0), qv[kk]);
+        // q (loaded above) is converted and the window's ids stored before the barrier: no vector
+        // memory load of the compiler's is outstanding once the page DMAs start
         load_window();
         // q' = q p2 as fp16 (+ its low part for fp32 q): qh, ql for the bias MFMAs; qa, qla the Q'
         // sources, divided by 16 in the int4 K-steps of high nibbles
@@ -947,13 +967,13 @@ __global__ __launch_bounds__(256) void combine_kernel(IN* __restrict__ out, cons
 template <int D, int BITS, typename IN, int NW>
 static int launch_decode(dim3 grid, hipStream_t stream, const void* q, void* out, const void* cache, int64_t bs,
                          int64_t hs, const void* tail_k, const int32_t* tail_idx, const int32_t* block_table,
-                         const int32_t* seq_lens, int64_t bt_stride, int hkv, int group, float p2, float rs, int n_splits,
+                         const int32_t* seq_lens, int64_t bt_stride, int bt_cols, int hkv, int group, float p2, float rs, int n_splits,
                          float* part_ml, float* part_o, int32_t* sync, const int32_t* seq_order) {
     // two page streams whenever the heads of a kv head fit in half the MFMA columns
     auto kern = group <= 8 ? decode_kernel<D, BITS, IN, NW, 2> : decode_kernel<D, BITS, IN, NW, 1>;
     kern<<<grid, dim3(NW * WAVE), 0, stream>>>(
         (const IN*)q, (IN*)out, (const uint8_t*)cache, bs, hs, (const IN*)tail_k, tail_idx, block_table, seq_lens,
-        bt_stride, hkv, group, p2, rs, n_splits, part_ml, part_o, sync, seq_order);
+        bt_stride, bt_cols, hkv, group, p2, rs, n_splits, part_ml, part_o, sync, seq_order);
     return kush_check_launch("kush_decode");
 }
 
@@ -963,12 +983,12 @@ using namespace kush;
 
 extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const void* q, void* out, const void* cache,
                            int64_t block_stride, int64_t head_stride, const void* tail_k, const int32_t* tail_idx,
-                           const int32_t* block_table, const int32_t* seq_lens, int64_t bt_stride, int32_t hkv,
-                           float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t* split_sync,
+                           const int32_t* block_table, const int32_t* seq_lens, int64_t bt_stride, int32_t bt_cols,
+                           int32_t hkv, float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t* split_sync,
                            int32_t waves, const int32_t* seq_order, int32_t n_seqs, void* stream) {
-    if (n_seqs < 0 || hkv <= 0 || group <= 0 || n_splits <= 0)
-        return kush_fail(-2, "kush_decode: bad n_seqs %d / hkv %d / group %d / n_splits %d", n_seqs, hkv, group,
-                         n_splits);
+    if (n_seqs < 0 || hkv <= 0 || group <= 0 || n_splits <= 0 || bt_cols < 0)
+        return kush_fail(-2, "kush_decode: bad n_seqs %d / hkv %d / group %d / n_splits %d / bt_cols %d", n_seqs, hkv,
+                         group, n_splits, bt_cols);
     if (n_splits > 1 && (part_ml == nullptr || part_o == nullptr))
         return kush_fail(-2, "kush_decode: n_splits %d needs the partial buffers", n_splits);
     if (((uintptr_t)cache | (uint64_t)block_stride | (uint64_t)head_stride) & 15)
@@ -998,7 +1018,7 @@ extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const v
         using IN = decltype(in);
         if (n_seqs == 0) return 0;
 #define KUSH_DECODE_ARGS grid, st, q, out, cache, block_stride, head_stride, tail_k, tail_idx, block_table, seq_lens, \
-                         bt_stride, hkv, group, p2, rs, n_splits, part_ml, part_o, split_sync, seq_order
+                         bt_stride, bt_cols, hkv, group, p2, rs, n_splits, part_ml, part_o, split_sync, seq_order
         // the largest of the requested, 4 and 2 waves whose rings fit in LDS
         if (waves >= 8) {
             if constexpr (decode_fits<D, BITS, 8>()) return launch_decode<D, BITS, IN, 8>(KUSH_DECODE_ARGS);

@@ -53,7 +53,7 @@ def test_abi_version(lib):
 
 def _decode_args(**kw):
     a = dict(head_dim=128, bits=4, group=7, dtype=2, q=None, out=None, cache=None, bs=0, hs=0, tail_k=None,
-             tail_idx=None, bt=None, seq_lens=None, bt_stride=0, hkv=4, scale=1.0, n_splits=1, part_ml=None,
+             tail_idx=None, bt=None, seq_lens=None, bt_stride=0, bt_cols=0, hkv=4, scale=1.0, n_splits=1, part_ml=None,
              part_o=None, sync=None, waves=0, seq_order=None, n_seqs=1, stream=None)
     a.update(kw)
     return list(a.values())
