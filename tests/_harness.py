@@ -3,6 +3,7 @@ own tests, and tolerance helpers."""
 from __future__ import annotations
 
 import contextlib
+import math
 
 import torch
 
@@ -61,8 +62,19 @@ def split_record(rec: torch.Tensor, D: int, bits: int):
     return kq, meta[..., :D], meta[..., D:2 * D], vq, meta[..., 2 * D:2 * D + PAGE], meta[..., 2 * D + PAGE:]
 
 
+def half_ulp(x: float, dtype: torch.dtype) -> float:
+    """Half an ulp of `dtype` at magnitude |x| (the largest rounding error of a value of that size):
+    2^(e - p) for |x| in [2^e, 2^(e+1)) and p significant bits (fp32 24, fp16 11, bf16 8)."""
+    p = {torch.float32: 24, torch.float16: 11, torch.bfloat16: 8}[dtype]
+    x = abs(float(x))
+    if x == 0.0:
+        return 0.0
+    e = math.frexp(x)[1] - 1                       # x = m 2^(e+1), m in [0.5, 1)
+    return math.ldexp(1.0, e - p)
+
+
 def out_tol(ref: torch.Tensor, dtype: torch.dtype, base: float = 2e-3) -> float:
     """Max-abs tolerance of a decode output in `dtype` against an fp32 reference: `base` plus half an
-    ulp of the output dtype at the largest |ref| (the rounding of the output itself)."""
-    half_ulp = {torch.float32: 2.0 ** -24, torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -9}[dtype]
-    return base + float(ref.abs().max()) * half_ulp
+    ulp of the output dtype at the largest |ref| (the rounding of the output itself; no element of
+    smaller magnitude rounds further)."""
+    return base + half_ulp(float(ref.abs().max()), dtype)

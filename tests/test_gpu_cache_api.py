@@ -19,14 +19,13 @@ import torch
 import torch.nn.functional as F
 
 import kushkash_amd as kk
+from _harness import half_ulp
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-BF16_HALF_ULP = 2.0 ** -9
-
-
 def _bound(ref: torch.Tensor, roundings: int) -> float:
-    return 2e-3 + roundings * BF16_HALF_ULP * float(ref.abs().max())
+    """2e-3 plus `roundings` bf16 roundings (half an ulp each) at the largest |ref|."""
+    return 2e-3 + roundings * half_ulp(float(ref.abs().max()), torch.bfloat16)
 
 
 def test_c1_rotated_cache():

@@ -291,3 +291,59 @@ def test_sequence_order_does_not_change_results(ns):
     o.decode(q.float().cpu(), want, cache.cpu(), bt.cpu(), seq_lens.cpu(), tail_idx.cpu(), tail_k.float().cpu(),
              D ** -0.5)
     assert (ref.float() - want).abs().max().item() <= out_tol(want, dtype)
+
+
+@pytest.mark.parametrize("waves,ns", [(4, 1), (2, 1), (8, 1), (4, 3)])
+def test_block_id_prefetch_does_not_change_results(waves, ns):
+    """kush_decode through the C ABI with the block table's column count (bt_cols: split 0 fetches its
+    first block ids before the length), with 0 (no prefetch) and with a count below the pages in use
+    (falls back to reading after the length): the same bytes. The table is a view of a wider one
+    (row stride > columns), and the lengths are ragged (0 to 40 pages)."""
+    from kushkash_amd import _lib
+    from kushkash_amd._ops import DTYPE_CODE, _byte_strides
+    torch.manual_seed(17)
+    lens = [1, 40 * PAGE, 0, 17 * PAGE + 5, 3 * PAGE, 31]
+    S, H, G, D, bits, dtype = len(lens), 2, 4, 128, 4, torch.bfloat16
+    ops = kk.Ops(torch.device(DEV), D, bits, G, dtype)
+    pages = -(-max(lens) // PAGE)
+    cache = torch.zeros(S * pages, H, kk.record_bytes(D, bits), dtype=torch.uint8, device=DEV)
+    wide = torch.full((S, pages + 9), -1, dtype=torch.int32, device=DEV)
+    wide[:, :pages] = torch.randperm(S * pages, dtype=torch.int32).view(S, pages).to(DEV)
+    bt = wide[:, :pages]
+    tail_k = torch.zeros(S, H, PAGE, D, dtype=dtype, device=DEV)
+    tail_idx = torch.arange(S, dtype=torch.int32, device=DEV)
+    n = sum(lens)
+    k = torch.randn(n, H, D, dtype=dtype, device=DEV)
+    v = torch.randn(n, H, D, dtype=dtype, device=DEV)
+    qsl = torch.tensor([0] + [sum(lens[:i + 1]) for i in range(S)], dtype=torch.int32, device=DEV)
+    seq_lens = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    jobs = [(s, p) for s in range(S) for p in range(-(-lens[s] // PAGE))]
+    js = torch.tensor([j[0] for j in jobs], dtype=torch.int32, device=DEV)
+    jp = torch.tensor([j[1] for j in jobs], dtype=torch.int32, device=DEV)
+    ops.write(k, v, qsl, seq_lens, tail_idx, js, jp, cache, bt, tail_k)
+    q = torch.randn(S, H * G, D, dtype=dtype, device=DEV)
+    work = torch.empty(S * H * ns * G * (D + 2), dtype=torch.float32, device=DEV)
+    bs, hs = _byte_strides(cache)
+    nml = S * H * ns * G * 2
+
+    def run(bt_cols):
+        out = torch.empty_like(q)
+        _lib.call("kush_decode", D, bits, G, DTYPE_CODE[dtype], q.data_ptr(), out.data_ptr(), cache.data_ptr(), bs, hs,
+                  tail_k.data_ptr(), tail_idx.data_ptr(), bt.data_ptr(), seq_lens.data_ptr(), bt.stride(0), bt_cols, H,
+                  D ** -0.5, ns, work.data_ptr() if ns > 1 else None, work.data_ptr() + nml * 4 if ns > 1 else None,
+                  ops._sync.data_ptr() if ns > 1 else None, waves, None, S, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        return out.cpu()
+
+    ref = run(pages)
+    o = OracleOps("cpu", D, bits, G)
+    want = torch.empty(q.shape)
+    o.decode(q.float().cpu(), want, cache.cpu(), bt.cpu().contiguous(), seq_lens.cpu(), tail_idx.cpu(),
+             tail_k.float().cpu(), D ** -0.5)
+    assert (ref.float() - want).abs().max().item() <= out_tol(want, dtype)
+    for cols in (0, 3):
+        got = run(cols)
+        if waves == 8:                       # pairs handed out dynamically: equal to rounding
+            assert (got.float() - ref.float()).abs().max().item() <= out_tol(want, dtype)
+        else:
+            assert torch.equal(got, ref), cols
