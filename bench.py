@@ -14,6 +14,12 @@ The 155 MB of records of one pool fit in the 256 MB Infinity Cache, so steps rot
 --pools independent KV pools (default 4, 621 MB) and every step reads records that left the
 cache.
 
+Timing: both graphs (--warmup steps, then exactly --steps steps) are captured first; the warm-up
+graph is replayed, the host synchronizes, and one replay of the timed graph is bracketed by HIP
+events. The default warm-up of 1,000 steps (~35 ms for C2) brings the GPU to its steady clocks: the
+first C2 line of a fresh process measured 35.0-38.2 us with 20 warm-up steps, 34.3-35.8 with 200 and
+33.1-33.2 with 1,000.
+
 Prints one JSON line (the driver's contract) with "roofline" (decode kernel: algorithmic bytes /
 its mean duration, from HIP events around the graph of decode kernels) and
 "cpu_baseline" (the C restatement of the reference CPU path, oracle/, on the host cores).
@@ -26,7 +32,7 @@ default, c2, is the headline):
   c4        Qwen3-8B decode, 32 q / 8 kv heads, D 128, int4, batch 8 x 131,072 tokens (K bias sigma 4 on
             5% of channels), split-K by the Ops.splits policy (--sweep adds NS 64, 128, 256 ...)
   c4-write  the chunked-prefill write of 2,048 new tokens per sequence of that layer (8 x 2,048 tokens,
-            two ordered launches), quantize-and-pack bytes read + written
+            one launch; --two-launch for the reference's two), quantize-and-pack bytes read + written
   c4-unpack the packed-prefill unpack of one sequence of that layer (131,072 history tokens = 4,096
             full pages dequantized, 2,048 new rows copied; kp / vp [133,120, 8, 128] bf16), records
             read + rows written (--rot also rotates the history back)
@@ -56,7 +62,9 @@ def parse_args(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200, help="timed steps (one graph of that many launches)")
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=1000,
+                    help="untimed steps replayed right before the timed ones (the GPU reaches its steady clocks "
+                         "after some tens of ms of sustained load)")
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--hq", type=int, default=28)
@@ -165,12 +173,19 @@ def graph_of(w, ns: int, waves: int, n_steps: int):
 
 def time_steps(w, ns: int, waves: int, steps: int, warmup: int) -> float:
     """Mean ms per step: `warmup` untimed steps (a graph of their own), then exactly `steps` steps in
-    one graph replay bracketed by synchronizations and HIP events on the replay stream."""
-    if warmup:
-        gw, _ = graph_of(w, ns, waves, warmup)
-        gw.replay()
-        del gw
+    one graph replay bracketed by synchronizations and HIP events on the replay stream. Both graphs
+    are captured before either runs, so the timed replay follows the warm-up after one host
+    synchronization, not after the host-side capture (milliseconds of an idle GPU)."""
     g, _ = graph_of(w, ns, waves, steps)
+    gw = graph_of(w, ns, waves, warmup)[0] if warmup else None
+    return _timed_replay(g, gw, steps)
+
+
+def _timed_replay(g, gw, steps: int) -> float:
+    """Replay the warm-up graph gw (if any), synchronize, then time one replay of g between HIP events
+    on the replay stream; returns ms per step."""
+    if gw is not None:
+        gw.replay()
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
@@ -269,7 +284,8 @@ def copy_calibration(a) -> None:
 # ---------------------------------------------------------------- other configurations (C3, C4)
 def time_graph(step, steps: int, warmup: int) -> float:
     """Mean ms per call of step(i): `warmup` calls in a graph of their own, then exactly `steps`
-    calls captured in one graph, replayed once between HIP events on the replay stream."""
+    calls captured in one graph, replayed once between HIP events on the replay stream (both graphs
+    captured first, as in time_steps)."""
     def capture(n):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
@@ -280,18 +296,9 @@ def time_graph(step, steps: int, warmup: int) -> float:
     for i in range(2):                       # eager calls first (lazy init outside the capture)
         step(i)
     torch.cuda.synchronize()
-    if warmup:
-        gw = capture(warmup)
-        gw.replay()
-        torch.cuda.synchronize()
-        del gw
     g = capture(steps)
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    g.replay()
-    b.record()
-    torch.cuda.synchronize()
-    return a.elapsed_time(b) / steps
+    gw = capture(warmup) if warmup else None
+    return _timed_replay(g, gw, steps)
 
 
 def ragged_cache(ops, lens, room: int, Hkv: int, bias_sigma: float, bias_frac: float, gen, dev):
