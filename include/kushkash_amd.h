@@ -52,11 +52,15 @@ extern "C" {
  * seq_lens[s] + pos_offset; negative positions (padding rows) are skipped. K goes to the exact
  * tail and its page is quantized when the token fills it; V is quantized straight into its
  * record row. advance != 0 stores pos + 1 back into seq_lens[s].
+ * rot (no counterpart in the reference, which rotates with a GEMM outside the kernels): 1 rotates
+ * each k / v row by the canonical Walsh-Hadamard transform, rounded to dtype, before it is
+ * quantized or stashed (the bytes of kush_fwht on the rows followed by rot = 0); 0 stores them as given.
  * Replaces kush_append (gpu.mojo:207-238) as launched by Ops.append (_ops.py:66-80). */
 int kush_append(int head_dim, int bits, int dtype, const void* k, const void* v, int64_t k_row_stride,
                 int64_t v_row_stride, int32_t* seq_lens, int32_t pos_offset, int32_t advance,
                 const int32_t* tail_idx, void* cache, int64_t block_stride, int64_t head_stride, void* tail_k,
-                const int32_t* block_table, int64_t bt_row_stride, int32_t hkv, int32_t n_seqs, void* stream);
+                const int32_t* block_table, int64_t bt_row_stride, int32_t hkv, int32_t n_seqs, int32_t rot,
+                void* stream);
 
 /* Ragged multi-token write, one launch per mode: sequence s owns rows
  * [query_start_loc[s], query_start_loc[s+1]) at positions ending at seq_lens[s] (already
@@ -64,13 +68,14 @@ int kush_append(int head_dim, int bits, int dtype, const void* k, const void* v,
  * rows and quantizes pages the chunk completes; mode 1 stashes the K rows of still-partial pages
  * in the tail. Call mode 0 for all jobs, then mode 1, on the same stream. mode 2 (no counterpart
  * in the reference) does both in one launch; it needs a job for every page each sequence's chunk
- * touches (the job list every caller of the reference builds, _ops.py:342-344).
+ * touches (the job list every caller of the reference builds, _ops.py:342-344). rot: as in
+ * kush_append (rows from the chunk are rotated; rows read back from a tail are rotated already).
  * Replaces kush_write (gpu.mojo:241-276) as launched by Ops.write (_ops.py:82-101). */
 int kush_write(int head_dim, int bits, int dtype, const void* k, const void* v, int64_t k_row_stride,
                int64_t v_row_stride, const int32_t* query_start_loc, const int32_t* seq_lens,
                const int32_t* tail_idx, const int32_t* job_seq, const int32_t* job_page, int32_t n_jobs,
                int32_t mode, void* cache, int64_t block_stride, int64_t head_stride, void* tail_k,
-               const int32_t* block_table, int64_t bt_row_stride, int32_t hkv, void* stream);
+               const int32_t* block_table, int64_t bt_row_stride, int32_t hkv, int32_t rot, void* stream);
 
 /* Decode attention of one query per sequence over its seq_lens[s] cached tokens, softmax scale
  * `scale`. n_splits == 1 writes out. n_splits > 1 splits every sequence's pages into n_splits
@@ -87,6 +92,9 @@ int kush_write(int head_dim, int bits, int dtype, const void* k, const void* v, 
  * bt_cols: entries per block_table row that may be read (the table's column count), or 0 when
  * unknown; with it the first block ids of split 0 are fetched before seq_lens is read (a shorter
  * dependent chain at the start of every workgroup), with 0 only entries below seq_lens are read.
+ * rot (no reference counterpart): 1 for a cache written with rot = 1: q is rotated by the canonical
+ * Walsh-Hadamard transform (rounded to dtype, as kush_fwht) on load and the output rotated back
+ * before its one rounding to dtype; the split partials stay unrotated (kush_combine takes the same rot).
  * q and tail_k must be 16-byte aligned.
  * Replaces kush_decode_tc / kush_decode (gpu.mojo:566-807, :840-1040) and, with split_sync, the
  * kush_combine launch (gpu.mojo:469-491) as issued by Ops.decode (_ops.py:191-213). */
@@ -94,8 +102,7 @@ int kush_decode(int head_dim, int bits, int group, int dtype, const void* q, voi
                 int64_t block_stride, int64_t head_stride, const void* tail_k, const int32_t* tail_idx,
                 const int32_t* block_table, const int32_t* seq_lens, int64_t bt_row_stride, int32_t bt_cols,
                 int32_t hkv, float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t* split_sync,
-                int32_t waves,
-                const int32_t* seq_order, int32_t n_seqs, void* stream);
+                int32_t waves, const int32_t* seq_order, int32_t n_seqs, int32_t rot, void* stream);
 
 /* Walsh-Hadamard rotation of rows of head_dim elements: y[r] = fwht(x[r]) for r < rows (row strides
  * in elements; y may alias x), in the canonical order — butterflies at strides 1, 2, ..., D/2, then
@@ -124,13 +131,13 @@ int kush_unpack(int head_dim, int bits, int dtype, const void* cache, int64_t bl
 /* Merge kush_decode's split partials into out [n_seqs][hkv*group][head_dim].
  * Replaces kush_combine (gpu.mojo:469-491) as launched by Ops.decode (_ops.py:212-213). */
 int kush_combine(int head_dim, int group, int dtype, void* out, const float* part_ml, const float* part_o,
-                 int32_t n_splits, int32_t hkv, int32_t n_seqs, void* stream);
+                 int32_t n_splits, int32_t hkv, int32_t n_seqs, int32_t rot, void* stream);
 
 /* Message of the last failing call on this thread ("" if none). No reference counterpart: the
  * reference raises the driver's error string directly (_cuda.py:39-43). */
 const char* kush_last_error(void);
 
-/* ABI revision of this header (5). No reference counterpart. */
+/* ABI revision of this header (6). No reference counterpart. */
 int kush_abi_version(void);
 
 #ifdef __cplusplus

@@ -8,7 +8,9 @@ Memory per layer
                                           are already final in the page's record
 Shared by all layers: block_table int32 [B, max_pages] (logical -> physical page).
 With rotation on (rotate=, KUSHKASH_ROTATE) pages and tail hold K H and V H (Hadamard H); every
-public method takes and returns unrotated tensors.
+public method takes and returns unrotated tensors. The rotation is the reference's GEMM by default;
+rotate_in_kernels=True folds it into the kernels instead (the canonical Walsh-Hadamard transform
+inside the write, append and decode launches: no rotation GEMMs per step).
 """
 from __future__ import annotations
 
@@ -49,13 +51,16 @@ class KushCache:
         scale: softmax scale (default 1/sqrt(head_dim)).
         rotate: Hadamard-rotate K, V and q inside the cache. None: KUSHKASH_ROTATE (auto: on for
             4-bit, off for 8-bit). Inputs and outputs stay unrotated.
+        rotate_in_kernels: with rotation on, rotate inside the kernels (canonical Walsh-Hadamard
+            transform, as Ops.fwht) instead of with a GEMM before and after them. No counterpart in
+            the reference; the rotated values differ from the GEMM's only in rounding.
     Contract: kushkash/cache.py:43-246.
     """
 
     def __init__(self, num_layers: int, num_kv_heads: int, num_q_heads: int, head_dim: int, *,
                  batch_size: int = 1, bits: int = 4, device: str | torch.device = "cuda",
                  dtype: torch.dtype = torch.float16, max_length: int | None = None, scale: float | None = None,
-                 rotate: bool | None = None):
+                 rotate: bool | None = None, rotate_in_kernels: bool = False):
         if bits not in (4, 8):
             raise ValueError("bits must be 4 or 8")
         if num_q_heads % num_kv_heads:
@@ -76,6 +81,7 @@ class KushCache:
         self.kdtype = dtype if self.gpu else torch.float32            # kernel / tail dtype
         self.ops = Ops(self.device, head_dim, bits, self.G, self.kdtype)
         self.rot = hadamard(head_dim, self.device) if rotation_enabled(bits, rotate) else None
+        self.krot = bool(rotate_in_kernels) and self.rot is not None      # rotation folded into the kernels
         self._work = torch.empty(0, dtype=torch.float32, device=self.device)
         pages0 = max(1, -(-(max_length or 4 * PAGE) // PAGE))
         self._pages = 0
@@ -136,13 +142,16 @@ class KushCache:
             return
         n = self._len[layer]
         self._map(-(-(n + T) // PAGE))                 # incl. the partial page (it holds its V rows)
-        k, v = rotate(k, self.rot, self.kdtype), rotate(v, self.rot, self.kdtype)
+        if not self.krot:
+            k, v = rotate(k, self.rot, self.kdtype), rotate(v, self.rot, self.kdtype)
         k = k.transpose(1, 2).to(self.kdtype)          # kernel rows: [B*T, H, D], head stride D
         v = v.transpose(1, 2).to(self.kdtype)
         if k.stride(-1) != 1 or k.stride(-2) != D or k.stride(0) != T * k.stride(1) or v.stride() != k.stride():
             k, v = k.contiguous(), v.contiguous()
         k, v = k.reshape(B * T, H, D), v.reshape(B * T, H, D)
         args = dict(cache=self.pool[layer], block_table=self.block_table, tail_k=self.tail_k[layer])
+        if self.krot:
+            args["rot"] = True
         if T == 1:
             self.ops.append(k, v, self.seq_lens[layer], self.tail_idx, pos_offset=0, advance=True, **args)
         else:
@@ -159,7 +168,7 @@ class KushCache:
         `_work` (only grows; freeze() fixes it for graph capture) (cache.py:164-183)."""
         if self._len[layer] == 0:
             raise RuntimeError("attend() on an empty cache")
-        q = rotate(q, self.rot, self.kdtype).contiguous()
+        q = (q.to(self.kdtype) if self.krot else rotate(q, self.rot, self.kdtype)).contiguous()
         out = torch.empty_like(q)
         pages = (self._capacity if self._frozen_ns else self._len[layer]) // PAGE
         ns = self._frozen_ns or self.ops.splits(self.B, self.H, pages)
@@ -169,9 +178,11 @@ class KushCache:
                 self._work = torch.empty(need, dtype=torch.float32, device=self.device)
         # GPU: the waves per workgroup from the cached length (the block table may be wider)
         kw = {"waves": self.ops.waves(self.B, self.H, ns, pages)} if self.gpu else {}
+        if self.krot:
+            kw["rot"] = True
         self.ops.decode(q, out, self.pool[layer], self.block_table, self.seq_lens[layer], self.tail_idx,
                         self.tail_k[layer], self.scale, ns, self._work, **kw)
-        return rotate(out, self.rot, self.dtype)
+        return out.to(self.dtype) if self.krot else rotate(out, self.rot, self.dtype)
 
     def attend_chunk(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                      block_bytes: int = 1 << 28) -> torch.Tensor:
@@ -181,10 +192,10 @@ class KushCache:
         if prof:
             ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             ev[0].record()
-        q, k, v = rotate(q, self.rot), rotate(k, self.rot), rotate(v, self.rot)
+        q, k, v = self._rotate(q), self._rotate(k), self._rotate(v)
         out = history_attention(q, k, v, as_records(self.pool[layer]), self.block_table, self._len[layer],
                                 self.tail_k[layer], self.D, self.bits, self.scale, block_bytes)
-        out = rotate(out, self.rot)
+        out = self._rotate(out)
         if prof:
             ev[1].record()
             self.profile.append(ev)
@@ -195,7 +206,15 @@ class KushCache:
         cache rotates. Testing only (cache.py:203-208)."""
         k, v = cached_kv(self.pool[layer], self.block_table, self._len[layer], self.tail_k[layer], self.D,
                          self.bits, self.dtype)
-        return rotate(k, self.rot), rotate(v, self.rot)
+        return self._rotate(k), self._rotate(v)
+
+    def _rotate(self, x: torch.Tensor) -> torch.Tensor:
+        """x rotated (or rotated back: the rotation is its own inverse) the way the cache's contents are:
+        the reference's GEMM, or with rotate_in_kernels the kernels' Walsh-Hadamard transform."""
+        if not self.krot:
+            return rotate(x, self.rot)
+        y = self.ops.fwht(x.to(self.kdtype).reshape(-1, self.D).contiguous())
+        return y.view(x.shape).to(x.dtype)
 
     # ---------------------------------------------------------------- graph-capture support
     def freeze(self, max_tokens: int) -> None:

@@ -1,983 +1,6 @@
-// Fused dequant decode attention over int4/int8 page records for gfx950 (CDNA4), with split-K
-// partials and a log-sum-exp combine. Contract: kushkash/kush/gpu.mojo:566-807 (decode),
-// :418-491 (split ranges, merge, combine), kushkash/_ops.py:182-213 (launch), arithmetic of the
-// reference CPU path kushkash/kush/cpu.mojo:320-451.
-//
-// Mapping onto CDNA4. One workgroup = NW waves (2, 4 or 8) for one (sequence, kv head, split,
-// 16-head chunk). The split's pages go out in pairs over windows of up to 1,024 pages whose block
-// ids sit in an LDS table; with 8 waves a counter in LDS hands out the pairs, with 2 or 4 waves
-// wave w takes pairs w, w + NW, ... Per pair a wave:
-//   1. has both records staged in its private LDS ring by buffer-to-LDS DMA (whole records, 1 KB
-//      per instruction, issued one pair ahead and waited on with explicit vmcnt counts);
-//   2. reads K code rows from the ring and turns them into exact subnormal fp16 operands (one
-//      v_perm and one v_bitop3 per pair of codes), and computes the scores S^T = K . Q'^T on MFMA
-//      16x16x32 f16 with Q' = q' * k_scale as an fp16 pair (q' = q times a power of two; the rest
-//      of scale * log2 e multiplies the fp32 scores); the K-bias and -HALF * k_scale terms come
-//      from two more MFMAs per K-step;
-//   3. runs a page-granular online softmax in base 2 per MFMA column (with G <= 8 two page
-//      streams share the 16 columns: page A in 0-7, page B in 8-15), moving the running max only
-//      when a page exceeds it by more than 2^3;
-//   4. gathers V codes column-wise from the ring (ds_read_b64_tr_b8) into V^T operands and
-//      accumulates O^T += V^T . P'^T on MFMA, with P' = fp16(e * v_scale); -HALF * sum P' comes
-//      from one MFMA and the V bias sum e * v_bias stays in fp32.
-// The partial last page takes exact fp32 K . q scores from the tail (spread over all waves) and V
-// rows from its record. The waves (and streams) merge through the idle ring at the end; with
-// split-K, partials are published write-through and the last workgroup of a (sequence, kv head)
-// merges them in the same launch.
-//
-// MFMA 16x16x32 f16 operand layout used throughout (lane l, r = l % 16, q = l / 16):
-//   A: row r, 8 contraction slots of lane group q;  B: column r, the same 8 slots;
-//   C: rows 4q .. 4q+3 of column r.
-// Which physical dim or token a slot stands for is chosen here (kdim, tok), identically for A
-// and B, so only the C layout is relied upon.
-#include <cmath>
-
-#include "kush_common.h"
-
-namespace kush {
-
-typedef _Float16 h4v __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
-
-// Physical dim of contraction slot j of lane group q in K-step kk (QK^T). The lane owns bytes
-// [q KB, (q+1) KB) of each code row (KB = DC / 4). int4: K-steps come in pairs over 8 of those
-// bytes, 2 pr and 2 pr + 1 taking their low and high nibbles, so the 8 dims of a K-step are
-// consecutive and its scales and biases are one 16-byte read. int8: dims q D/4 + 8 kk + j.
-template <int D, int BITS>
-__device__ __forceinline__ int kdim(int kk, int q, int j) {
-    if constexpr (BITS == 4)
-        return (kk & 1) * (D / 2) + q * (D / 8) + 8 * (kk >> 1) + j;
-    else
-        return q * (D / 4) + 8 * kk + j;
-}
-
-// Token of slot j of lane group q in the PV contraction: the token the QK^T accumulators of lane
-// group q hold in register j % 4 of tile j / 4.
-__device__ __forceinline__ int tok(int q, int j) { return 16 * (j >> 2) + 4 * q + (j & 3); }
-
-// ------------------------------------------------------------------ LDS page stage
-// A wave stages whole records in a ring of LDS slots with buffer-to-LDS DMA (64 lanes x 16 bytes per
-// instruction, lane l -> 16-byte chunk l of the instruction's 1 KB). Chunks of the 64 code rows are
-// placed XOR-swizzled within their row, chunk c of row r at position c ^ swz(r), so the column-wise
-// V gathers and the K row reads spread over the 64 LDS banks; the scales and biases stay in place.
-// The swizzle is applied on the source side: the lane that fills LDS chunk L loads record chunk
-// src_chunk(L). A slot is exactly one record: instruction i covers chunks [64 i, 64 i + 64), except
-// the last, which covers the record's last 64 chunks and so rewrites the overlap with the same bytes
-// (a lane past the end of its 1 KB would write zeros beyond the slot).
-template <int D, int BITS>
-struct Ring {
-    using F = Fmt<D, BITS>;
-    static constexpr int CPR = F::DC / 16;                  // 16-byte chunks per code row
-    static constexpr int CODE_CHUNKS = 64 * CPR;            // K rows then V rows
-    static constexpr int CHUNKS = F::REC / 16;
-    static constexpr int DMA = (CHUNKS + WAVE - 1) / WAVE;   // 1 KB instructions per page
-    static constexpr int SLOT = F::REC;                     // LDS bytes per ring slot
-    static constexpr int RSHIFT = F::DC >= 256 ? 0 : (F::DC == 128 ? 1 : (F::DC == 64 ? 2 : 3));
-    static_assert(CHUNKS >= WAVE, "a record spans at least one full instruction");
-    // first LDS chunk filled by instruction i
-    static constexpr int chunk0(int i) { return i < DMA - 1 ? WAVE * i : CHUNKS - WAVE; }
-};
-
-// Swizzle of code row r (0-31 K, 32-63 V). K rows are read row-wise (16 rows by 16 lanes):
-// rows r and r + 4 (DC = 64) must land on different banks, so the swizzle takes the row bits
-// above those that already select the bank. V rows are gathered column-wise, 16 tokens per half
-// wave, t = 16 a + 4 q + b (b < 4, q the lane group, a the tile); u = b | (q & 1) << 2 | a << 3
-// indexes them, and the swizzle takes the bits of u that the row address leaves on one bank.
-template <int D, int BITS>
-__device__ __forceinline__ int swz(int r) {
-    using R = Ring<D, BITS>;
-    if (r < 32) return (r >> R::RSHIFT) & (R::CPR - 1);
-    const int t = r - 32;
-    const int u = (t & 3) | (((t >> 2) & 1) << 2) | (((t >> 4) & 1) << 3);
-    return (u >> R::RSHIFT) & (R::CPR - 1);
-}
-
-// byte offset in a slot of record chunk c (16 bytes) of code row r (0-31 K, 32-63 V)
-template <int D, int BITS>
-__device__ __forceinline__ int slot_chunk(int r, int c) {
-    using R = Ring<D, BITS>;
-    return (r * R::CPR + (c ^ swz<D, BITS>(r))) * 16;
-}
-
-template <int D, int BITS>
-__device__ __forceinline__ uint32_t src_chunk(int L) {
-    using R = Ring<D, BITS>;
-    if (L >= R::CODE_CHUNKS) return (uint32_t)L;             // scales / biases (and padding) in place
-    const int r = L / R::CPR, j = L % R::CPR;
-    return (uint32_t)(r * R::CPR + (j ^ swz<D, BITS>(r)));
-}
-
-// s_waitcnt with only vmcnt(N) (gfx9 encoding: vmcnt [3:0] + [15:14], expcnt [6:4], lgkmcnt [11:8]),
-// then a compiler barrier: no LDS read of the landed data is moved above the wait
-#define KUSH_WAIT_VM(N)                                                                          \
-    do {                                                                                         \
-        __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | (7 << 4) | (15 << 8));      \
-        asm volatile("" ::: "memory");                                                           \
-    } while (0)
-
-// Subnormal fp16 codes: the bit pattern n (0..255) is the fp16 value n * 2^-24, exact, so unsigned
-// code bytes become MFMA operands with one byte shuffle and no arithmetic; the products are exact in
-// fp32 and the 2^24 is applied to the fp32 results. n = c + HALF: the HALF offset is removed through
-// the bias terms. perm(x, 0, 0x0C010C00) = bytes [x0, 0, x1, 0].
-__device__ __forceinline__ h8 sub_codes4(uint32_t lo, uint32_t hi) {    // 4 + 4 nibble values, masked
-    return __builtin_bit_cast(h8, u4{__builtin_amdgcn_perm(0u, lo, 0x0C010C00u), __builtin_amdgcn_perm(0u, lo, 0x0C030C02u),
-                                     __builtin_amdgcn_perm(0u, hi, 0x0C010C00u), __builtin_amdgcn_perm(0u, hi, 0x0C030C02u)});
-}
-
-// int4 codes to operands. The xor with 0x88 turns a two's-complement nibble into n = c + 8; a
-// nibble is then masked in place: a low nibble is the subnormal n, a high nibble lands 4 bits up,
-// as 16 n. Each of (x ^ 0x88888888) & mask is one v_bitop3.
-constexpr uint32_t NIB_XOR = 0x88888888u, NIB_LO = 0x000F000Fu, NIB_HI = 0x00F000F0u;
-
-// K: two words (8 code bytes of a row, dims in order) -> the low nibbles (n) and the high nibbles
-// (16 n) of the 8 bytes, in byte order: v_perm spreads two bytes into the low bytes of the halves.
-__device__ __forceinline__ void k_codes4(uint32_t w0, uint32_t w1, h8& lo, h8& hi) {
-    const uint32_t p[4] = {__builtin_amdgcn_perm(0u, w0, 0x0C010C00u), __builtin_amdgcn_perm(0u, w0, 0x0C030C02u),
-                           __builtin_amdgcn_perm(0u, w1, 0x0C010C00u), __builtin_amdgcn_perm(0u, w1, 0x0C030C02u)};
-    u4 l, h;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        l[i] = (p[i] ^ NIB_XOR) & NIB_LO;
-        h[i] = (p[i] ^ NIB_XOR) & NIB_HI;
-    }
-    lo = __builtin_bit_cast(h8, l);
-    hi = __builtin_bit_cast(h8, h);
-}
-
-// V^T: two words of 4 token bytes each (PV slots 0-3, 4-7) -> low nibbles (n) and high nibbles
-// (16 n) in slot order 0 2 1 3 4 6 5 7: bytes 0 and 2 of a word are masked in place, bytes 1 and 3
-// after a shift by 8. The P' operand takes the same order (VSLOT).
-__device__ __forceinline__ void v_codes4(uint32_t w0, uint32_t w1, h8& lo, h8& hi) {
-    const uint32_t p[4] = {w0, w0 >> 8, w1, w1 >> 8};
-    u4 l, h;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        l[i] = (p[i] ^ NIB_XOR) & NIB_LO;
-        h[i] = (p[i] ^ NIB_XOR) & NIB_HI;
-    }
-    lo = __builtin_bit_cast(h8, l);
-    hi = __builtin_bit_cast(h8, h);
-}
-
-// PV slot held by operand position k (int4: the v_codes4 order; int8: in order)
-template <int BITS>
-__device__ __forceinline__ constexpr int vslot(int k) {
-    return BITS == 4 ? (k & 4) | ((k & 1) << 1) | ((k >> 1) & 1) : k;
-}
-
-// two int8 words (8 codes) -> n = c + 128
-__device__ __forceinline__ h8 int8_sub(uint32_t w0, uint32_t w1) {
-    return sub_codes4(w0 ^ 0x80808080u, w1 ^ 0x80808080u);
-}
-
-// max / sum over the 4 lanes l, l ^ 16, l ^ 32, l ^ 48 (one q head's lane groups), on the VALU
-__device__ __forceinline__ float rows_max(float x) {
-    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = __builtin_fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __builtin_fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-
-__device__ __forceinline__ float rows_sum(float x) {
-    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-    auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-
-typedef int v2i __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) v2i lds_v2i;
-typedef __attribute__((address_space(3))) void lds_void;
-
-// V^T operand gather: within each 16-lane group, ds_read_b64_tr_b8 hands output lane i byte
-// (i % 8) of the 8-byte rows supplied by lanes 2k + (i % 16) / 8, k = 0..7. Lane (2k + half) of
-// group q supplies V token tok(q, k) at byte column 16 ct + 8 half, so lane r of the group receives
-// byte column 16 ct + r of its 8 tokens, in PV slot order.
-template <int D, int BITS>
-__device__ __forceinline__ v2i gather_vt(const uint8_t* slot, int ct, int lane) {
-    const int s16 = lane & 15, q = lane >> 4;
-    const uint8_t* src = slot + slot_chunk<D, BITS>(32 + tok(q, s16 >> 1), ct) + 8 * (s16 & 1);
-    return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(src));
-}
-
-// Softmax update over NP staged pages at once and their PV accumulation from the staged V codes.
-// Scores in log2 units are x = a s[p][j] + b[p] (a > 0) for tokens tok(q, j); masked tokens carry
-// s = -inf. o accumulates in units of 2^-24 (subnormal codes; int4 high-nibble tiles, o[D/32 ..],
-// in units of 2^-20); with P' = fp16(e vs) a page adds sum P' n (MFMA), -HALF sum P' (MFMA into
-// vacc, units of 2^-24) and sum e vb (vb_run), i.e. sum e (vs' c + vb) with vs' = P' / e.
-template <int D, int BITS, int NP>
-__device__ __forceinline__ void consume_pages(const uint8_t* const (&slot)[NP], f4 (&o)[D / 16], f4& vacc,
-                                              const float (&sv)[NP][8], float a, const float (&b)[NP],
-                                              float& m_run, float& l_run, float& vb_run, int lane) {
-    using F = Fmt<D, BITS>;
-    const int q = lane >> 4;
-    float pm = -__builtin_inff();
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-        float mx = sv[p][0];
-#pragma unroll
-        for (int j = 1; j < 8; ++j) mx = __builtin_fmaxf(mx, sv[p][j]);
-        pm = __builtin_fmaxf(pm, __builtin_fmaf(mx, a, b[p]));
-    }
-    // the reference point of the exponentials moves only when the max exceeds it by more than 2^3:
-    // weights stay <= 8 (P' = e vs stays far from fp16 overflow) and most steps skip the O rescale
-    pm = rows_max(pm);
-    const float m_new = pm > m_run + 3.0f ? pm : m_run;
-    const float corr = __builtin_amdgcn_exp2f(m_run - m_new);   // first step: exp2(-inf) = 0
-
-    float lsum = 0.0f, vbsum = 0.0f;
-    h8 pw[NP];
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-        const float bp = b[p] - m_new;
-        const h4v vs0 = *reinterpret_cast<const h4v*>(slot[p] + F::OFF_VS + 8 * q);
-        const h4v vs1 = *reinterpret_cast<const h4v*>(slot[p] + F::OFF_VS + 32 + 8 * q);
-        const h4v vb0 = *reinterpret_cast<const h4v*>(slot[p] + F::OFF_VB + 8 * q);
-        const h4v vb1 = *reinterpret_cast<const h4v*>(slot[p] + F::OFF_VB + 32 + 8 * q);
-        _Float16 pv[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float vsj = (float)(j < 4 ? vs0[j] : vs1[j - 4]);
-            const float vbj = (float)(j < 4 ? vb0[j] : vb1[j - 4]);
-            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[p][j], a, bp));
-            pv[j] = (_Float16)__builtin_fmaf(e, vsj, 0.0f);   // e vs (fma_mix, then one pack per pair)
-            lsum += e;
-            vbsum = __builtin_fmaf(e, vbj, vbsum);
-        }
-#pragma unroll
-        for (int k = 0; k < 8; ++k) pw[p][k] = pv[vslot<BITS>(k)];
-    }
-    l_run = l_run * corr + lsum;
-    vb_run = vb_run * corr + vbsum;
-    m_run = m_new;
-    if (corr != 1.0f) {
-#pragma unroll
-        for (int dt = 0; dt < D / 16; ++dt) o[dt] *= corr;
-        vacc *= corr;
-    }
-
-    constexpr int NCOL = BITS == 4 ? D / 32 : D / 16;
-#pragma unroll
-    for (int ct = 0; ct < NCOL; ++ct)
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            const v2i w = gather_vt<D, BITS>(slot[p], ct, lane);
-            if constexpr (BITS == 4) {
-                h8 lo, hi;
-                v_codes4((uint32_t)w[0], (uint32_t)w[1], lo, hi);
-                o[ct] = mfma16(lo, pw[p], o[ct]);
-                o[ct + D / 32] = mfma16(hi, pw[p], o[ct + D / 32]);
-            } else {
-                o[ct] = mfma16(int8_sub((uint32_t)w[0], (uint32_t)w[1]), pw[p], o[ct]);
-            }
-        }
-    // -HALF sum P' per head: A rows all -HALF 2^-24 (fp16 bits 0x8000 | HALF, exact)
-    const _Float16 nh = __builtin_bit_cast(_Float16, (uint16_t)(0x8000u | (uint32_t)F::HALF));
-    const h8 neg_half = h8{nh, nh, nh, nh, nh, nh, nh, nh};
-#pragma unroll
-    for (int p = 0; p < NP; ++p) vacc = mfma16(neg_half, pw[p], vacc);
-}
-
-// Stage the record of block blk into LDS at dst: R::DMA buffer-to-LDS loads of 1 KB. An invalid page
-// (past the window's last) gets an empty buffer range: the loads then fill the slot with zeros and
-// touch no memory, and still count in vmcnt like a real page.
-// The loads are written in asm so that the compiler does not track them: the page loop waits for
-// them with explicit vmcnt counts alone. Vector loads complete in order, so any vector memory op the
-// compiler adds (issued later) only makes those waits stricter.
-template <int D, int BITS>
-__device__ __forceinline__ void issue_page(uint8_t* dst, bool valid, int blk, const uint8_t* head_base, int64_t bs,
-                                           const uint32_t* voff) {
-    using F = Fmt<D, BITS>;
-    using R = Ring<D, BITS>;
-    const uint64_t rec = (uint64_t)(uintptr_t)(head_base + (int64_t)blk * bs);
-    // raw buffer descriptor: base, stride 0, num_records (0: every lane out of range), dword format
-    const u4 rsrc = u4{(uint32_t)rec, (uint32_t)(rec >> 32) & 0xFFFFu, valid ? (uint32_t)F::REC : 0u, 0x00020000u};
-    const uint32_t lds = (uint32_t)(uintptr_t)(lds_void*)dst;
-    // m0 is reserved by the compiler; nothing else in the decode kernels uses it (checked on their
-    // assembly by tests/test_isa.py), so setting it here is safe
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-#pragma unroll
-    for (int i = 0; i < R::DMA; ++i)
-        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                     :: "s"(lds + R::chunk0(i) * 16), "v"(voff[i]), "s"(rsrc) : "memory", "m0");
-#pragma clang diagnostic pop
-}
-
-// Scores of the 64 tokens of a staged page pair (page 0 at s0, page 1 in the next slot):
-// x = a sacc[p][j / 4][j % 4] + kx[p] in log2 units for token tok(q, j) of page p, head r16, with
-// a = rs 2^24.
-// sacc = K . Q'^T on codes n = c + HALF as subnormal fp16 (units of 2^-24) and Q' = q' ks as an fp16
-// pair qp + qr, q' = q p2 (p2 a power of two: q' is exact in fp16 for bf16 / fp16 q; fp32 q adds
-// its low fp16 part ql). int4 high nibbles enter as 16 n against Q' / 16 (qa holds q' / 16 there).
-// kx = rs (sum_d kb[d] q'[d] - HALF sum_d ks[d] q'[d]): two MFMAs per K-step for both pages, their
-// A rows alternating between the pages' biases and scales (row r: page r % 2, so C register i holds
-// page i % 2).
-template <int D, int BITS, bool QLO>
-__device__ __forceinline__ void pair_scores(const uint8_t* s0, const h8 (&qa)[D / 32],
-                                            const h8 (&qla)[D / 32], const h8 (&qh)[D / 32], const h8 (&ql)[D / 32],
-                                            float (&sv)[2][8], float (&kx)[2], float rs, int lane) {
-    using F = Fmt<D, BITS>;
-    constexpr int KSTEPS = D / 32;
-    constexpr int KBYTES = F::DC / 4;                // K code bytes per lane per 16-token tile
-    const int r16 = lane & 15, q = lane >> 4;
-    const uint8_t* const sl[2] = {s0, s0 + Ring<D, BITS>::SLOT};
-    const uint8_t* const own = s0 + (r16 & 1) * Ring<D, BITS>::SLOT;
-    f4 sacc[2][2];
-#pragma unroll
-    for (int p = 0; p < 2; ++p) sacc[p][0] = sacc[p][1] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    f4 kb_acc = f4{0.0f, 0.0f, 0.0f, 0.0f}, ks_acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) {
-        const int d0 = kdim<D, BITS>(kk, q, 0);
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            h8 a[2];
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-                // code bytes of row 16 tt + r16 for this K-step, from the swizzled slot
-                const int row = 16 * tt + r16;
-                const int byte = q * KBYTES + 8 * (BITS == 4 ? kk >> 1 : kk);
-                const u2 wv = *reinterpret_cast<const u2*>(sl[p] + slot_chunk<D, BITS>(row, byte / 16) + byte % 16);
-                if constexpr (BITS == 4) {
-                    h8 lo, hi;
-                    k_codes4(wv[0], wv[1], lo, hi);
-                    a[tt] = (kk & 1) ? hi : lo;
-                } else {
-                    a[tt] = int8_sub(wv[0], wv[1]);
-                }
-            }
-            const h8 ks8 = *reinterpret_cast<const h8*>(sl[p] + F::OFF_KS + 2 * d0);
-            // Q' = q' ks as an fp16 pair: qp = fp16(q' ks), qr = the exact residual of that product
-            // (plus ql ks for fp32 q), rounded once
-            const h8 qp = qa[kk] * ks8;
-            h8 qr = __builtin_elementwise_fma(qa[kk], ks8, -qp);
-            if constexpr (QLO) qr = __builtin_elementwise_fma(qla[kk], ks8, qr);
-            sacc[p][0] = mfma16(a[0], qp, sacc[p][0]);
-            sacc[p][1] = mfma16(a[1], qp, sacc[p][1]);
-            sacc[p][0] = mfma16(a[0], qr, sacc[p][0]);
-            sacc[p][1] = mfma16(a[1], qr, sacc[p][1]);
-        }
-        const h8 kbo = *reinterpret_cast<const h8*>(own + F::OFF_KB + 2 * d0);
-        const h8 kso = *reinterpret_cast<const h8*>(own + F::OFF_KS + 2 * d0);
-        kb_acc = mfma16(kbo, qh[kk], kb_acc);
-        ks_acc = mfma16(kso, qh[kk], ks_acc);
-        if constexpr (QLO) {
-            kb_acc = mfma16(kbo, ql[kk], kb_acc);
-            ks_acc = mfma16(kso, ql[kk], ks_acc);
-        }
-    }
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) sv[p][j] = sacc[p][j >> 2][j & 3];
-        kx[p] = rs * __builtin_fmaf(-(float)F::HALF, ks_acc[p], kb_acc[p]);
-    }
-}
-
-// ------------------------------------------------------------------ two page streams (G <= 8)
-// With at most 8 q heads per kv head, MFMA column c stands for head c % 8 of page stream c / 8: a
-// page pair puts page A in columns 0-7 and page B in columns 8-15, so each lane's Q', softmax and
-// P' work covers one (head, page) and no column is idle. Each column keeps its own online-softmax
-// state; the streams of a head are merged with the waves at the end.
-
-// Scores of a staged pair (page A at s0, page B in the next slot) for this lane's column: sv[j] for
-// token tok(q, j) of its page, x = a sv[j] + kx. The Q' operand is built once for both pages (each
-// column from its own page's scales); K of page A and of page B each meet it in their own MFMAs,
-// and a column keeps the product with its page.
-template <int D, int BITS, bool QLO>
-__device__ __forceinline__ void pair_scores2(const uint8_t* s0, const h8 (&qa)[D / 32], const h8 (&qla)[D / 32],
-                                             const h8 (&qh)[D / 32], const h8 (&ql)[D / 32], float (&sv)[8],
-                                             float& kx, float rs, int lane) {
-    using F = Fmt<D, BITS>;
-    constexpr int KSTEPS = D / 32;
-    constexpr int KBYTES = F::DC / 4;
-    constexpr int SLOT = Ring<D, BITS>::SLOT;
-    const int r16 = lane & 15, q = lane >> 4, st = r16 >> 3;
-    const uint8_t* const sl[2] = {s0, s0 + SLOT};
-    const uint8_t* const mine = s0 + st * SLOT;                 // the page of this lane's column
-    const uint8_t* const own = s0 + (r16 & 1) * SLOT;           // A row r16 of the bias MFMAs
-    f4 sacc[2][2];
-#pragma unroll
-    for (int p = 0; p < 2; ++p) sacc[p][0] = sacc[p][1] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    f4 kb_acc = f4{0.0f, 0.0f, 0.0f, 0.0f}, ks_acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) {
-        const int d0 = kdim<D, BITS>(kk, q, 0);
-        const h8 ks8 = *reinterpret_cast<const h8*>(mine + F::OFF_KS + 2 * d0);
-        const h8 qp = qa[kk] * ks8;
-        h8 qr = __builtin_elementwise_fma(qa[kk], ks8, -qp);
-        if constexpr (QLO) qr = __builtin_elementwise_fma(qla[kk], ks8, qr);
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            h8 a[2];
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-                const int row = 16 * tt + r16;
-                const int byte = q * KBYTES + 8 * (BITS == 4 ? kk >> 1 : kk);
-                const u2 wv = *reinterpret_cast<const u2*>(sl[p] + slot_chunk<D, BITS>(row, byte / 16) + byte % 16);
-                if constexpr (BITS == 4) {
-                    h8 lo, hi;
-                    k_codes4(wv[0], wv[1], lo, hi);
-                    a[tt] = (kk & 1) ? hi : lo;
-                } else {
-                    a[tt] = int8_sub(wv[0], wv[1]);
-                }
-            }
-            sacc[p][0] = mfma16(a[0], qp, sacc[p][0]);
-            sacc[p][1] = mfma16(a[1], qp, sacc[p][1]);
-            sacc[p][0] = mfma16(a[0], qr, sacc[p][0]);
-            sacc[p][1] = mfma16(a[1], qr, sacc[p][1]);
-        }
-        const h8 kbo = *reinterpret_cast<const h8*>(own + F::OFF_KB + 2 * d0);
-        const h8 kso = *reinterpret_cast<const h8*>(own + F::OFF_KS + 2 * d0);
-        kb_acc = mfma16(kbo, qh[kk], kb_acc);
-        ks_acc = mfma16(kso, qh[kk], ks_acc);
-        if constexpr (QLO) {
-            kb_acc = mfma16(kbo, ql[kk], kb_acc);
-            ks_acc = mfma16(kso, ql[kk], ks_acc);
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) sv[j] = st ? sacc[1][j >> 2][j & 3] : sacc[0][j >> 2][j & 3];
-    kx = rs * __builtin_fmaf(-(float)F::HALF, st ? ks_acc[1] : ks_acc[0], st ? kb_acc[1] : kb_acc[0]);
-}
-
-// Softmax update of this lane's column over its page (scores x = a sv[j] + kx; masked tokens
-// sv = -inf; a column may be masked whole) and the PV accumulation of page A (at s0) into columns
-// 0-7 and page B (at s0 + ds) into columns 8-15: each MFMA takes P' with the other stream's
-// columns zeroed. Units as in consume_pages.
-template <int D, int BITS>
-__device__ __forceinline__ void consume2(const uint8_t* s0, int ds, f4 (&o)[D / 16], f4& vacc, const float (&sv)[8],
-                                         float a, float kx, float& m_run, float& l_run, float& vb_run, int lane) {
-    using F = Fmt<D, BITS>;
-    const int r16 = lane & 15, q = lane >> 4, st = r16 >> 3;
-    const uint8_t* const mine = s0 + st * ds;
-    float pm = sv[0];
-#pragma unroll
-    for (int j = 1; j < 8; ++j) pm = __builtin_fmaxf(pm, sv[j]);
-    pm = rows_max(__builtin_fmaf(pm, a, kx));
-    const float m_new = pm > m_run + 3.0f ? pm : m_run;
-    const bool none = m_new == -__builtin_inff();                 // nothing seen yet in this column
-    const float corr = none ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-    const float bp = none ? 0.0f : kx - m_new;
-
-    const h4v vs0 = *reinterpret_cast<const h4v*>(mine + F::OFF_VS + 8 * q);
-    const h4v vs1 = *reinterpret_cast<const h4v*>(mine + F::OFF_VS + 32 + 8 * q);
-    const h4v vb0 = *reinterpret_cast<const h4v*>(mine + F::OFF_VB + 8 * q);
-    const h4v vb1 = *reinterpret_cast<const h4v*>(mine + F::OFF_VB + 32 + 8 * q);
-    float lsum = 0.0f, vbsum = 0.0f;
-    _Float16 pv[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const float vsj = (float)(j < 4 ? vs0[j] : vs1[j - 4]);
-        const float vbj = (float)(j < 4 ? vb0[j] : vb1[j - 4]);
-        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[j], a, bp));
-        pv[j] = (_Float16)__builtin_fmaf(e, vsj, 0.0f);
-        lsum += e;
-        vbsum = __builtin_fmaf(e, vbj, vbsum);
-    }
-    h8 pw;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) pw[k] = pv[vslot<BITS>(k)];
-    const u4 pu = __builtin_bit_cast(u4, pw);
-    const uint32_t keep_a = st ? 0u : ~0u;
-    const h8 pwa = __builtin_bit_cast(h8, pu & keep_a), pwb = __builtin_bit_cast(h8, pu & ~keep_a);
-    l_run = l_run * corr + lsum;
-    vb_run = vb_run * corr + vbsum;
-    m_run = m_new;
-    if (corr != 1.0f) {
-#pragma unroll
-        for (int dt = 0; dt < D / 16; ++dt) o[dt] *= corr;
-        vacc *= corr;
-    }
-
-    constexpr int NCOL = BITS == 4 ? D / 32 : D / 16;
-#pragma unroll
-    for (int ct = 0; ct < NCOL; ++ct) {
-        const v2i wa = gather_vt<D, BITS>(s0, ct, lane);
-        const v2i wb = gather_vt<D, BITS>(s0 + ds, ct, lane);
-        if constexpr (BITS == 4) {
-            h8 lo, hi;
-            v_codes4((uint32_t)wa[0], (uint32_t)wa[1], lo, hi);
-            o[ct] = mfma16(lo, pwa, o[ct]);
-            o[ct + D / 32] = mfma16(hi, pwa, o[ct + D / 32]);
-            v_codes4((uint32_t)wb[0], (uint32_t)wb[1], lo, hi);
-            o[ct] = mfma16(lo, pwb, o[ct]);
-            o[ct + D / 32] = mfma16(hi, pwb, o[ct + D / 32]);
-        } else {
-            o[ct] = mfma16(int8_sub((uint32_t)wa[0], (uint32_t)wa[1]), pwa, o[ct]);
-            o[ct] = mfma16(int8_sub((uint32_t)wb[0], (uint32_t)wb[1]), pwb, o[ct]);
-        }
-    }
-    const _Float16 nh = __builtin_bit_cast(_Float16, (uint16_t)(0x8000u | (uint32_t)F::HALF));
-    vacc = mfma16(h8{nh, nh, nh, nh, nh, nh, nh, nh}, pw, vacc);   // column c sums its own P'
-}
-
-// Pages per window of the page loop: the block ids of a window sit in an LDS table.
-constexpr int WIN = 1024;
-
-// Static LDS of one decode workgroup: two arrays, each holding one page pair per wave (wave w at
-// 2 w SLOT), the window's block-id table and the pair counter. After the page loop the idle arrays
-// hold everything else: the cross-wave merge in the first; the exact-K tail's q and scores, the
-// waves' softmax state and the split-K flag in the second.
-template <int D, int BITS, int NW>
-constexpr int decode_lds_bytes() {
-    return 4 * NW * Ring<D, BITS>::SLOT + 4 * WIN + 16;
-}
-
-template <int D, int BITS, int NW>
-constexpr bool decode_fits() {
-    return decode_lds_bytes<D, BITS, NW>() <= 160 * 1024;
-}
-
-// byte offsets in the second array of the after-loop scratch: q [16][D] fp32, tail scores [16][PAGE],
-// m and l per wave and head [NW][16] each, the split-K flag
-template <int D>
-struct AfterLoop {
-    static constexpr int Q_OFF = 0, SC_OFF = 16 * D * 4, ML_OFF = SC_OFF + 16 * PAGE * 4;
-};
-
-// Split-K partials cross XCDs (separate L2s): stored write-through and read past the local L2, as
-// relaxed device-scope atomics (global_store / global_load with sc1).
-__device__ __forceinline__ void publish(float* p, float x) {
-    __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float fetch(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// grid (S, Hkv, n_splits * ceil(G / 16)), block NW * 64. Registers are budgeted for two waves per SIMD
-// (amdgpu_waves_per_eu(2); the library is built with MFMA accumulators in VGPRs): with a 512-register
-// budget the 4-wave variant used 236 VGPRs + 76 AGPRs and spent 46 v_accvgpr moves per page in its
-// loop; at <= 256 it needs none, and two 4-wave workgroups fit on one CU. ST = 2 (G <= 8): two page streams share the
-// MFMA columns (page A of each pair in columns 0-7, page B in 8-15); ST = 1: one page's 16 heads.
-// NS > 1: each workgroup writes its split's partials; with `sync` (one zeroed int32 per
-// (sequence, kv head, head chunk)), the last workgroup of a (sequence, kv head, head chunk) to
-// finish merges all splits into `out` and resets its counter, so no second launch is needed.
-template <int D, int BITS, typename IN, int NW, int ST>
-__global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) void decode_kernel(
-    const IN* __restrict__ qg, IN* __restrict__ out, const uint8_t* __restrict__ cache, int64_t bs, int64_t hs,
-    const IN* __restrict__ tail_k, const int32_t* __restrict__ tail_idx, const int32_t* __restrict__ block_table,
-    const int32_t* __restrict__ seq_lens, int64_t bt_stride, int bt_cols, int H, int G, float p2, float rs, int NS,
-    float* __restrict__ part_ml, float* __restrict__ part_o, int32_t* __restrict__ sync,
-    const int32_t* __restrict__ seq_order) {
-    using F = Fmt<D, BITS>;
-    using R = Ring<D, BITS>;
-    constexpr int KSTEPS = D / 32;
-    constexpr int DT = D / 16;
-    constexpr int NLO = BITS == 4 ? D / 32 : D / 16;          // O tiles in units of 2^-24 (the rest 2^-20)
-    constexpr float TWO24 = 16777216.0f, TWO20 = 1048576.0f;
-    constexpr bool QLO = std::is_same<IN, float>::value;      // q needs a low fp16 part
-    constexpr bool DYN = NW == 8;                             // pairs from the LDS counter
-    const float sm_log2 = p2 * rs;                            // exact: p2 is a power of two
-    static_assert(NW == 2 || NW == 4 || NW == 8, "the tail splits 16 heads over 2 NW lane halves");
-    static_assert(ST == 1 || ST == 2, "one or two page streams");
-    using AL = AfterLoop<D>;
-    static_assert(2 * NW * R::SLOT >= AL::ML_OFF + 2 * NW * 16 * 4 + 16, "the after-loop scratch must fit");
-    static_assert(2 * R::DMA <= 63, "vmcnt holds at most 63 loads");
-
-    // one array per page pair (wave w at 2 w R::SLOT): the compiler tells the pairs apart and leaves
-    // the DMA waits to the explicit vmcnt below (it need not tell the two pages of a pair apart: a
-    // pair is only read once both have landed)
-    __shared__ __align__(16) uint8_t ringA[2 * NW * R::SLOT];
-    __shared__ __align__(16) uint8_t ringB[2 * NW * R::SLOT];
-    __shared__ __align__(16) int tbl[WIN];                               // block ids of the window
-    __shared__ uint32_t pair_ctr;                                        // next pair of the window
-    float* const m_l = reinterpret_cast<float*>(ringB + AL::ML_OFF);      // after the loop only
-    float* const l_l = m_l + NW * 16;
-    int* const last_flag = reinterpret_cast<int*>(l_l + NW * 16);
-
-    const int lane = threadIdx.x & (WAVE - 1);
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);   // wave-uniform: scalar page loop
-    const int r16 = lane & 15, q = lane >> 4;
-    // with seq_order, workgroups go out sequence by sequence (all kv heads of one, then the next) in
-    // the given order: the hardware starts workgroups in linear order
-    int s = blockIdx.x, h = blockIdx.y;
-    if (seq_order != nullptr) {
-        const int L = blockIdx.x + gridDim.x * blockIdx.y;
-        s = seq_order[L / H];
-        h = L % H;
-    }
-    const int z = blockIdx.z % NS, gc = blockIdx.z / NS, g0 = gc * 16;
-    const int Gc = min(16, G - g0);
-
-    const int32_t* bt = block_table + (int64_t)s * bt_stride;
-    const int64_t qbase = ((int64_t)s * H + h) * G * D + (int64_t)g0 * D;
-    // Issued before the length is read, which neither depends on: this lane's q head (B column r16)
-    // over its contraction dims (8 consecutive dims per K-step; lanes of heads past the chunk read
-    // the chunk's last head and zero it later) and, for split 0 (whose pages start at 0), the first
-    // window's block ids up to the table's column count bt_cols (entries past the length are never
-    // used). The length then arrives with them instead of before them.
-    const int hq = ST == 2 ? (r16 & 7) : r16;                            // the head of this lane's column
-    const bool gv = hq < Gc;
-    float qv[KSTEPS][8];
-#pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) load8(qg + qbase + (int64_t)min(hq, Gc - 1) * D + kdim<D, BITS>(kk, q, 0), qv[kk]);
-    constexpr int PRE = WIN / (NW * WAVE);                               // prefetched ids per thread
-    const int npre = z == 0 ? min(WIN, bt_cols) : 0;
-    int pre[PRE];
-#pragma unroll
-    for (int k = 0; k < PRE; ++k) {
-        const int i = (int)threadIdx.x + k * NW * WAVE;
-        pre[k] = i < npre ? bt[i] : 0;
-    }
-
-    const int n = seq_lens[s];
-    const int full = n / PAGE, tail_n = n % PAGE;
-    const int pps = (full + NS - 1) / NS;
-    const int p0 = min(full, z * pps), p1 = min(full, p0 + pps);
-    const uint8_t* head_base = cache + (int64_t)h * hs;
-    const bool has_tail = tail_n > 0 && z == NS - 1;
-    uint8_t* const sl0 = ringA + 2 * w * R::SLOT;
-    uint8_t* const sl1 = sl0 + R::SLOT;
-    uint8_t* const sl2 = ringB + 2 * w * R::SLOT;
-    uint8_t* const sl3 = sl2 + R::SLOT;
-
-    // per-lane DMA source offsets (swizzled code rows), fixed for every page
-    uint32_t voff[R::DMA];
-#pragma unroll
-    for (int i = 0; i < R::DMA; ++i) voff[i] = src_chunk<D, BITS>(R::chunk0(i) + lane) * 16u;
-
-    f4 o[DT], vacc = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    float m_run = -__builtin_inff(), l_run = 0.0f, vb_run = 0.0f;
-
-    // The split's pages go out in pairs (k: pages 2k, 2k + 1 of the window), over windows of WIN pages
-    // whose block ids are first copied to an LDS table. With 8 waves (two per SIMD, which the hardware
-    // does not run at the same rate) the pairs come from a counter in LDS: the waves run more often
-    // simply take more pairs and all finish together, at the price of bitwise reproducibility (which
-    // wave accumulates which page varies from run to run; results agree to rounding). With 2 or 4
-    // waves, wave w takes pairs w, w + NW, ... (deterministic). A wave holds two pairs,
-    // in slots (0, 1) and (2, 3): one is consumed while the other is in flight. A wave's pairs only
-    // grow, so once the pair it would consume is past the window's end, so is the one in flight. Each
-    // pair issue is 2 R::DMA instructions, also for a pair past the end (an empty buffer range: no
-    // memory access), so vmcnt counts stay exact.
-    if (p1 > p0) {
-        int wb = p0, wn = min(WIN, p1 - p0), pairs = (wn + 1) / 2;
-        const auto load_window = [&]() {
-            if (wb == 0 && wn <= npre) {                                 // split 0's first window, prefetched
-#pragma unroll
-                for (int k = 0; k < PRE; ++k) {
-                    const int i = (int)threadIdx.x + k * NW * WAVE;
-                    if (i < wn) tbl[i] = pre[k];
-                }
-            } else {
-                for (int i = threadIdx.x; i < wn; i += NW * WAVE) tbl[i] = bt[wb + i];
-            }
-            if (threadIdx.x == 0) pair_ctr = 2 * NW;
-        };
-#define KUSH_ISSUE_PAIR(SA, SB, P)                                                                 \
-    {                                                                                              \
-        const int2 id2 = *reinterpret_cast<const int2*>(tbl + min(2 * (P), WIN - 2));              \
-        issue_page<D, BITS>(SA, (P) < pairs, __builtin_amdgcn_readfirstlane(id2.x), head_base, bs, voff);  \
-        issue_page<D, BITS>(SB, 2 * (P) + 1 < wn, __builtin_amdgcn_readfirstlane(id2.y), head_base, bs, voff); \
-    }
-        // q (loaded above) is converted and the window's ids stored before the barrier: no vector
-        // memory load of the compiler's is outstanding once the page DMAs start
-        load_window();
-        // q' = q p2 as fp16 (+ its low part for fp32 q): qh, ql for the bias MFMAs; qa, qla the Q'
-        // sources, divided by 16 in the int4 K-steps of high nibbles
-        h8 qh[KSTEPS], ql[KSTEPS], qa[KSTEPS], qla[KSTEPS];
-#pragma unroll
-        for (int kk = 0; kk < KSTEPS; ++kk)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float xq = gv ? qv[kk][j] * p2 : 0.0f;
-                const _Float16 hi = (_Float16)xq;
-                const _Float16 lo = QLO ? (_Float16)(xq - (float)hi) : (_Float16)0.0f;
-                const bool hin = BITS == 4 && (kk & 1);
-                qh[kk][j] = hi;
-                ql[kk][j] = lo;
-                qa[kk][j] = hin ? (_Float16)((float)hi * 0.0625f) : hi;
-                qla[kk][j] = hin ? (_Float16)((float)lo * 0.0625f) : lo;
-            }
-        const float sa = rs * TWO24;                             // x = sa s + kx
-        int pa = w, pb = NW + w;                                         // the pairs in slots (0, 1), (2, 3)
-        __syncthreads();
-        KUSH_ISSUE_PAIR(sl0, sl1, pa)
-        KUSH_ISSUE_PAIR(sl2, sl3, pb)
-
-        // One pair step: the pair has landed once at most the other pair's loads are outstanding;
-        // the next pair is taken from the counter (its result and the table read hide behind the
-        // scores), then scores of both pages, one softmax update, PV of both; then, every read of the
-        // two slots complete (lgkmcnt 0), they take the next pair. The second page of a window's odd
-        // last pair is masked.
-#define KUSH_STEP(SA, SB, P)                                                                       \
-    {                                                                                              \
-        if ((P) >= pairs) break;                                                                   \
-        KUSH_WAIT_VM(2 * R::DMA);                                                                  \
-        int nx = (P) + 2 * NW;                           /* static: this wave's pair after next */  \
-        if (DYN && lane == 0) nx = (int)__builtin_amdgcn_atomic_inc32(&pair_ctr, ~0u, __ATOMIC_RELAXED, "workgroup"); \
-        int2 id2;                                                                                  \
-        if constexpr (ST == 2) {                                                                   \
-            float sv[8], kx;                                                                       \
-            pair_scores2<D, BITS, QLO>(SA, qa, qla, qh, ql, sv, kx, rs, lane);                     \
-            if (2 * (P) + 1 >= wn && r16 >= 8) {                                                   \
-                _Pragma("unroll") for (int jj = 0; jj < 8; ++jj) sv[jj] = -__builtin_inff();       \
-            }                                                                                      \
-            nx = __builtin_amdgcn_readfirstlane(nx);                                               \
-            id2 = *reinterpret_cast<const int2*>(tbl + min(2 * nx, WIN - 2));                      \
-            consume2<D, BITS>(SA, R::SLOT, o, vacc, sv, sa, kx, m_run, l_run, vb_run, lane);       \
-        } else {                                                                                   \
-            const uint8_t* const sp[2] = {SA, SB};                                                 \
-            float sv[2][8], kx[2];                                                                 \
-            pair_scores<D, BITS, QLO>(SA, qa, qla, qh, ql, sv, kx, rs, lane);                      \
-            if (2 * (P) + 1 >= wn) {                                                               \
-                _Pragma("unroll") for (int jj = 0; jj < 8; ++jj) sv[1][jj] = -__builtin_inff();    \
-            }                                                                                      \
-            nx = __builtin_amdgcn_readfirstlane(nx);                                               \
-            id2 = *reinterpret_cast<const int2*>(tbl + min(2 * nx, WIN - 2));                      \
-            consume_pages<D, BITS, 2>(sp, o, vacc, sv, sa, kx, m_run, l_run, vb_run, lane);        \
-        }                                                                                          \
-        __builtin_amdgcn_s_waitcnt(0xC07F);                    /* lgkmcnt(0): slot reads done */    \
-        issue_page<D, BITS>(SA, nx < pairs, __builtin_amdgcn_readfirstlane(id2.x), head_base, bs, voff);  \
-        issue_page<D, BITS>(SB, 2 * nx + 1 < wn, __builtin_amdgcn_readfirstlane(id2.y), head_base, bs, voff); \
-        (P) = nx;                                                                                  \
-    }
-        for (;;) {
-            for (;;) {
-                KUSH_STEP(sl0, sl1, pa)
-                KUSH_STEP(sl2, sl3, pb)
-            }
-            KUSH_WAIT_VM(0);                                     // drain the trailing (empty) issues
-            __syncthreads();                                     // table, counter and rings idle
-            wb += WIN;
-            if (wb >= p1) break;
-            wn = min(WIN, p1 - wb);
-            pairs = (wn + 1) / 2;
-            pa = w;
-            pb = NW + w;
-            load_window();
-            __syncthreads();
-            KUSH_ISSUE_PAIR(sl0, sl1, pa)
-            KUSH_ISSUE_PAIR(sl2, sl3, pb)
-        }
-#undef KUSH_STEP
-#undef KUSH_ISSUE_PAIR
-    }
-
-    // partial last page (last split only): V rows from its record, staged by one wave in its slot 0;
-    // exact fp32 K . q scores from the tail, spread over all waves (lane: token lane % 32, heads
-    // 2 w + lane / 32 + 2 NW i), with q (fp32, times sm log2 e) and the scores in the rings
-    if (has_tail) {
-        float* const qs = reinterpret_cast<float*>(ringB + AL::Q_OFF);    // [16][D] q sm log2e
-        float* const sc = reinterpret_cast<float*>(ringB + AL::SC_OFF);   // [16][PAGE] tail scores
-        const int ow = (p1 - p0) % NW;
-        uint8_t* const tslot = ringA + 2 * ow * R::SLOT;
-        if (w == ow) issue_page<D, BITS>(tslot, true, bt[full], head_base, bs, voff);
-        for (int i = threadIdx.x; i < 16 * D; i += NW * WAVE)
-            qs[i] = i < Gc * D ? to_f32(qg[qbase + i]) * sm_log2 : 0.0f;
-        __syncthreads();
-        constexpr int HPL = 16 / (2 * NW);                       // heads per lane
-        const int t = lane & 31, hg = 2 * w + (lane >> 5);
-        const IN* tk = tail_k + (((int64_t)tail_idx[s] * H + h) * PAGE + min(t, tail_n - 1)) * D;
-        float acc[HPL];
-#pragma unroll
-        for (int i = 0; i < HPL; ++i) acc[i] = 0.0f;
-#pragma unroll 4
-        for (int d = 0; d < D; d += 8) {
-            float kx[8];
-            load8(tk + d, kx);
-#pragma unroll
-            for (int i = 0; i < HPL; ++i) {
-                const float4 qa = *reinterpret_cast<const float4*>(&qs[(hg + 2 * NW * i) * D + d]);
-                const float4 qb = *reinterpret_cast<const float4*>(&qs[(hg + 2 * NW * i) * D + d + 4]);
-                acc[i] += qa.x * kx[0] + qa.y * kx[1] + qa.z * kx[2] + qa.w * kx[3] +
-                          qb.x * kx[4] + qb.y * kx[5] + qb.z * kx[6] + qb.w * kx[7];
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < HPL; ++i) sc[(hg + 2 * NW * i) * PAGE + t] = t < tail_n ? acc[i] : -__builtin_inff();
-        __syncthreads();
-        if (w == ow) {
-            float x[1][8];
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj)
-                x[0][jj] = ST == 2 && r16 >= 8 ? -__builtin_inff() : sc[r16 * PAGE + tok(q, jj)];
-            KUSH_WAIT_VM(0);
-            if constexpr (ST == 2) {                             // stream 0 takes the page
-                consume2<D, BITS>(tslot, 0, o, vacc, x[0], 1.0f, 0.0f, m_run, l_run, vb_run, lane);
-            } else {
-                const uint8_t* const sp[1] = {tslot};
-                const float b0[1] = {0.0f};
-                consume_pages<D, BITS, 1>(sp, o, vacc, x, 1.0f, b0, m_run, l_run, vb_run, lane);
-            }
-        }
-    }
-
-    // Merge the waves (and, ST = 2, the two streams of a head: columns c and c ^ 8). Every wave
-    // rescales its O to the workgroup max of its head, adds a head's two stream columns (one DPP
-    // move; columns 0-7 then hold the sums) and stores it in the idle rings (region of wave ww: 16 D
-    // floats, dims d as [d / 4][column][d % 4], one 16-byte store per lane and tile); after one
-    // barrier, wave w sums tiles w, w + NW, ... over the waves and writes them out.
-    constexpr int OBYTES = 16 * D * 4;
-    static_assert(NW * OBYTES <= 2 * NW * R::SLOT, "the merge needs 16 D floats per wave in the first array");
-    l_run = rows_sum(l_run);
-    vb_run = __builtin_fmaf(vacc[0], TWO24, rows_sum(vb_run));   // every row of vacc holds the head's sum
-    if (q == 0) {
-        m_l[w * 16 + r16] = m_run;
-        l_l[w * 16 + r16] = l_run;
-    }
-    __syncthreads();                                             // rings idle, m_l / l_l complete
-    const int rx = ST == 2 ? (r16 ^ 8) : r16;                    // the other stream's column of this head
-    float M = -__builtin_inff();
-#pragma unroll
-    for (int ww = 0; ww < NW; ++ww) M = __builtin_fmaxf(M, __builtin_fmaxf(m_l[ww * 16 + r16], m_l[ww * 16 + rx]));
-    {
-        const float f = m_run == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m_run - M);
-        uint8_t* reg = ringA + w * OBYTES;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            f4 v;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                v[i] = __builtin_fmaf(o[dt][i], dt < NLO ? TWO24 : TWO20, vb_run) * f;
-                if constexpr (ST == 2) v[i] += lane_xor<8>(v[i]);   // the head's two streams (column c ^ 8)
-            }
-            if (ST == 1 || r16 < 8) *reinterpret_cast<f4*>(reg + (((4 * dt + q) * 16 + r16) * 4) * 4) = v;
-        }
-    }
-    // softmax denominator of head r16: every wave's (and stream's) l at the workgroup max. A column
-    // that saw no token holds m = -inf and l = 0, and exp2(-inf) = 0, so no term needs a branch and
-    // all the LDS reads go out together (the sum keeps its order)
-    float L = 0.0f;
-    if (M > -__builtin_inff()) {
-        float mv[NW][ST], lv[NW][ST];
-#pragma unroll
-        for (int ww = 0; ww < NW; ++ww)
-#pragma unroll
-            for (int c2 = 0; c2 < ST; ++c2) {
-                mv[ww][c2] = m_l[ww * 16 + (c2 ? rx : r16)];
-                lv[ww][c2] = l_l[ww * 16 + (c2 ? rx : r16)];
-            }
-#pragma unroll
-        for (int ww = 0; ww < NW; ++ww)
-#pragma unroll
-            for (int c2 = 0; c2 < ST; ++c2) L += lv[ww][c2] * __builtin_amdgcn_exp2f(mv[ww][c2] - M);
-    }
-    __syncthreads();
-    const float inv_l = L > 0.0f ? 1.0f / L : 0.0f;
-    const int64_t pb = (((int64_t)s * H + h) * NS + z) * G + g0 + r16;   // partials row of head r16
-    const bool out_vec = (((uintptr_t)out) & 15) == 0;
-    const int hcol = ST == 2 ? (r16 & 7) : r16;                  // the column holding head r16's sum
-    for (int dt = w; dt < DT; dt += NW) {
-        f4 part[NW];                                             // every wave's piece, read together
-#pragma unroll
-        for (int ww = 0; ww < NW; ++ww)
-            part[ww] = *reinterpret_cast<const f4*>(ringA + ww * OBYTES + (((4 * dt + q) * 16 + hcol) * 4) * 4);
-        f4 acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int ww = 0; ww < NW; ++ww) acc += part[ww];
-        if (r16 < Gc) {
-            const int d0 = 16 * dt + 4 * q;
-            if (NS == 1) {
-                IN* dst = out + qbase + r16 * D + d0;
-                if (out_vec) {                                   // one 8- or 16-byte store
-                    IN v4[4];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) v4[i] = from_f32<IN>(acc[i] * inv_l);
-                    if constexpr (sizeof(IN) == 2) {
-                        *reinterpret_cast<u2*>(dst) = __builtin_bit_cast(u2, v4);
-                    } else {
-                        *reinterpret_cast<f4*>(dst) = __builtin_bit_cast(f4, v4);
-                    }
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) dst[i] = from_f32<IN>(acc[i] * inv_l);
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) publish(part_o + pb * D + d0 + i, acc[i]);
-            }
-        }
-    }
-    if (NS > 1 && w == 0 && q == 0 && r16 < Gc) {
-        publish(part_ml + 2 * pb, M);
-        publish(part_ml + 2 * pb + 1, L);
-    }
-    if (NS == 1 || sync == nullptr) return;
-
-    // split-K: the last workgroup of this (sequence, kv head, head chunk) merges every split. The
-    // partials went out as write-through stores (publish); once every wave has seen them complete
-    // (vmcnt 0, then the barrier), thread 0 counts the split in at the device's coherence point, and
-    // the last workgroup reads the other splits' partials past its own XCD's L2 (fetch). No L2-wide
-    // write-back or invalidate, which would stall every other workgroup streaming on the XCD.
-    KUSH_WAIT_VM(0);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int n_gc = gridDim.z / NS;
-        int32_t* ctr = sync + ((int64_t)s * H + h) * n_gc + gc;
-        const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *last_flag = prev == NS - 1;
-        if (prev == NS - 1) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (!*last_flag) return;
-    const int64_t base = ((int64_t)s * H + h) * NS;
-    for (int i = threadIdx.x; i < Gc * D; i += NW * WAVE) {
-        const int g = g0 + i / D, d = i % D;
-        float Mg = -__builtin_inff();
-        for (int zz = 0; zz < NS; ++zz) Mg = __builtin_fmaxf(Mg, fetch(part_ml + 2 * ((base + zz) * G + g)));
-        float L = 0.0f, acc = 0.0f;
-        if (Mg > -__builtin_inff()) {
-            for (int zz = 0; zz < NS; ++zz) {
-                const int64_t pb = (base + zz) * G + g;
-                const float mz = fetch(part_ml + 2 * pb);
-                if (mz > -__builtin_inff()) {
-                    const float fz = __builtin_amdgcn_exp2f(mz - Mg);
-                    L += fetch(part_ml + 2 * pb + 1) * fz;
-                    acc += fz * fetch(part_o + pb * D + d);
-                }
-            }
-        }
-        out[qbase + i] = from_f32<IN>(L > 0.0f ? acc / L : 0.0f);
-    }
-}
-
-// grid (S, Hkv), block 256: merge split-K partials (M, L, unnormalized O) into the output.
-// M is in log2 units. Splits with no tokens (M = -inf) are skipped (gpu.mojo:469-491).
-template <typename IN>
-__global__ __launch_bounds__(256) void combine_kernel(IN* __restrict__ out, const float* __restrict__ part_ml,
-                                                      const float* __restrict__ part_o, int NS, int H, int G, int D) {
-    const int s = blockIdx.x, h = blockIdx.y;
-    const int64_t base = ((int64_t)s * H + h) * NS;
-    for (int i = threadIdx.x; i < G * D; i += 256) {
-        const int g = i / D, d = i % D;
-        float M = -__builtin_inff();
-        for (int z = 0; z < NS; ++z) M = __builtin_fmaxf(M, part_ml[2 * ((base + z) * G + g)]);
-        float L = 0.0f, o = 0.0f;
-        if (M > -__builtin_inff()) {
-            for (int z = 0; z < NS; ++z) {
-                const int64_t pb = (base + z) * G + g;
-                const float mz = part_ml[2 * pb];
-                if (mz > -__builtin_inff()) {
-                    const float fz = __builtin_amdgcn_exp2f(mz - M);
-                    L += part_ml[2 * pb + 1] * fz;
-                    o += fz * part_o[pb * D + d];
-                }
-            }
-        }
-        out[((int64_t)s * H + h) * G * D + i] = from_f32<IN>(L > 0.0f ? o / L : 0.0f);
-    }
-}
-
-template <int D, int BITS, typename IN, int NW>
-static int launch_decode(dim3 grid, hipStream_t stream, const void* q, void* out, const void* cache, int64_t bs,
-                         int64_t hs, const void* tail_k, const int32_t* tail_idx, const int32_t* block_table,
-                         const int32_t* seq_lens, int64_t bt_stride, int bt_cols, int hkv, int group, float p2, float rs, int n_splits,
-                         float* part_ml, float* part_o, int32_t* sync, const int32_t* seq_order) {
-    // two page streams whenever the heads of a kv head fit in half the MFMA columns
-    auto kern = group <= 8 ? decode_kernel<D, BITS, IN, NW, 2> : decode_kernel<D, BITS, IN, NW, 1>;
-    kern<<<grid, dim3(NW * WAVE), 0, stream>>>(
-        (const IN*)q, (IN*)out, (const uint8_t*)cache, bs, hs, (const IN*)tail_k, tail_idx, block_table, seq_lens,
-        bt_stride, bt_cols, hkv, group, p2, rs, n_splits, part_ml, part_o, sync, seq_order);
-    return kush_check_launch("kush_decode");
-}
-
-}  // namespace kush
+// C entry points of the fused dequant decode attention (kush_decode) and the split-K combine
+// (kush_combine); the kernels and their launch are in kush_decode.h (contract and design notes there).
+#include "kush_decode.h"
 
 using namespace kush;
 
@@ -985,10 +8,10 @@ extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const v
                            int64_t block_stride, int64_t head_stride, const void* tail_k, const int32_t* tail_idx,
                            const int32_t* block_table, const int32_t* seq_lens, int64_t bt_stride, int32_t bt_cols,
                            int32_t hkv, float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t* split_sync,
-                           int32_t waves, const int32_t* seq_order, int32_t n_seqs, void* stream) {
-    if (n_seqs < 0 || hkv <= 0 || group <= 0 || n_splits <= 0 || bt_cols < 0)
-        return kush_fail(-2, "kush_decode: bad n_seqs %d / hkv %d / group %d / n_splits %d / bt_cols %d", n_seqs, hkv,
-                         group, n_splits, bt_cols);
+                           int32_t waves, const int32_t* seq_order, int32_t n_seqs, int32_t rot, void* stream) {
+    if (n_seqs < 0 || hkv <= 0 || group <= 0 || n_splits <= 0 || bt_cols < 0 || rot < 0 || rot > 1)
+        return kush_fail(-2, "kush_decode: bad n_seqs %d / hkv %d / group %d / n_splits %d / bt_cols %d / rot %d", n_seqs,
+                         hkv, group, n_splits, bt_cols, rot);
     if (n_splits > 1 && (part_ml == nullptr || part_o == nullptr))
         return kush_fail(-2, "kush_decode: n_splits %d needs the partial buffers", n_splits);
     if (((uintptr_t)cache | (uint64_t)block_stride | (uint64_t)head_stride) & 15)
@@ -1020,32 +43,34 @@ extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const v
 #define KUSH_DECODE_ARGS grid, st, q, out, cache, block_stride, head_stride, tail_k, tail_idx, block_table, seq_lens, \
                          bt_stride, bt_cols, hkv, group, p2, rs, n_splits, part_ml, part_o, split_sync, seq_order
         // the largest of the requested, 4 and 2 waves whose rings fit in LDS
+        const auto launch = [&](auto nw) -> int {
+            constexpr int NW = decltype(nw)::value;
+            return rot ? launch_decode<D, BITS, IN, NW, true>(KUSH_DECODE_ARGS)
+                       : launch_decode<D, BITS, IN, NW, false>(KUSH_DECODE_ARGS);
+        };
         if (waves >= 8) {
-            if constexpr (decode_fits<D, BITS, 8>()) return launch_decode<D, BITS, IN, 8>(KUSH_DECODE_ARGS);
+            if constexpr (decode_fits<D, BITS, 8>()) return launch(std::integral_constant<int, 8>{});
         }
         if (waves >= 4) {
-            if constexpr (decode_fits<D, BITS, 4>()) return launch_decode<D, BITS, IN, 4>(KUSH_DECODE_ARGS);
+            if constexpr (decode_fits<D, BITS, 4>()) return launch(std::integral_constant<int, 4>{});
         }
         static_assert(decode_fits<D, BITS, 2>(), "two waves' rings must fit in LDS");
-        return launch_decode<D, BITS, IN, 2>(KUSH_DECODE_ARGS);
+        return launch(std::integral_constant<int, 2>{});
 #undef KUSH_DECODE_ARGS
     });
 }
 
 extern "C" int kush_combine(int head_dim, int group, int dtype, void* out, const float* part_ml, const float* part_o,
-                            int32_t n_splits, int32_t hkv, int32_t n_seqs, void* stream) {
-    if (n_seqs < 0 || hkv <= 0 || group <= 0 || n_splits <= 0)
+                            int32_t n_splits, int32_t hkv, int32_t n_seqs, int32_t rot, void* stream) {
+    if (n_seqs < 0 || hkv <= 0 || group <= 0 || n_splits <= 0 || rot < 0 || rot > 1)
         return kush_fail(-2, "kush_combine: bad arguments");
-    if (head_dim != 64 && head_dim != 128 && head_dim != 256)
-        return kush_fail(-1, "kush_combine: unsupported head_dim %d", head_dim);
-    if (n_seqs == 0) return 0;
-    const dim3 grid(n_seqs, hkv);
-    hipStream_t st = (hipStream_t)stream;
-    switch (dtype) {
-        case 0: combine_kernel<float><<<grid, 256, 0, st>>>((float*)out, part_ml, part_o, n_splits, hkv, group, head_dim); break;
-        case 1: combine_kernel<_Float16><<<grid, 256, 0, st>>>((_Float16*)out, part_ml, part_o, n_splits, hkv, group, head_dim); break;
-        case 2: combine_kernel<bf16_t><<<grid, 256, 0, st>>>((bf16_t*)out, part_ml, part_o, n_splits, hkv, group, head_dim); break;
-        default: return kush_fail(-1, "kush_combine: unsupported dtype code %d", dtype);
-    }
-    return kush_check_launch("kush_combine");
+    // bits does not matter here: any record format's partials
+    return dispatch_shape(head_dim, 4, dtype, "kush_combine", [&](auto dd, auto, auto in) -> int {
+        constexpr int D = decltype(dd)::value;
+        using IN = decltype(in);
+        if (n_seqs == 0) return 0;
+        auto kern = rot ? combine_kernel<D, IN, true> : combine_kernel<D, IN, false>;
+        kern<<<dim3(n_seqs, hkv), dim3(256), 0, (hipStream_t)stream>>>((IN*)out, part_ml, part_o, n_splits, hkv, group);
+        return kush_check_launch("kush_combine");
+    });
 }

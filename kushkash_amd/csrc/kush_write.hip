@@ -13,7 +13,13 @@
 // range is reduced over the CG lanes of its row (xor shuffles); a K channel's range over the 32
 // rows goes through a tile of the K rows in LDS, kept in the input dtype (exact), one channel
 // per thread.
-#include "kush_common.h"
+//
+// Rotated caches (rot): the rows a cache quantizes or stashes may be rotated by the canonical
+// Walsh-Hadamard transform first, in registers: a thread's 16 dims of a row are exactly the
+// butterfly layout of fwht_runs (D / 16 consecutive lanes per row, dims 8c.. and D/2 + 8c..), and the
+// rotated values are rounded to the input dtype, so a rotated write stores the bytes that Ops.fwht
+// on the rows followed by an unrotated write would. Rows that come from a K tail are rotated already.
+#include "kush_fwht.h"
 
 namespace kush {
 
@@ -63,6 +69,13 @@ struct Row16 {
 #pragma unroll
         for (int j = 0; j < 16; ++j) x[j] = to_f32(v[j]);
     }
+    // the 16 values back as IN (values already representable in IN: rotate16's output)
+    __device__ __forceinline__ void set(const float (&x)[16]) {
+        IN v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = from_f32<IN>(x[j]);
+        __builtin_memcpy(w, v, sizeof(w));
+    }
     // both runs into the tile row (16-byte aligned)
     __device__ __forceinline__ void store(IN* row, int lo, int hi) const {
 #pragma unroll
@@ -72,6 +85,23 @@ struct Row16 {
         }
     }
 };
+
+// This lane's 16 values of a row (lane c of the row's D / 16 lanes) rotated by the canonical
+// Walsh-Hadamard transform and rounded to IN, as Ops.fwht writes the row
+template <int D, typename IN>
+__device__ __forceinline__ void rotate16(float (&x)[16], int c) {
+    fwht_runs<D>(x, c);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) x[j] = to_f32(store_rounded<IN>(x[j]));
+}
+
+template <int D, typename IN, bool VEC>
+__device__ __forceinline__ void rotate_row(Row16<IN, VEC>& row, int c) {
+    float x[16];
+    row.floats(x);
+    rotate16<D, IN>(x, c);
+    row.set(x);
+}
 
 // codes of the 16 values of a thread (x[0..8): dims 8c.., x[8..16): dims D/2 + 8c..) -> the bytes
 // they make: int4 byte i = code(x[i]) & 15 | (code(x[8 + i]) & 15) << 4 (row bytes 8c + i, in lo);
@@ -128,7 +158,7 @@ __device__ __forceinline__ void row_range(float& mn, float& mx) {
 // from v_new + (t - vlo) * v_stride) and, when do_k, the K page: rows t < split from k_tail
 // (stride D), the others from k_new + (t - split) * k_stride. rec: the page's record. lds:
 // tile_bytes<D, IN>() bytes. Every thread of the workgroup calls this (it has barriers when do_k).
-template <int D, int BITS, typename IN, bool VEC, int THREADS>
+template <int D, int BITS, typename IN, bool VEC, int THREADS, bool ROT>
 __device__ __forceinline__ void page_task(const IN* __restrict__ k_tail, const IN* __restrict__ k_new, int64_t k_stride,
                                           int split, bool do_k, const IN* __restrict__ v_new, int64_t v_stride,
                                           int vlo, int vhi, uint8_t* __restrict__ rec, uint8_t* lds) {
@@ -149,6 +179,7 @@ __device__ __forceinline__ void page_task(const IN* __restrict__ k_tail, const I
             vr.load(v_new + (int64_t)(r - vlo) * v_stride, 8 * c, D / 2 + 8 * c);
             float x[16];
             vr.floats(x);
+            if constexpr (ROT) rotate16<D, IN>(x, c);
             float mn = x[0], mx = x[0];
 #pragma unroll
             for (int j = 1; j < 16; ++j) {
@@ -188,6 +219,9 @@ __device__ __forceinline__ void page_task(const IN* __restrict__ k_tail, const I
         const int r = r0 + pp * RW::RP;
         if (r >= PAGE) continue;
         kr[pp].load(r < split ? k_tail + r * D : k_new + (int64_t)(r - split) * k_stride, 8 * c, D / 2 + 8 * c);
+        if constexpr (ROT) {
+            if (r >= split) rotate_row<D>(kr[pp], c);                   // a whole row's lanes branch together
+        }
         kr[pp].store(tile + r * D, 8 * c, D / 2 + 8 * c);
     }
     v_rows();
@@ -242,12 +276,29 @@ __device__ __forceinline__ void page_task(const IN* __restrict__ k_tail, const I
     __syncthreads();   // tile is free again
 }
 
-// n rows of D elements from src (row stride src_stride) to dst (row stride D), by THREADS threads
-template <int D, typename IN, bool VEC, int THREADS = WRITE_THREADS>
-__device__ __forceinline__ void copy_rows(IN* __restrict__ dst, const IN* __restrict__ src, int64_t src_stride, int n) {
-    for (int i = threadIdx.x; i < n * (D / 8); i += THREADS) {
-        const int r = i / (D / 8), j = 8 * (i % (D / 8));
-        copy8<VEC>(dst + r * D + j, src + (int64_t)r * src_stride + j);
+// n K rows from src (row stride src_stride) into a tail at dst (row stride D), rotated when ROT, by
+// THREADS threads: without rotation a plain copy, with it D / 16 lanes per row in the butterfly layout
+template <int D, typename IN, bool VEC, bool ROT, int THREADS>
+__device__ __forceinline__ void stash_rows(IN* __restrict__ dst, const IN* __restrict__ src, int64_t src_stride, int n,
+                                           int tid) {
+    if constexpr (!ROT) {
+        for (int i = tid; i < n * (D / 8); i += THREADS) {
+            const int r = i / (D / 8), j = 8 * (i % (D / 8));
+            copy8<VEC>(dst + r * D + j, src + (int64_t)r * src_stride + j);
+        }
+    } else {
+        constexpr int CG = D / 16, RP = THREADS / CG;
+        static_assert(THREADS % CG == 0, "whole rows per pass");
+        const int c = tid % CG;
+        for (int r = tid / CG; r < n; r += RP) {                   // a row's lanes iterate together
+            Row16<IN, VEC> row;
+            row.load(src + (int64_t)r * src_stride, 8 * c, D / 2 + 8 * c);
+            rotate_row<D>(row, c);
+            float x[16];
+            row.floats(x);
+            put8<VEC>(dst + r * D + 8 * c, x);
+            put8<VEC>(dst + r * D + D / 2 + 8 * c, x + 8);
+        }
     }
 }
 
@@ -256,7 +307,7 @@ __device__ __forceinline__ void copy_rows(IN* __restrict__ dst, const IN* __rest
 // tail (quantized when its page fills: rows 0..30 from the tail, row 31 this token, read from k),
 // V straight into its record row. Contract: gpu.mojo:207-238, cpu.mojo:248-270 (seq_lens
 // advances in advance_kernel, launched after this one).
-template <int D, int BITS, typename IN, bool VEC>
+template <int D, int BITS, typename IN, bool VEC, bool ROT>
 __global__ __launch_bounds__(WRITE_THREADS) void append_kernel(
     const IN* __restrict__ k, const IN* __restrict__ v, int64_t k_stride, int64_t v_stride,
     const int32_t* __restrict__ seq_lens, int pos_offset, const int32_t* __restrict__ tail_idx,
@@ -271,8 +322,8 @@ __global__ __launch_bounds__(WRITE_THREADS) void append_kernel(
     IN* tail = tail_k + ((int64_t)tail_idx[s] * H + h) * PAGE * D;
     const IN* krow = k + (int64_t)s * k_stride + (int64_t)h * D;
     uint8_t* rec = cache + blk * bs + (int64_t)h * hs;
-    copy_rows<D, IN, VEC>(tail + slot * D, krow, 0, 1);
-    page_task<D, BITS, IN, VEC, WRITE_THREADS>(tail, krow, 0, PAGE - 1, slot == PAGE - 1,
+    stash_rows<D, IN, VEC, ROT, WRITE_THREADS>(tail + slot * D, krow, 0, 1, threadIdx.x);
+    page_task<D, BITS, IN, VEC, WRITE_THREADS, ROT>(tail, krow, 0, PAGE - 1, slot == PAGE - 1,
                                                v + (int64_t)s * v_stride + (int64_t)h * D, 0, slot, slot + 1, rec, lds);
 }
 
@@ -296,7 +347,7 @@ __global__ __launch_bounds__(256) void advance_kernel(int32_t* seq_lens, int pos
 // page's job writes the tail after its own reads (same workgroup, behind page_task's last barrier);
 // otherwise the partial page's job does. Needs a job for every page the chunk touches.
 // Contract: gpu.mojo:241-276, cpu.mojo:273-304.
-template <int D, int BITS, typename IN, bool VEC, bool FUSE>
+template <int D, int BITS, typename IN, bool VEC, bool FUSE, bool ROT>
 __global__ __launch_bounds__(write_threads<D>()) void write_kernel(
     const IN* __restrict__ k, const IN* __restrict__ v, int64_t k_stride, int64_t v_stride,
     const int32_t* __restrict__ qsl, const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ tail_idx,
@@ -318,7 +369,7 @@ __global__ __launch_bounds__(write_threads<D>()) void write_kernel(
         const int hi = ps + PAGE < total ? ps + PAGE : total;
         int split = ctx - ps;                               // K rows before it come from the tail
         split = split < 0 ? 0 : (split > PAGE ? PAGE : split);
-        page_task<D, BITS, IN, VEC, write_threads<D>()>(tail, k + (int64_t)(q0 + ps + split - ctx) * k_stride + hoff,
+        page_task<D, BITS, IN, VEC, write_threads<D>(), ROT>(tail, k + (int64_t)(q0 + ps + split - ctx) * k_stride + hoff,
                                                         k_stride, split, complete,
                                                         v + (int64_t)(q0 + lo - ctx) * v_stride + hoff, v_stride,
                                                         lo - ps, hi - ps, rec, lds);
@@ -329,15 +380,16 @@ __global__ __launch_bounds__(write_threads<D>()) void write_kernel(
         if (total % PAGE != 0 && ps / PAGE == owner) {
             const int pl = last * PAGE;
             const int lo2 = pl > ctx ? pl : ctx;
-            copy_rows<D, IN, VEC, write_threads<D>()>(tail + (lo2 - pl) * D, k + (int64_t)(q0 + lo2 - ctx) * k_stride + hoff,
-                                                      k_stride, total - lo2);
+            stash_rows<D, IN, VEC, ROT, write_threads<D>()>(tail + (lo2 - pl) * D,
+                                                             k + (int64_t)(q0 + lo2 - ctx) * k_stride + hoff, k_stride,
+                                                             total - lo2, threadIdx.x);
         }
     }
 }
 
 // grid (ceil(n_jobs * Hkv / 4)), block 256: the write's mode 1, one wave per (job, kv head): stash
 // the new K rows of a still-partial page in the tail (a complete page's wave returns at once).
-template <int D, typename IN, bool VEC>
+template <int D, typename IN, bool VEC, bool ROT>
 __global__ __launch_bounds__(256) void tail_kernel(const IN* __restrict__ k, int64_t k_stride,
                                                    const int32_t* __restrict__ qsl, const int32_t* __restrict__ seq_lens,
                                                    const int32_t* __restrict__ tail_idx,
@@ -356,10 +408,7 @@ __global__ __launch_bounds__(256) void tail_kernel(const IN* __restrict__ k, int
     const int lo = ps > ctx ? ps : ctx;
     IN* dst = tail_k + (((int64_t)tail_idx[s] * H + h) * PAGE + (lo - ps)) * D;
     const IN* src = k + (int64_t)(q0 + lo - ctx) * k_stride + (int64_t)h * D;
-    for (int i = lane; i < (total - lo) * (D / 8); i += WAVE) {
-        const int r = i / (D / 8), c = 8 * (i % (D / 8));
-        copy8<VEC>(dst + r * D + c, src + (int64_t)r * k_stride + c);
-    }
+    stash_rows<D, IN, VEC, ROT, WAVE>(dst, src, k_stride, total - lo, lane);
 }
 
 // 16-byte loads and stores when k / v rows (pointer and row stride) and tail_k are 16-byte aligned
@@ -378,15 +427,17 @@ extern "C" int kush_append(int head_dim, int bits, int dtype, const void* k, con
                            int64_t v_stride, int32_t* seq_lens, int32_t pos_offset, int32_t advance,
                            const int32_t* tail_idx, void* cache, int64_t block_stride, int64_t head_stride,
                            void* tail_k, const int32_t* block_table, int64_t bt_stride, int32_t hkv, int32_t n_seqs,
-                           void* stream) {
-    if (n_seqs < 0 || hkv <= 0) return kush_fail(-2, "kush_append: bad n_seqs %d / hkv %d", n_seqs, hkv);
+                           int32_t rot, void* stream) {
+    if (n_seqs < 0 || hkv <= 0 || rot < 0 || rot > 1)
+        return kush_fail(-2, "kush_append: bad n_seqs %d / hkv %d / rot %d", n_seqs, hkv, rot);
     return dispatch_shape(head_dim, bits, dtype, "kush_append", [&](auto dd, auto bb, auto in) -> int {
         constexpr int D = decltype(dd)::value, BITS = decltype(bb)::value;
         using IN = decltype(in);
         if (n_seqs == 0) return 0;
         hipStream_t st = (hipStream_t)stream;
-        auto kern = rows_aligned<IN>(k, v, k_stride, v_stride, tail_k) ? append_kernel<D, BITS, IN, true>
-                                                                         : append_kernel<D, BITS, IN, false>;
+        const bool vec = rows_aligned<IN>(k, v, k_stride, v_stride, tail_k);
+        auto kern = rot ? (vec ? append_kernel<D, BITS, IN, true, true> : append_kernel<D, BITS, IN, false, true>)
+                        : (vec ? append_kernel<D, BITS, IN, true, false> : append_kernel<D, BITS, IN, false, false>);
         kern<<<dim3(n_seqs, hkv), dim3(WRITE_THREADS), 0, st>>>((const IN*)k, (const IN*)v, k_stride, v_stride,
                                                                 seq_lens, pos_offset, tail_idx, (uint8_t*)cache,
                                                                 block_stride, head_stride, (IN*)tail_k, block_table,
@@ -400,9 +451,9 @@ extern "C" int kush_write(int head_dim, int bits, int dtype, const void* k, cons
                           int64_t v_stride, const int32_t* query_start_loc, const int32_t* seq_lens,
                           const int32_t* tail_idx, const int32_t* job_seq, const int32_t* job_page, int32_t n_jobs,
                           int32_t mode, void* cache, int64_t block_stride, int64_t head_stride, void* tail_k,
-                          const int32_t* block_table, int64_t bt_stride, int32_t hkv, void* stream) {
-    if (n_jobs < 0 || hkv <= 0 || mode < 0 || mode > 2)
-        return kush_fail(-2, "kush_write: bad n_jobs %d / hkv %d / mode %d", n_jobs, hkv, mode);
+                          const int32_t* block_table, int64_t bt_stride, int32_t hkv, int32_t rot, void* stream) {
+    if (n_jobs < 0 || hkv <= 0 || mode < 0 || mode > 2 || rot < 0 || rot > 1)
+        return kush_fail(-2, "kush_write: bad n_jobs %d / hkv %d / mode %d / rot %d", n_jobs, hkv, mode, rot);
     return dispatch_shape(head_dim, bits, dtype, "kush_write", [&](auto dd, auto bb, auto in) -> int {
         constexpr int D = decltype(dd)::value, BITS = decltype(bb)::value;
         using IN = decltype(in);
@@ -410,13 +461,19 @@ extern "C" int kush_write(int head_dim, int bits, int dtype, const void* k, cons
         const bool vec = rows_aligned<IN>(k, v, k_stride, v_stride, tail_k);
         hipStream_t st = (hipStream_t)stream;
         if (mode != 1) {
-            auto kern = mode == 2 ? (vec ? write_kernel<D, BITS, IN, true, true> : write_kernel<D, BITS, IN, false, true>)
-                                  : (vec ? write_kernel<D, BITS, IN, true, false> : write_kernel<D, BITS, IN, false, false>);
+            using K = decltype(&write_kernel<D, BITS, IN, true, true, true>);
+            const K table[2][2][2] = {                                  // [vec][fuse][rot]
+                {{write_kernel<D, BITS, IN, false, false, false>, write_kernel<D, BITS, IN, false, false, true>},
+                 {write_kernel<D, BITS, IN, false, true, false>, write_kernel<D, BITS, IN, false, true, true>}},
+                {{write_kernel<D, BITS, IN, true, false, false>, write_kernel<D, BITS, IN, true, false, true>},
+                 {write_kernel<D, BITS, IN, true, true, false>, write_kernel<D, BITS, IN, true, true, true>}}};
+            auto kern = table[vec][mode == 2][rot];
             kern<<<dim3(n_jobs, hkv), dim3(write_threads<D>()), 0, st>>>(
                 (const IN*)k, (const IN*)v, k_stride, v_stride, query_start_loc, seq_lens, tail_idx, job_seq, job_page,
                 (uint8_t*)cache, block_stride, head_stride, (IN*)tail_k, block_table, bt_stride, hkv);
         } else {
-            auto kern = vec ? tail_kernel<D, IN, true> : tail_kernel<D, IN, false>;
+            auto kern = rot ? (vec ? tail_kernel<D, IN, true, true> : tail_kernel<D, IN, false, true>)
+                            : (vec ? tail_kernel<D, IN, true, false> : tail_kernel<D, IN, false, false>);
             kern<<<dim3(((int64_t)n_jobs * hkv + 3) / 4), dim3(256), 0, st>>>(
                 (const IN*)k, k_stride, query_start_loc, seq_lens, tail_idx, job_seq, job_page, n_jobs, (IN*)tail_k, hkv);
         }

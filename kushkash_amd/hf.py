@@ -94,16 +94,19 @@ class KushHFCache(Cache):
         bits: 4 (default) or 8.
         max_length: optional per-sequence capacity hint (pages are mapped on demand otherwise).
         rotate: Hadamard rotation inside the cache (None: KUSHKASH_ROTATE; auto = on for 4-bit).
+        rotate_in_kernels: fold that rotation into the write and decode kernels (KushCache's option of
+            the same name; no reference counterpart).
     The KushCache itself is created by the first update(), on the device and in the dtype of the
     model's K/V (a GPU device: the kernels run on the GPU only).
     """
 
-    def __init__(self, config, bits: int = 4, max_length: int | None = None, rotate: bool | None = None):
+    def __init__(self, config, bits: int = 4, max_length: int | None = None, rotate: bool | None = None,
+                 rotate_in_kernels: bool = False):
         cfg = _text_config(config)
         self.num_layers = cfg.num_hidden_layers
         self.num_q_heads = cfg.num_attention_heads
         self.head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
-        self.bits, self.max_length, self.rotate = bits, max_length, rotate
+        self.bits, self.max_length, self.rotate, self.rotate_in_kernels = bits, max_length, rotate, rotate_in_kernels
         self.kv: KushCache | None = None
         super().__init__(layers=[_KushLayer(self, i) for i in range(self.num_layers)])
 
@@ -114,7 +117,7 @@ class KushHFCache(Cache):
             B, H, _, D = key_states.shape
             self.kv = KushCache(self.num_layers, H, self.num_q_heads, D, batch_size=B, bits=self.bits,
                                 device=key_states.device, dtype=key_states.dtype, max_length=self.max_length,
-                                rotate=self.rotate)
+                                rotate=self.rotate, rotate_in_kernels=self.rotate_in_kernels)
         self.layers[layer_idx].is_initialized = True
         _handoff.cache = self
         return key_states, value_states

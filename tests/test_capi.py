@@ -54,7 +54,7 @@ def test_abi_version(lib):
 def _decode_args(**kw):
     a = dict(head_dim=128, bits=4, group=7, dtype=2, q=None, out=None, cache=None, bs=0, hs=0, tail_k=None,
              tail_idx=None, bt=None, seq_lens=None, bt_stride=0, bt_cols=0, hkv=4, scale=1.0, n_splits=1, part_ml=None,
-             part_o=None, sync=None, waves=0, seq_order=None, n_seqs=1, stream=None)
+             part_o=None, sync=None, waves=0, seq_order=None, n_seqs=1, rot=0, stream=None)
     a.update(kw)
     return list(a.values())
 
@@ -68,6 +68,7 @@ def _decode_args(**kw):
     (dict(n_splits=4), -2, "needs the partial buffers"),
     (dict(bs=8), -2, "16-byte aligned"),
     (dict(waves=3), -2, "waves"),
+    (dict(rot=2), -2, "rot"),
 ])
 def test_decode_rejects_bad_arguments(lib, kw, code, msg):
     assert lib.kush_decode(*_decode_args(**kw)) == code
@@ -82,11 +83,17 @@ def test_error_codes_map_to_reference_exceptions(lib):
 
 
 def test_combine_and_writes_reject_bad_arguments(lib):
-    assert lib.kush_combine(128, 7, 2, None, None, None, 0, 4, 1, None) == -2
-    assert lib.kush_combine(96, 7, 2, None, None, None, 2, 4, 1, None) == -1
-    assert lib.kush_append(96, 4, 2, None, None, 0, 0, None, 0, 0, None, None, 0, 0, None, None, 0, 4, 1, None) == -1
+    assert lib.kush_combine(128, 7, 2, None, None, None, 0, 4, 1, 0, None) == -2
+    assert lib.kush_combine(96, 7, 2, None, None, None, 2, 4, 1, 0, None) == -1
+    assert lib.kush_combine(128, 7, 2, None, None, None, 2, 4, 1, 2, None) == -2           # rot is 0 or 1
+    assert lib.kush_append(96, 4, 2, None, None, 0, 0, None, 0, 0, None, None, 0, 0, None, None, 0, 4, 1, 0,
+                           None) == -1
+    assert lib.kush_append(128, 4, 2, None, None, 0, 0, None, 0, 0, None, None, 0, 0, None, None, 0, 4, 1, 3,
+                           None) == -2
     assert lib.kush_write(128, 5, 2, None, None, 0, 0, None, None, None, None, None, 1, 0, None, 0, 0, None, None,
-                          0, 4, None) == -1
+                          0, 4, 0, None) == -1
+    assert lib.kush_write(128, 4, 2, None, None, 0, 0, None, None, None, None, None, 1, 0, None, 0, 0, None, None,
+                          0, 4, -1, None) == -2
 
 
 def test_ops_is_gpu_only():

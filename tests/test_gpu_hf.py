@@ -191,3 +191,34 @@ def test_generate_eos_async_stop(graph):
     assert torch.equal(out[:, :k + 1], ref[:, :k + 1])
     assert bool((out[0, k + 1:] == eos).all())
     assert out.shape[1] <= k + 2 * EOS_LAG < ref.shape[1]
+
+
+def test_generate_rotate_in_kernels():
+    """An int4 cache whose rotation is folded into the kernels decodes like the same cache rotated by the
+    reference's GEMM (the two rotations differ only in rounding: within 2 % of the largest logit, far
+    inside int4's own error), both stay within 10 % of an fp32 DynamicCache run (int4), and
+    graph-replayed generate gives the eager tokens."""
+    from transformers import DynamicCache
+    model = _llama(512, 128, torch.float16)
+    ref_model = copy.deepcopy(model).float()
+    ids = torch.randint(0, 512, (2, 200), generator=torch.Generator().manual_seed(9)).to(DEV)
+    logits = {}
+    with torch.no_grad():
+        kk.enable(model)
+        for folded in (False, True):
+            cache = kk.KushHFCache(model.config, bits=4, rotate=True, rotate_in_kernels=folded)
+            model(ids, past_key_values=cache, use_cache=True)
+            logits[folded] = model(ids[:, -1:], past_key_values=cache, use_cache=True).logits.float()
+            assert cache.kv.krot == folded
+        rc = DynamicCache(config=ref_model.config)
+        ref_model.set_attn_implementation("sdpa")
+        ref_model(ids, past_key_values=rc, use_cache=True)
+        r1 = ref_model(ids[:, -1:], past_key_values=rc, use_cache=True).logits
+    top = logits[False].abs().max()
+    assert (logits[True] - logits[False]).abs().max() < 0.02 * top
+    for folded in (False, True):
+        assert (logits[folded] - r1).abs().max() < 0.10 * r1.abs().max()
+    mk = lambda: kk.KushHFCache(model.config, bits=4, max_length=260, rotate_in_kernels=True)
+    eager = kk.generate(model, ids, 40, cache=mk(), cuda_graph=False)
+    graphed = kk.generate(model, ids, 40, cache=mk(), cuda_graph=True)
+    assert torch.equal(eager, graphed)

@@ -331,7 +331,7 @@ def test_block_id_prefetch_does_not_change_results(waves, ns):
         _lib.call("kush_decode", D, bits, G, DTYPE_CODE[dtype], q.data_ptr(), out.data_ptr(), cache.data_ptr(), bs, hs,
                   tail_k.data_ptr(), tail_idx.data_ptr(), bt.data_ptr(), seq_lens.data_ptr(), bt.stride(0), bt_cols, H,
                   D ** -0.5, ns, work.data_ptr() if ns > 1 else None, work.data_ptr() + nml * 4 if ns > 1 else None,
-                  ops._sync.data_ptr() if ns > 1 else None, waves, None, S, torch.cuda.current_stream().cuda_stream)
+                  ops._sync.data_ptr() if ns > 1 else None, waves, None, S, 0, torch.cuda.current_stream().cuda_stream)
         torch.cuda.synchronize()
         return out.cpu()
 

@@ -12,20 +12,29 @@ from pathlib import Path
 import pytest
 
 ROOT = Path(__file__).resolve().parent.parent
-SRC = ROOT / "kushkash_amd" / "csrc" / "kush_decode.hip"
+SRC = ROOT / "kushkash_amd" / "csrc" / "kush_decode_inst.hip"
 
 
 @pytest.fixture(scope="module")
 def asm(tmp_path_factory):
+    """The device assembly of every decode instantiation: one compile per (input dtype, rot), as the build."""
     hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(hipcc).exists():
         pytest.skip("hipcc not available")
-    from kushkash_amd.build import FLAGS
-    out = tmp_path_factory.mktemp("isa") / "kush_decode.s"
+    from concurrent.futures import ThreadPoolExecutor
+    from kushkash_amd.build import DECODE_INST, FLAGS
+    tmp = tmp_path_factory.mktemp("isa")
     flags = [f for f in FLAGS if f not in ("-shared", "-fPIC")]
-    subprocess.run([hipcc, *flags, f"-I{ROOT / 'include'}", "-S", "--cuda-device-only", str(SRC), "-o", str(out)],
-                   check=True, capture_output=True)
-    return out.read_text()
+
+    def compile_one(i_defs):
+        i, defs = i_defs
+        out = tmp / f"kush_decode_{i}.s"
+        subprocess.run([hipcc, *flags, *(f"-D{k}={v}" for k, v in defs.items()), f"-I{ROOT / 'include'}", "-S",
+                        "--cuda-device-only", str(SRC), "-o", str(out)], check=True, capture_output=True)
+        return out.read_text()
+
+    with ThreadPoolExecutor(len(DECODE_INST)) as ex:
+        return "\n".join(ex.map(compile_one, enumerate(DECODE_INST)))
 
 
 def kernels(asm_text: str) -> dict[str, list[str]]:
