@@ -81,7 +81,9 @@ def parse_args(argv=None):
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="instead of the decode, run --steps device-to-device copies of MIB MiB: the plain copy "
                          "kernel of known size that scales rocprofv3's FETCH_SIZE / WRITE_SIZE")
-    ap.add_argument("--rot", action="store_true", help="c4-unpack: rotate history rows back (canonical FWHT)")
+    ap.add_argument("--rot", action="store_true",
+                    help="c2 / c4-write: the Walsh-Hadamard rotation folded into the kernels (rot = 1); "
+                         "c4-unpack: rotate history rows back (canonical FWHT)")
     ap.add_argument("--two-launch", action="store_true",
                     help="c4-write: the reference's two launches (mode 0, mode 1) instead of one fused launch")
     ap.add_argument("--config", default="c2", choices=("c2", "c3", "c4", "c4-write", "c4-unpack", "c4-fwht"),
@@ -126,12 +128,12 @@ def make_workload(a, dev):
             js = torch.arange(n, dtype=torch.int32, device=dev).repeat_interleave(pages)
             jp = torch.arange(pages, dtype=torch.int32, device=dev).repeat(n)
             ops.write(k, v, qsl, seq_lens[s0:s1], tail_idx[s0:s1], js, jp, cache, tables[i][s0:s1].contiguous(),
-                      tail_k)
+                      tail_k, rot=a.rot)
             del k, v
     q = torch.randn(B, a.hq, D, generator=gen, device=dev).to(dtype)
     torch.cuda.synchronize()
     return dict(ops=ops, cache=cache, tables=tables, tail_k=tail_k, tail_idx=tail_idx, seq_lens=seq_lens, q=q,
-                B=B, N=N, Hkv=Hkv, G=G, D=D, bits=bits, RB=RB, pages=pages, kk=kk)
+                B=B, N=N, Hkv=Hkv, G=G, D=D, bits=bits, RB=RB, pages=pages, kk=kk, rot=a.rot)
 
 
 def algorithmic_bytes(w) -> int:
@@ -158,7 +160,7 @@ def graph_of(w, ns: int, waves: int, n_steps: int):
 
     def step(i):
         ops.decode(w["q"], out, w["cache"], w["tables"][i % P], w["seq_lens"], w["tail_idx"], w["tail_k"], sm, ns,
-                   work, waves=waves)
+                   work, waves=waves, rot=w["rot"])
 
     for i in range(P):                     # eager first call per pool (lazy init outside the capture)
         step(i)
@@ -464,11 +466,11 @@ def bench_c4_write(a) -> None:
 
     def step(i):
         k, v, cache, table = sets[i % P]
-        ops.write(k, v, qsl, sl, tail_idx, js, jp, cache, table, tail_k, fused=not a.two_launch)
+        ops.write(k, v, qsl, sl, tail_idx, js, jp, cache, table, tail_k, fused=not a.two_launch, rot=a.rot)
 
     ms = time_graph(step, a.steps, a.warmup)
     alg = 2 * B * T * Hkv * D * 2 + B * pages * Hkv * RB
-    launches = "two launches: mode 0, mode 1" if a.two_launch else "one launch: mode 2"
+    launches = ("two launches: mode 0, mode 1" if a.two_launch else "one launch: mode 2") + (", rot" if a.rot else "")
     _line("chunked-prefill write us/step + achieved HBM GB/s (% peak), int4, 8 x 2048 tokens", ms * 1e3, alg,
           {"workload": f"C4 write: {B} x {T} new tokens, {Hkv} kv heads, D {D}, int{bits} (512 page jobs x {Hkv} "
                        f"heads, {launches})", "global_batch": B, "tokens": B * T},
@@ -598,7 +600,7 @@ def main(argv=None):
     wv = a.waves or w["ops"].waves(w["B"], w["Hkv"], ns, w["pages"])
     ms = time_steps(w, ns, wv, a.steps, a.warmup)
     workload = (f"C2 Qwen2.5-7B decode layer: {a.hq} q / {a.hkv} kv heads, D {a.dim}, int{a.bits}, page 32, "
-                f"batch {a.batch} x {a.ctx} tokens")
+                f"batch {a.batch} x {a.ctx} tokens" + (", rotation folded into the kernels" if a.rot else ""))
     ms_dec = ms                                   # one kernel per step: the decode kernel is the step
     gbs = alg / ms / 1e6
     gbs_dec = alg / ms_dec / 1e6
