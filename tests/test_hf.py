@@ -179,3 +179,18 @@ def test_generate_needs_gpu_inputs():
     model = _tiny("llama")
     with pytest.raises(ValueError, match="GPU"):
         kk.generate(model, torch.randint(0, 256, (1, 8)), 4)
+
+
+def test_pick_greedy_and_sampling():
+    """generate's token choice (_generate.py:23-30): greedy is argmax; sampling with top_k = 1 is argmax
+    too; top_k never picks outside the k largest logits."""
+    from kushkash_amd._generate import _pick
+    g = torch.Generator().manual_seed(0)
+    logits = torch.randn(4, 50, generator=g)
+    assert torch.equal(_pick(logits, False, 1.0, 0), logits.argmax(-1))
+    torch.manual_seed(1)
+    assert torch.equal(_pick(logits, True, 0.7, 1), logits.argmax(-1))
+    top3 = logits.topk(3, -1).indices
+    for _ in range(20):
+        tok = _pick(logits, True, 1.5, 3)
+        assert bool((top3 == tok[:, None]).any(-1).all())
