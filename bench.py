@@ -28,7 +28,7 @@ its mean duration, from HIP events around the graph of decode kernels) and
 default, c2, is the headline):
   c3        Llama-3.1-8B decode step, 32 q / 8 kv heads, D 128, int8, batch 128 with ragged contexts
             N_i ~ U[256, 8192] (seed 0): append of one token per sequence (pos_offset -1, the vLLM
-            convention) then decode over N_i + 1 tokens
+            convention) and decode over N_i + 1 tokens, in one launch (--two-launch: append, then decode)
   c4        Qwen3-8B decode, 32 q / 8 kv heads, D 128, int4, batch 8 x 131,072 tokens (K bias sigma 4 on
             5% of channels), split-K by the Ops.splits policy (--sweep adds NS 64, 128, 256 ...)
   c4-write  the chunked-prefill write of 2,048 new tokens per sequence of that layer (8 x 2,048 tokens,
@@ -85,7 +85,8 @@ def parse_args(argv=None):
                     help="c2 / c4-write: the Walsh-Hadamard rotation folded into the kernels (rot = 1); "
                          "c4-unpack: rotate history rows back (canonical FWHT)")
     ap.add_argument("--two-launch", action="store_true",
-                    help="c4-write: the reference's two launches (mode 0, mode 1) instead of one fused launch")
+                    help="c4-write: the reference's two launches (mode 0, mode 1); c3: append, then decode, "
+                         "instead of one fused launch")
     ap.add_argument("--config", default="c2", choices=("c2", "c3", "c4", "c4-write", "c4-unpack", "c4-fwht"),
                     help="which configuration to measure (c2: the headline line)")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "decode_c2_traffic.md"),
@@ -386,8 +387,12 @@ def bench_c3(a) -> None:
     wv = a.waves or ops.waves(B, Hkv, ns, max(n1 for n1 in lens) // PAGE + 1)
 
     def step(i):
-        ops.append(k_new, v_new, sl, tail_idx, cache, table, tail_k, pos_offset=-1, advance=False)
-        ops.decode(q, out, cache, table, sl, tail_idx, tail_k, sm, ns, work, waves=wv, order=order)
+        if a.two_launch:                          # the reference's pair of launches
+            ops.append(k_new, v_new, sl, tail_idx, cache, table, tail_k, pos_offset=-1, advance=False)
+            ops.decode(q, out, cache, table, sl, tail_idx, tail_k, sm, ns, work, waves=wv, order=order)
+        else:                                     # one launch: the page's workgroup appends first
+            ops.append_decode(k_new, v_new, q, out, cache, table, sl, tail_idx, tail_k, sm, ns, work, waves=wv,
+                              order=order)
 
     ms = time_graph(step, a.steps, a.warmup)
     RB, DC = record_bytes(D, bits), (D if bits == 8 else D // 2)
@@ -399,10 +404,12 @@ def bench_c3(a) -> None:
     alg = dec + qo + app + B * 4 * (table.shape[1] + 2)
     _line("append + decode us/step + achieved HBM GB/s (% peak), int8, bs128 ragged U[256, 8192]", ms * 1e3, alg,
           {"workload": f"C3 Llama-3.1-8B layer: {Hq} q / {Hkv} kv heads, D {D}, int{bits}, page 32, batch {B}, "
-                       f"N_i ~ U[256, 8192] (seed 0; sum {sum(lens)} tokens), append (pos_offset -1) + decode",
+                       f"N_i ~ U[256, 8192] (seed 0; sum {sum(lens)} tokens), append (pos_offset -1) + decode"
+                       + (" (two launches)" if a.two_launch else " (one launch)"),
            "global_batch": B, "split_k": ns, "tokens": sum(n1), "sequence_order": "longest first",
            "waves": wv},
-          f"append_kernel<{D},{bits},bf16> + decode_kernel<{D},{bits},bf16,{wv}>")
+          (f"append_kernel<{D},{bits},bf16> + " if a.two_launch else "fused append + ")
+          + f"decode_kernel<{D},{bits},bf16,{wv}>")
 
 
 def bench_c4(a) -> None:

@@ -104,6 +104,19 @@ int kush_decode(int head_dim, int bits, int group, int dtype, const void* q, voi
                 int32_t hkv, float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t* split_sync,
                 int32_t waves, const int32_t* seq_order, int32_t n_seqs, int32_t rot, void* stream);
 
+/* kush_append (pos_offset = -1, advance = 0: row s of k / v is the token at position seq_lens[s] - 1,
+ * which seq_lens already counts, the serving engines' convention) followed by kush_decode, in one
+ * launch: the workgroup that reads the token's page appends it first (same bytes as kush_append).
+ * group <= 16 and 16-byte aligned k / v rows (otherwise -2: call the two entry points). No
+ * reference counterpart (the reference launches kush_append then a decode kernel, gpu.mojo:207-238,
+ * :566-807, as _ops.py:66-80 and :191-213 issue them). */
+int kush_append_decode(int head_dim, int bits, int group, int dtype, const void* k, const void* v,
+                       int64_t k_row_stride, int64_t v_row_stride, const void* q, void* out, void* cache,
+                       int64_t block_stride, int64_t head_stride, void* tail_k, const int32_t* tail_idx,
+                       const int32_t* block_table, const int32_t* seq_lens, int64_t bt_row_stride, int32_t bt_cols,
+                       int32_t hkv, float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t* split_sync,
+                       int32_t waves, const int32_t* seq_order, int32_t n_seqs, int32_t rot, void* stream);
+
 /* Walsh-Hadamard rotation of rows of head_dim elements: y[r] = fwht(x[r]) for r < rows (row strides
  * in elements; y may alias x), in the canonical order — butterflies at strides 1, 2, ..., D/2, then
  * one fp32 multiply by 1/sqrt(D), rounded once to dtype — bit-identical to the reference's CPU
@@ -137,7 +150,7 @@ int kush_combine(int head_dim, int group, int dtype, void* out, const float* par
  * reference raises the driver's error string directly (_cuda.py:39-43). */
 const char* kush_last_error(void);
 
-/* ABI revision of this header (6). No reference counterpart. */
+/* ABI revision of this header (7). No reference counterpart. */
 int kush_abi_version(void);
 
 #ifdef __cplusplus

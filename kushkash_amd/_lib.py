@@ -14,7 +14,7 @@ from pathlib import Path
 import torch   # noqa: F401  -- loads torch's HIP runtime first; the library binds to it (same soname)
 
 LIB = Path(__file__).resolve().parent / "libkushhip.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _P, _I32, _I64, _F = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float
 SIGNATURES = {
@@ -31,6 +31,11 @@ SIGNATURES = {
     # rot, stream
     "kush_decode": [_I32, _I32, _I32, _I32, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _I64, _I32, _I32, _F, _I32, _P,
                     _P, _P, _I32, _P, _I32, _I32, _P],
+    # head_dim, bits, group, dtype, k, v, k_row_stride, v_row_stride, q, out, cache, block_stride, head_stride,
+    # tail_k, tail_idx, block_table, seq_lens, bt_row_stride, bt_cols, hkv, scale, n_splits, part_ml, part_o,
+    # split_sync, waves, seq_order, n_seqs, rot, stream
+    "kush_append_decode": [_I32, _I32, _I32, _I32, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _I64,
+                           _I32, _I32, _F, _I32, _P, _P, _P, _I32, _P, _I32, _I32, _P],
     # head_dim, group, dtype, out, part_ml, part_o, n_splits, hkv, n_seqs, rot, stream
     "kush_combine": [_I32, _I32, _I32, _P, _P, _P, _I32, _I32, _I32, _I32, _P],
     # head_dim, dtype, x, y, x_row_stride, y_row_stride, rows, stream

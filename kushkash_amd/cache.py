@@ -168,6 +168,27 @@ class KushCache:
         `_work` (only grows; freeze() fixes it for graph capture) (cache.py:164-183)."""
         if self._len[layer] == 0:
             raise RuntimeError("attend() on an empty cache")
+        return self._decode(layer, q, None, None)
+
+    def append_attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        """write(layer, k, v) of one token per sequence, then attend(layer, q), with the append done
+        inside the decode launch (Ops.append_decode): one launch fewer per decode step. k, v: [B, Hkv,
+        1, D]; q: [B, Hq, D]. The same cache contents and outputs as the two calls. No reference
+        counterpart (its attention backends call write, then attend)."""
+        B, H, T, D = k.shape
+        if (B, H, T, D) != (self.B, self.H, 1, self.D) or v.shape != k.shape:
+            raise ValueError(f"expected k, v of shape [{self.B}, {self.H}, 1, {self.D}], got {tuple(k.shape)}")
+        n = self._len[layer]
+        self._map(-(-(n + 1) // PAGE))
+        if not self.krot:
+            k, v = rotate(k, self.rot, self.kdtype), rotate(v, self.rot, self.kdtype)
+        k = k.to(self.kdtype).reshape(B, H, D).contiguous()
+        v = v.to(self.kdtype).reshape(B, H, D).contiguous()
+        self.seq_lens[layer].add_(1)                   # the kernel appends at seq_lens - 1 (counted)
+        self._len[layer] = n + 1
+        return self._decode(layer, q, k, v)
+
+    def _decode(self, layer: int, q: torch.Tensor, k: torch.Tensor | None, v: torch.Tensor | None) -> torch.Tensor:
         q = (q.to(self.kdtype) if self.krot else rotate(q, self.rot, self.kdtype)).contiguous()
         out = torch.empty_like(q)
         pages = (self._capacity if self._frozen_ns else self._len[layer]) // PAGE
@@ -180,8 +201,12 @@ class KushCache:
         kw = {"waves": self.ops.waves(self.B, self.H, ns, pages)} if self.gpu else {}
         if self.krot:
             kw["rot"] = True
-        self.ops.decode(q, out, self.pool[layer], self.block_table, self.seq_lens[layer], self.tail_idx,
-                        self.tail_k[layer], self.scale, ns, self._work, **kw)
+        args = (self.pool[layer], self.block_table, self.seq_lens[layer], self.tail_idx, self.tail_k[layer], self.scale,
+                ns, self._work)
+        if k is None:
+            self.ops.decode(q, out, *args, **kw)
+        else:
+            self.ops.append_decode(k, v, q, out, *args, **kw)
         return out.to(self.dtype) if self.krot else rotate(out, self.rot, self.dtype)
 
     def attend_chunk(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,

@@ -23,7 +23,10 @@
 // The partial last page takes exact fp32 K . q scores from the tail (spread over all waves) and V
 // rows from its record. A rotated cache (ROT) gets q rotated by the canonical Walsh-Hadamard
 // transform on load (rows of the chunk's heads in the butterfly layout, through LDS) and the output
-// rotated back before its one rounding; split partials stay unrotated. The waves (and streams) merge through the idle ring at the end; with
+// rotated back before its one rounding; split partials stay unrotated. With app_k (the fused append
+// + decode), the workgroup that reads the new token's page first appends the token (row s of app_k /
+// app_v at position seq_lens[s] - 1): K to the tail, V into its record row, the K page quantized
+// when the token completes it -- the page quantizer of kush_page.h over the idle ring LDS. The waves (and streams) merge through the idle ring at the end; with
 // split-K, partials are published write-through and the last workgroup of a (sequence, kv head)
 // merges them in the same launch.
 //
@@ -36,7 +39,7 @@
 
 #include <cmath>
 
-#include "kush_fwht.h"
+#include "kush_page.h"
 
 namespace kush {
 
@@ -588,11 +591,12 @@ __device__ __forceinline__ float fetch(const float* p) {
 // finish merges all splits into `out` and resets its counter, so no second launch is needed.
 template <int D, int BITS, typename IN, int NW, int ST, bool ROT>
 __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) void decode_kernel(
-    const IN* __restrict__ qg, IN* __restrict__ out, const uint8_t* __restrict__ cache, int64_t bs, int64_t hs,
-    const IN* __restrict__ tail_k, const int32_t* __restrict__ tail_idx, const int32_t* __restrict__ block_table,
+    const IN* __restrict__ qg, IN* __restrict__ out, uint8_t* __restrict__ cache, int64_t bs, int64_t hs,
+    IN* __restrict__ tail_k, const int32_t* __restrict__ tail_idx, const int32_t* __restrict__ block_table,
     const int32_t* __restrict__ seq_lens, int64_t bt_stride, int bt_cols, int H, int G, float p2, float rs, int NS,
     float* __restrict__ part_ml, float* __restrict__ part_o, int32_t* __restrict__ sync,
-    const int32_t* __restrict__ seq_order) {
+    const int32_t* __restrict__ seq_order, const IN* __restrict__ app_k, const IN* __restrict__ app_v, int64_t app_ks,
+    int64_t app_vs) {
     using F = Fmt<D, BITS>;
     using R = Ring<D, BITS>;
     constexpr int KSTEPS = D / 32;
@@ -607,6 +611,8 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     using AL = AfterLoop<D>;
     static_assert(2 * NW * R::SLOT >= AL::ML_OFF + 2 * NW * 16 * 4 + 16, "the after-loop scratch must fit");
     static_assert(2 * R::DMA <= 63, "vmcnt holds at most 63 loads");
+    static_assert(2 * NW * R::SLOT >= 16 * D * 4, "ROT stages the chunk's q rows in the first array");
+    static_assert(2 * NW * R::SLOT >= tile_bytes<D, IN>(), "the fused append's K tile lives in the first array");
 
     // one array per page pair (wave w at 2 w R::SLOT): the compiler tells the pairs apart and leaves
     // the DMA waits to the explicit vmcnt below (it need not tell the two pages of a pair apart: a
@@ -673,6 +679,28 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     const int pps = (full + NS - 1) / NS;
     const int p0 = min(full, z * pps), p1 = min(full, p0 + pps);
     const uint8_t* head_base = cache + (int64_t)h * hs;
+
+    // Fused append (app_k): the token at position n - 1 of sequence s, kv head h, is written by the one
+    // workgroup that reads its page -- the split holding the page when the token completes it, else
+    // the last split (which takes the partial page) -- of the first head chunk (the entry point takes
+    // at most 16 q heads per kv head). Its stores are complete and visible to its own page loads after
+    // the barrier; no other workgroup reads that page or the sequence's tail.
+    if (app_k != nullptr) {
+        if (gc == 0 && n > 0) {
+            const int pos = n - 1, slot = pos % PAGE, pg = pos / PAGE;
+            const int owner = slot == PAGE - 1 ? pg / max(pps, 1) : NS - 1;
+            if (z == owner) {
+                const IN* krow = app_k + (int64_t)s * app_ks + (int64_t)h * D;
+                IN* tail = tail_k + ((int64_t)tail_idx[s] * H + h) * PAGE * D;
+                uint8_t* rec = cache + (int64_t)bt[pg] * bs + (int64_t)h * hs;
+                stash_rows<D, IN, true, ROT, NW * WAVE>(tail + slot * D, krow, 0, 1, (int)threadIdx.x);
+                page_task<D, BITS, IN, true, NW * WAVE, ROT>(tail, krow, 0, PAGE - 1, slot == PAGE - 1,
+                                                             app_v + (int64_t)s * app_vs + (int64_t)h * D, 0, slot,
+                                                             slot + 1, rec, ringA);
+            }
+        }
+        __syncthreads();
+    }
     const bool has_tail = tail_n > 0 && z == NS - 1;
     uint8_t* const sl0 = ringA + 2 * w * R::SLOT;
     uint8_t* const sl1 = sl0 + R::SLOT;
@@ -1084,19 +1112,22 @@ template <int D, int BITS, typename IN, int NW, bool ROT>
 int launch_decode(dim3 grid, hipStream_t stream, const void* q, void* out, const void* cache, int64_t bs,
                          int64_t hs, const void* tail_k, const int32_t* tail_idx, const int32_t* block_table,
                          const int32_t* seq_lens, int64_t bt_stride, int bt_cols, int hkv, int group, float p2, float rs,
-                         int n_splits, float* part_ml, float* part_o, int32_t* sync, const int32_t* seq_order);
+                         int n_splits, float* part_ml, float* part_o, int32_t* sync, const int32_t* seq_order,
+                         const void* app_k, const void* app_v, int64_t app_ks, int64_t app_vs);
 
 #ifdef KUSH_DECODE_INSTANTIATE
 template <int D, int BITS, typename IN, int NW, bool ROT>
 int launch_decode(dim3 grid, hipStream_t stream, const void* q, void* out, const void* cache, int64_t bs,
                          int64_t hs, const void* tail_k, const int32_t* tail_idx, const int32_t* block_table,
                          const int32_t* seq_lens, int64_t bt_stride, int bt_cols, int hkv, int group, float p2, float rs,
-                         int n_splits, float* part_ml, float* part_o, int32_t* sync, const int32_t* seq_order) {
+                         int n_splits, float* part_ml, float* part_o, int32_t* sync, const int32_t* seq_order,
+                         const void* app_k, const void* app_v, int64_t app_ks, int64_t app_vs) {
     // two page streams whenever the heads of a kv head fit in half the MFMA columns
     auto kern = group <= 8 ? decode_kernel<D, BITS, IN, NW, 2, ROT> : decode_kernel<D, BITS, IN, NW, 1, ROT>;
     kern<<<grid, dim3(NW * WAVE), 0, stream>>>(
-        (const IN*)q, (IN*)out, (const uint8_t*)cache, bs, hs, (const IN*)tail_k, tail_idx, block_table, seq_lens,
-        bt_stride, bt_cols, hkv, group, p2, rs, n_splits, part_ml, part_o, sync, seq_order);
+        (const IN*)q, (IN*)out, (uint8_t*)cache, bs, hs, (IN*)tail_k, tail_idx, block_table, seq_lens, bt_stride,
+        bt_cols, hkv, group, p2, rs, n_splits, part_ml, part_o, sync, seq_order, (const IN*)app_k, (const IN*)app_v,
+        app_ks, app_vs);
     return kush_check_launch("kush_decode");
 }
 #endif

@@ -1,26 +1,36 @@
-// C entry points of the fused dequant decode attention (kush_decode) and the split-K combine
-// (kush_combine); the kernels and their launch are in kush_decode.h (contract and design notes there).
+// C entry points of the fused dequant decode attention (kush_decode), the same launch with the
+// step's token appended first (kush_append_decode) and the split-K combine (kush_combine); the
+// kernels and their launch are in kush_decode.h (contract and design notes there).
 #include "kush_decode.h"
 
 using namespace kush;
 
-extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const void* q, void* out, const void* cache,
-                           int64_t block_stride, int64_t head_stride, const void* tail_k, const int32_t* tail_idx,
-                           const int32_t* block_table, const int32_t* seq_lens, int64_t bt_stride, int32_t bt_cols,
-                           int32_t hkv, float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t* split_sync,
-                           int32_t waves, const int32_t* seq_order, int32_t n_seqs, int32_t rot, void* stream) {
+namespace {
+
+// The new tokens of a fused append + decode (row s of k / v at position seq_lens[s] - 1), or none
+struct Append {
+    const void* k = nullptr;
+    const void* v = nullptr;
+    int64_t k_stride = 0, v_stride = 0;
+};
+
+int decode_impl(const char* what, int head_dim, int bits, int group, int dtype, const void* q, void* out,
+                const void* cache, int64_t block_stride, int64_t head_stride, const void* tail_k, const int32_t* tail_idx,
+                const int32_t* block_table, const int32_t* seq_lens, int64_t bt_stride, int32_t bt_cols, int32_t hkv,
+                float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t* split_sync, int32_t waves,
+                const int32_t* seq_order, int32_t n_seqs, int32_t rot, const Append& app, void* stream) {
     if (n_seqs < 0 || hkv <= 0 || group <= 0 || n_splits <= 0 || bt_cols < 0 || rot < 0 || rot > 1)
-        return kush_fail(-2, "kush_decode: bad n_seqs %d / hkv %d / group %d / n_splits %d / bt_cols %d / rot %d", n_seqs,
+        return kush_fail(-2, "%s: bad n_seqs %d / hkv %d / group %d / n_splits %d / bt_cols %d / rot %d", what, n_seqs,
                          hkv, group, n_splits, bt_cols, rot);
     if (n_splits > 1 && (part_ml == nullptr || part_o == nullptr))
-        return kush_fail(-2, "kush_decode: n_splits %d needs the partial buffers", n_splits);
+        return kush_fail(-2, "%s: n_splits %d needs the partial buffers", what, n_splits);
     if (((uintptr_t)cache | (uint64_t)block_stride | (uint64_t)head_stride) & 15)
-        return kush_fail(-2, "kush_decode: cache records must be 16-byte aligned");
-    if (((uintptr_t)q | (uintptr_t)tail_k) & 15) return kush_fail(-2, "kush_decode: q and tail_k must be 16-byte aligned");
+        return kush_fail(-2, "%s: cache records must be 16-byte aligned", what);
+    if (((uintptr_t)q | (uintptr_t)tail_k) & 15) return kush_fail(-2, "%s: q and tail_k must be 16-byte aligned", what);
     if (waves == 0) waves = 8;
-    if (waves != 2 && waves != 4 && waves != 8) return kush_fail(-2, "kush_decode: waves must be 0, 2, 4 or 8");
+    if (waves != 2 && waves != 4 && waves != 8) return kush_fail(-2, "%s: waves must be 0, 2, 4 or 8", what);
     const int n_gc = (group + 15) / 16;
-    if ((int64_t)n_splits * n_gc > 65535) return kush_fail(-2, "kush_decode: n_splits %d too large", n_splits);
+    if ((int64_t)n_splits * n_gc > 65535) return kush_fail(-2, "%s: n_splits %d too large", what, n_splits);
     // scores in log2 units: scale log2 e = p2 rs with p2 a signed power of two (q p2 is exact in fp16
     // for bf16 / fp16 q) and rs in [2^-0.5, 2^0.5] (a zero scale becomes 2^-120: x ~ 0, masks stay -inf)
     const float sm_log2 = (float)((double)scale * 1.4426950408889634);
@@ -36,12 +46,13 @@ extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const v
     }
     const dim3 grid(n_seqs, hkv, n_splits * n_gc);
     hipStream_t st = (hipStream_t)stream;
-    return dispatch_shape(head_dim, bits, dtype, "kush_decode", [&](auto dd, auto bb, auto in) -> int {
+    return dispatch_shape(head_dim, bits, dtype, what, [&](auto dd, auto bb, auto in) -> int {
         constexpr int D = decltype(dd)::value, BITS = decltype(bb)::value;
         using IN = decltype(in);
         if (n_seqs == 0) return 0;
 #define KUSH_DECODE_ARGS grid, st, q, out, cache, block_stride, head_stride, tail_k, tail_idx, block_table, seq_lens, \
-                         bt_stride, bt_cols, hkv, group, p2, rs, n_splits, part_ml, part_o, split_sync, seq_order
+                         bt_stride, bt_cols, hkv, group, p2, rs, n_splits, part_ml, part_o, split_sync, seq_order, app.k, \
+                         app.v, app.k_stride, app.v_stride
         // the largest of the requested, 4 and 2 waves whose rings fit in LDS
         const auto launch = [&](auto nw) -> int {
             constexpr int NW = decltype(nw)::value;
@@ -58,6 +69,35 @@ extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const v
         return launch(std::integral_constant<int, 2>{});
 #undef KUSH_DECODE_ARGS
     });
+}
+
+}  // namespace
+
+extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const void* q, void* out, const void* cache,
+                           int64_t block_stride, int64_t head_stride, const void* tail_k, const int32_t* tail_idx,
+                           const int32_t* block_table, const int32_t* seq_lens, int64_t bt_stride, int32_t bt_cols,
+                           int32_t hkv, float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t* split_sync,
+                           int32_t waves, const int32_t* seq_order, int32_t n_seqs, int32_t rot, void* stream) {
+    return decode_impl("kush_decode", head_dim, bits, group, dtype, q, out, cache, block_stride, head_stride, tail_k,
+                       tail_idx, block_table, seq_lens, bt_stride, bt_cols, hkv, scale, n_splits, part_ml, part_o,
+                       split_sync, waves, seq_order, n_seqs, rot, Append{}, stream);
+}
+
+extern "C" int kush_append_decode(int head_dim, int bits, int group, int dtype, const void* k, const void* v,
+                                  int64_t k_row_stride, int64_t v_row_stride, const void* q, void* out, void* cache,
+                                  int64_t block_stride, int64_t head_stride, void* tail_k, const int32_t* tail_idx,
+                                  const int32_t* block_table, const int32_t* seq_lens, int64_t bt_stride,
+                                  int32_t bt_cols, int32_t hkv, float scale, int32_t n_splits, float* part_ml,
+                                  float* part_o, int32_t* split_sync, int32_t waves, const int32_t* seq_order,
+                                  int32_t n_seqs, int32_t rot, void* stream) {
+    if (group > 16) return kush_fail(-2, "kush_append_decode: group %d > 16 (use kush_append, then kush_decode)", group);
+    if (k == nullptr || v == nullptr) return kush_fail(-2, "kush_append_decode: k and v are required");
+    const int64_t e = dtype == 0 ? 4 : 2;
+    if (((uintptr_t)k | (uintptr_t)v | (uint64_t)(k_row_stride * e) | (uint64_t)(v_row_stride * e)) & 15)
+        return kush_fail(-2, "kush_append_decode: k / v rows must be 16-byte aligned (use kush_append, then kush_decode)");
+    return decode_impl("kush_append_decode", head_dim, bits, group, dtype, q, out, cache, block_stride, head_stride,
+                       tail_k, tail_idx, block_table, seq_lens, bt_stride, bt_cols, hkv, scale, n_splits, part_ml, part_o,
+                       split_sync, waves, seq_order, n_seqs, rot, Append{k, v, k_row_stride, v_row_stride}, stream);
 }
 
 extern "C" int kush_combine(int head_dim, int group, int dtype, void* out, const float* part_ml, const float* part_o,

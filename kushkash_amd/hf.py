@@ -10,7 +10,7 @@ Per layer, transformers calls ``Cache.update`` and then the attention function w
 K/V chunk. ``KushHFCache.update`` stores nothing: it creates the KushCache on first use and leaves
 itself in a thread-local slot, which the attention function takes (the attention interface passes
 no cache). The attention function then, by the chunk's length T and the cached length n:
-  T = 1          append the token (append kernel), decode over the cache (decode kernel);
+  T = 1          append the token and decode over the cache, in one launch (KushCache.append_attend);
   T > 1, n = 0   exact causal attention over the prompt, then the ragged write of the prompt;
   T > 1, n > 0   attention over the dequantized history, one page block at a time, plus the chunk
                  (causal), merged by log-sum-exp (KushCache.attend_chunk); then the write.
@@ -173,8 +173,7 @@ def kush_attention(module, query, key, value, attention_mask, scaling=None, drop
         kv.scale = float(scaling)
     T = query.shape[2]
     if T == 1:
-        kv.write(layer, key, value)
-        return kv.attend(layer, query[:, :, 0]).unsqueeze(1), None
+        return kv.append_attend(layer, query[:, :, 0], key, value).unsqueeze(1), None
     if layer == 0:
         _check_start(kv, kwargs.get("position_ids"))
     if kv.length(layer) == 0:

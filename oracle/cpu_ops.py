@@ -139,6 +139,12 @@ class OracleOps:
              tail_k.data_ptr(), tail_idx.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(),
              block_table.stride(0), H, self.G, float(scale), S)
 
+    def append_decode(self, k, v, q, out, cache, block_table, seq_lens, tail_idx, tail_k, scale: float,
+                      n_splits: int = 1, work=None, **kw) -> None:
+        """The reference's two calls in order: append at seq_lens - 1 (already counted), then decode."""
+        self.append(k, v, seq_lens, tail_idx, cache, block_table, tail_k, pos_offset=-1, advance=False)
+        self.decode(q, out, cache, block_table, seq_lens, tail_idx, tail_k, scale, n_splits, work)
+
 
 if os.environ.get("KUSH_ORACLE_THREADS"):
     set_threads(int(os.environ["KUSH_ORACLE_THREADS"]))

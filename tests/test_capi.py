@@ -34,7 +34,8 @@ def header_functions() -> dict[str, int]:
 
 def test_header_declares_the_entry_points():
     fns = header_functions()
-    assert set(fns) == {"kush_append", "kush_write", "kush_decode", "kush_combine", "kush_fwht", "kush_unpack", "kush_last_error",
+    assert set(fns) == {"kush_append", "kush_write", "kush_decode", "kush_append_decode", "kush_combine", "kush_fwht",
+                        "kush_unpack", "kush_last_error",
                         "kush_abi_version"}
 
 
