@@ -6,7 +6,8 @@ accumulation (the acceptance bound of the compressed-KV decode).
 
 C2: Qwen2.5-7B layer, int4, 64 x 4096 tokens (the headline line's workload).
 C3: Llama-3.1-8B layer, int8, 128 ragged sequences U[256, 8192] with one appended token each and
-    the longest-first order, 2 waves.
+    the longest-first order, 2 waves; the append and decode in one launch (the bench line's step) and
+    in two.
 C4: Qwen3-8B layer, int4, 8 x 131,072 tokens with split-K merged in the launch, 8 waves."""
 import math
 
@@ -45,7 +46,8 @@ def test_c2_full_size():
     check(out, reference(w["q"], w["cache"], w["tables"][0], w["N"], w["tail_k"], D, w["bits"]), "C2")
 
 
-def test_c3_full_size():
+@pytest.mark.parametrize("fused", [True, False])
+def test_c3_full_size(fused):
     from kushkash_amd._ops import Ops
     B, Hq, Hkv, D, bits = 128, 32, 8, 128, 8
     G, dtype = Hq // Hkv, torch.bfloat16
@@ -58,13 +60,17 @@ def test_c3_full_size():
     v_new = torch.randn(B, Hkv, D, generator=gen, device=DEV).to(dtype)
     q = torch.randn(B, Hq, D, generator=gen, device=DEV).to(dtype)
     sl = torch.tensor(lens, dtype=torch.int32, device=DEV) + 1
-    ops.append(k_new, v_new, sl, tail_idx, cache, table, tail_k, pos_offset=-1, advance=False)
     ns = ops.splits(B, Hkv, max(lens) // PAGE + 1)
     work = torch.empty(max(1, B * Hkv * ns * G * (D + 2)), dtype=torch.float32, device=DEV)
     order = torch.tensor(sorted(range(B), key=lambda i: -lens[i]), dtype=torch.int32, device=DEV)
     out = torch.empty_like(q)
-    ops.decode(q, out, cache, table, sl, tail_idx, tail_k, 1.0 / math.sqrt(D), ns, work,
-               waves=ops.waves(B, Hkv, ns, max(lens) // PAGE + 1), order=order)
+    launch = dict(waves=ops.waves(B, Hkv, ns, max(lens) // PAGE + 1), order=order)
+    if fused:
+        ops.append_decode(k_new, v_new, q, out, cache, table, sl, tail_idx, tail_k, 1.0 / math.sqrt(D), ns, work,
+                          **launch)
+    else:
+        ops.append(k_new, v_new, sl, tail_idx, cache, table, tail_k, pos_offset=-1, advance=False)
+        ops.decode(q, out, cache, table, sl, tail_idx, tail_k, 1.0 / math.sqrt(D), ns, work, **launch)
     for i in range(B):                                         # ragged: one sequence at a time
         t = int(tail_idx[i])
         ref = reference(q[i:i + 1], cache, table[i:i + 1], lens[i] + 1, tail_k[t:t + 1], D, bits)
