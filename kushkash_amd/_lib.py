@@ -14,32 +14,41 @@ from pathlib import Path
 import torch   # noqa: F401  -- loads torch's HIP runtime first; the library binds to it (same soname)
 
 LIB = Path(__file__).resolve().parent / "libkushhip.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _P, _I32, _I64, _F = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float
+
+# head_dim, bits, dtype, k, v, k_row_stride, v_row_stride, seq_lens, pos_offset, advance, tail_idx, cache,
+# block_stride, head_stride, tail_k, block_table, bt_row_stride, hkv, n_seqs, stream
+_APPEND = [_I32, _I32, _I32, _P, _P, _I64, _I64, _P, _I32, _I32, _P, _P, _I64, _I64, _P, _P, _I64, _I32, _I32, _P]
+# head_dim, bits, dtype, k, v, k_row_stride, v_row_stride, query_start_loc, seq_lens, tail_idx, job_seq, job_page,
+# n_jobs, mode, cache, block_stride, head_stride, tail_k, block_table, bt_row_stride, hkv, stream
+_WRITE = [_I32, _I32, _I32, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _I32, _I32, _P, _I64, _I64, _P, _P, _I64, _I32, _P]
+# head_dim, bits, group, dtype, q, out, cache, block_stride, head_stride, tail_k, tail_idx, block_table, seq_lens,
+# bt_row_stride, hkv, scale, n_splits, part_ml, part_o, n_seqs, stream
+_DECODE = [_I32, _I32, _I32, _I32, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _I64, _I32, _F, _I32, _P, _P, _I32, _P]
+# bt_cols, split_sync, waves, seq_order, rot
+_DECODE_EXT = [_I32, _P, _I32, _P, _I32]
+# head_dim, group, dtype, out, part_ml, part_o, n_splits, hkv, n_seqs, stream
+_COMBINE = [_I32, _I32, _I32, _P, _P, _P, _I32, _I32, _I32, _P]
+
+# Each reference entry point takes the reference's argument list; its `_ex` variant appends this
+# library's extensions after the stream (include/kushkash_amd.h).
 SIGNATURES = {
-    # head_dim, bits, dtype, k, v, k_row_stride, v_row_stride, seq_lens, pos_offset, advance, tail_idx,
-    # cache, block_stride, head_stride, tail_k, block_table, bt_row_stride, hkv, n_seqs, rot, stream
-    "kush_append": [_I32, _I32, _I32, _P, _P, _I64, _I64, _P, _I32, _I32, _P, _P, _I64, _I64, _P, _P, _I64, _I32,
-                    _I32, _I32, _P],
-    # head_dim, bits, dtype, k, v, k_row_stride, v_row_stride, query_start_loc, seq_lens, tail_idx, job_seq,
-    # job_page, n_jobs, mode, cache, block_stride, head_stride, tail_k, block_table, bt_row_stride, hkv, rot, stream
-    "kush_write": [_I32, _I32, _I32, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _I32, _I32, _P, _I64, _I64, _P, _P,
-                   _I64, _I32, _I32, _P],
-    # head_dim, bits, group, dtype, q, out, cache, block_stride, head_stride, tail_k, tail_idx, block_table,
-    # seq_lens, bt_row_stride, bt_cols, hkv, scale, n_splits, part_ml, part_o, split_sync, waves, seq_order, n_seqs,
-    # rot, stream
-    "kush_decode": [_I32, _I32, _I32, _I32, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _I64, _I32, _I32, _F, _I32, _P,
-                    _P, _P, _I32, _P, _I32, _I32, _P],
-    # head_dim, bits, group, dtype, k, v, k_row_stride, v_row_stride, q, out, cache, block_stride, head_stride,
-    # tail_k, tail_idx, block_table, seq_lens, bt_row_stride, bt_cols, hkv, scale, n_splits, part_ml, part_o,
-    # split_sync, waves, seq_order, n_seqs, rot, stream
-    "kush_append_decode": [_I32, _I32, _I32, _I32, _P, _P, _I64, _I64, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _I64,
-                           _I32, _I32, _F, _I32, _P, _P, _P, _I32, _P, _I32, _I32, _P],
-    # head_dim, group, dtype, out, part_ml, part_o, n_splits, hkv, n_seqs, rot, stream
-    "kush_combine": [_I32, _I32, _I32, _P, _P, _P, _I32, _I32, _I32, _I32, _P],
+    "kush_append": _APPEND,
+    "kush_append_ex": _APPEND + [_I32],                          # + rot
+    "kush_write": _WRITE,
+    "kush_write_ex": _WRITE + [_I32],                            # + rot
+    "kush_decode": _DECODE,
+    "kush_decode_ex": _DECODE + _DECODE_EXT,
+    # + k, v, k_row_stride, v_row_stride, then the decode extensions
+    "kush_append_decode": _DECODE + [_P, _P, _I64, _I64] + _DECODE_EXT,
+    "kush_combine": _COMBINE,
+    "kush_combine_ex": _COMBINE + [_I32],                        # + rot
     # head_dim, dtype, x, y, x_row_stride, y_row_stride, rows, stream
     "kush_fwht": [_I32, _I32, _P, _P, _I64, _I64, _I64, _P],
+    # head_dim, bits, dtype, cache, block_stride, head_stride, hkv, page_blk, page_dst, n_pages, tail_blk, tail_info,
+    # n_tail, tail_k, k_new, v_new, k_stride, v_stride, new_dst, n_new, kp, vp, rot, stream
     "kush_unpack": [_I32, _I32, _I32, _P, _I64, _I64, _I32, _P, _P, _I64, _P, _P, _I64, _P, _P, _P, _I64, _I64, _P,
                     _I64, _P, _P, _I32, _P],
     "kush_last_error": [],

@@ -199,10 +199,10 @@ class Ops:
             raise ValueError("seq_lens, tail_idx and block_table need one entry per sequence")
         self._check_values(cache, block_table, seq_lens, tail_idx, tail_k, S, extra=pos_offset + 1)
         bs, hs = _byte_strides(cache)
-        self._lib.call("kush_append", self.D, self.bits, self._dt, k.data_ptr(), v.data_ptr(), k.stride(0),
+        self._lib.call("kush_append_ex", self.D, self.bits, self._dt, k.data_ptr(), v.data_ptr(), k.stride(0),
                        v.stride(0), seq_lens.data_ptr(), int(pos_offset), int(bool(advance)), tail_idx.data_ptr(),
                        cache.data_ptr(), bs, hs, tail_k.data_ptr(), block_table.data_ptr(), block_table.stride(0),
-                       H, S, int(bool(rot)), self._stream())
+                       H, S, self._stream(), int(bool(rot)))
 
     def write(self, k: torch.Tensor, v: torch.Tensor, query_start_loc: torch.Tensor, seq_lens: torch.Tensor,
               tail_idx: torch.Tensor, job_seq: torch.Tensor, job_page: torch.Tensor, cache: torch.Tensor,
@@ -238,11 +238,11 @@ class Ops:
             self._check_values(cache, block_table, seq_lens, tail_idx, tail_k, S)
         bs, hs = _byte_strides(cache)
         for mode in ((2,) if fused else (0, 1)):
-            self._lib.call("kush_write", self.D, self.bits, self._dt, k.data_ptr(), v.data_ptr(), k.stride(0),
+            self._lib.call("kush_write_ex", self.D, self.bits, self._dt, k.data_ptr(), v.data_ptr(), k.stride(0),
                            v.stride(0), query_start_loc.data_ptr(), seq_lens.data_ptr(), tail_idx.data_ptr(),
                            job_seq.data_ptr(), job_page.data_ptr(), n_jobs, mode, cache.data_ptr(), bs, hs,
-                           tail_k.data_ptr(), block_table.data_ptr(), block_table.stride(0), H, int(bool(rot)),
-                           self._stream())
+                           tail_k.data_ptr(), block_table.data_ptr(), block_table.stride(0), H, self._stream(),
+                           int(bool(rot)))
 
     # ---------------------------------------------------------------- rotation
     def fwht(self, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -415,19 +415,19 @@ class Ops:
         fused = n_splits > 1 and S * H * (-(-G // 16)) <= SYNC_SLOTS
         sync = self._sync.data_ptr() if fused else None
         wv = self.waves(S, H, n_splits, block_table.shape[1]) if waves is None else int(waves)
-        tail = (block_table.stride(0), min(block_table.shape[1], 1 << 30), H, float(scale), int(n_splits), part_ml,
-                part_o, sync, wv, order.data_ptr() if order is not None else None, S, int(bool(rot)), stream)
+        ref = (D, self.bits, G, self._dt, q.data_ptr(), out.data_ptr(), cache.data_ptr(), bs, hs, tail_k.data_ptr(),
+               tail_idx.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(), block_table.stride(0), H, float(scale),
+               int(n_splits), part_ml, part_o, S, stream)
+        ext = (min(block_table.shape[1], 1 << 30), sync, wv, order.data_ptr() if order is not None else None,
+               int(bool(rot)))
         if app_k is None:
-            self._lib.call("kush_decode", D, self.bits, G, self._dt, q.data_ptr(), out.data_ptr(), cache.data_ptr(),
-                           bs, hs, tail_k.data_ptr(), tail_idx.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(),
-                           *tail)
+            self._lib.call("kush_decode_ex", *ref, *ext)
         else:
-            self._lib.call("kush_append_decode", D, self.bits, G, self._dt, app_k.data_ptr(), app_v.data_ptr(),
-                           app_k.stride(0), app_v.stride(0), q.data_ptr(), out.data_ptr(), cache.data_ptr(), bs, hs,
-                           tail_k.data_ptr(), tail_idx.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(), *tail)
+            self._lib.call("kush_append_decode", *ref, app_k.data_ptr(), app_v.data_ptr(), app_k.stride(0),
+                           app_v.stride(0), *ext)
         if n_splits > 1 and not fused:
-            self._lib.call("kush_combine", D, G, self._dt, out.data_ptr(), part_ml, part_o, int(n_splits), H, S,
-                           int(bool(rot)), stream)
+            self._lib.call("kush_combine_ex", D, G, self._dt, out.data_ptr(), part_ml, part_o, int(n_splits), H, S,
+                           stream, int(bool(rot)))
 
 
 # ---------------------------------------------------------------- reference / prefill helpers (pure torch)

@@ -29,4 +29,4 @@ int kush_check_launch(const char* what) {
 extern "C" const char* kush_last_error(void) { return g_err; }
 
 // Bumped when an entry point's signature or meaning changes.
-extern "C" int kush_abi_version(void) { return 7; }
+extern "C" int kush_abi_version(void) { return 8; }

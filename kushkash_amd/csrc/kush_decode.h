@@ -5,8 +5,8 @@
 //
 // Mapping onto CDNA4. One workgroup = NW waves (2, 4 or 8) for one (sequence, kv head, split,
 // 16-head chunk). The split's pages go out in pairs over windows of up to 1,024 pages whose block
-// ids sit in an LDS table; with 8 waves a counter in LDS hands out the pairs, with 2 or 4 waves
-// wave w takes pairs w, w + NW, ... Per pair a wave:
+// ids sit in an LDS table; wave w takes pairs w, w + NW, ... (a fixed assignment: the same call
+// always sums the same pages in the same order, so its output bits are reproducible). Per pair a wave:
 //   1. has both records staged in its private LDS ring by buffer-to-LDS DMA (whole records, 1 KB
 //      per instruction, issued one pair ahead and waited on with explicit vmcnt counts);
 //   2. reads K code rows from the ring and turns them into exact subnormal fp16 operands (one
@@ -526,7 +526,7 @@ __device__ __forceinline__ void consume2(const uint8_t* s0, int ds, f4 (&o)[D / 
 constexpr int WIN = 1024;
 
 // Static LDS of one decode workgroup: two arrays, each holding one page pair per wave (wave w at
-// 2 w SLOT), the window's block-id table and the pair counter. After the page loop the idle arrays
+// 2 w SLOT) and the window's block-id table. After the page loop the idle arrays
 // hold everything else: the cross-wave merge in the first; the exact-K tail's q and scores, the
 // waves' softmax state and the split-K flag in the second.
 template <int D, int BITS, int NW>
@@ -604,7 +604,6 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     constexpr int NLO = BITS == 4 ? D / 32 : D / 16;          // O tiles in units of 2^-24 (the rest 2^-20)
     constexpr float TWO24 = 16777216.0f, TWO20 = 1048576.0f;
     constexpr bool QLO = std::is_same<IN, float>::value;      // q needs a low fp16 part
-    constexpr bool DYN = NW == 8;                             // pairs from the LDS counter
     const float sm_log2 = p2 * rs;                            // exact: p2 is a power of two
     static_assert(NW == 2 || NW == 4 || NW == 8, "the tail splits 16 heads over 2 NW lane halves");
     static_assert(ST == 1 || ST == 2, "one or two page streams");
@@ -620,7 +619,6 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     __shared__ __align__(16) uint8_t ringA[2 * NW * R::SLOT];
     __shared__ __align__(16) uint8_t ringB[2 * NW * R::SLOT];
     __shared__ __align__(16) int tbl[WIN];                               // block ids of the window
-    __shared__ uint32_t pair_ctr;                                        // next pair of the window
     float* const m_l = reinterpret_cast<float*>(ringB + AL::ML_OFF);      // after the loop only
     float* const l_l = m_l + NW * 16;
     int* const last_flag = reinterpret_cast<int*>(l_l + NW * 16);
@@ -718,11 +716,10 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     float m_run = -__builtin_inff(), l_run = 0.0f, vb_run = 0.0f;
 
     // The split's pages go out in pairs (k: pages 2k, 2k + 1 of the window), over windows of WIN pages
-    // whose block ids are first copied to an LDS table. With 8 waves (two per SIMD, which the hardware
-    // does not run at the same rate) the pairs come from a counter in LDS: the waves run more often
-    // simply take more pairs and all finish together, at the price of bitwise reproducibility (which
-    // wave accumulates which page varies from run to run; results agree to rounding). With 2 or 4
-    // waves, wave w takes pairs w, w + NW, ... (deterministic). A wave holds two pairs,
+    // whose block ids are first copied to an LDS table. Wave w takes pairs w, w + NW, ...: a fixed
+    // assignment, so which wave sums which page, and in which order, never changes between calls
+    // (a counter handing pairs to whichever wave asks first balances two waves per SIMD better, but
+    // then the sums, and so the output bits, vary from call to call). A wave holds two pairs,
     // in slots (0, 1) and (2, 3): one is consumed while the other is in flight. A wave's pairs only
     // grow, so once the pair it would consume is past the window's end, so is the one in flight. Each
     // pair issue is 2 R::DMA instructions, also for a pair past the end (an empty buffer range: no
@@ -739,7 +736,6 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
             } else {
                 for (int i = threadIdx.x; i < wn; i += NW * WAVE) tbl[i] = bt[wb + i];
             }
-            if (threadIdx.x == 0) pair_ctr = 2 * NW;
         };
 #define KUSH_ISSUE_PAIR(SA, SB, P)                                                                 \
     {                                                                                              \
@@ -793,16 +789,15 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         KUSH_ISSUE_PAIR(sl2, sl3, pb)
 
         // One pair step: the pair has landed once at most the other pair's loads are outstanding;
-        // the next pair is taken from the counter (its result and the table read hide behind the
-        // scores), then scores of both pages, one softmax update, PV of both; then, every read of the
+        // scores of both pages (the next pair's table read hides behind them), one softmax update,
+        // PV of both; then, every read of the
         // two slots complete (lgkmcnt 0), they take the next pair. The second page of a window's odd
         // last pair is masked.
 #define KUSH_STEP(SA, SB, P)                                                                       \
     {                                                                                              \
         if ((P) >= pairs) break;                                                                   \
         KUSH_WAIT_VM(2 * R::DMA);                                                                  \
-        int nx = (P) + 2 * NW;                           /* static: this wave's pair after next */  \
-        if (DYN && lane == 0) nx = (int)__builtin_amdgcn_atomic_inc32(&pair_ctr, ~0u, __ATOMIC_RELAXED, "workgroup"); \
+        const int nx = (P) + 2 * NW;                     /* this wave's pair after next */          \
         int2 id2;                                                                                  \
         if constexpr (ST == 2) {                                                                   \
             float sv[8], kx;                                                                       \
@@ -810,7 +805,6 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
             if (2 * (P) + 1 >= wn && r16 >= 8) {                                                   \
                 _Pragma("unroll") for (int jj = 0; jj < 8; ++jj) sv[jj] = -__builtin_inff();       \
             }                                                                                      \
-            nx = __builtin_amdgcn_readfirstlane(nx);                                               \
             id2 = *reinterpret_cast<const int2*>(tbl + min(2 * nx, WIN - 2));                      \
             consume2<D, BITS>(SA, R::SLOT, o, vacc, sv, sa, kx, m_run, l_run, vb_run, lane);       \
         } else {                                                                                   \
@@ -820,7 +814,6 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
             if (2 * (P) + 1 >= wn) {                                                               \
                 _Pragma("unroll") for (int jj = 0; jj < 8; ++jj) sv[1][jj] = -__builtin_inff();    \
             }                                                                                      \
-            nx = __builtin_amdgcn_readfirstlane(nx);                                               \
             id2 = *reinterpret_cast<const int2*>(tbl + min(2 * nx, WIN - 2));                      \
             consume_pages<D, BITS, 2>(sp, o, vacc, sv, sa, kx, m_run, l_run, vb_run, lane);        \
         }                                                                                          \
@@ -835,7 +828,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
                 KUSH_STEP(sl2, sl3, pb)
             }
             KUSH_WAIT_VM(0);                                     // drain the trailing (empty) issues
-            __syncthreads();                                     // table, counter and rings idle
+            __syncthreads();                                     // table and rings idle
             wb += WIN;
             if (wb >= p1) break;
             wn = min(WIN, p1 - wb);

@@ -73,23 +73,35 @@ int decode_impl(const char* what, int head_dim, int bits, int group, int dtype, 
 
 }  // namespace
 
-extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const void* q, void* out, const void* cache,
-                           int64_t block_stride, int64_t head_stride, const void* tail_k, const int32_t* tail_idx,
-                           const int32_t* block_table, const int32_t* seq_lens, int64_t bt_stride, int32_t bt_cols,
-                           int32_t hkv, float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t* split_sync,
-                           int32_t waves, const int32_t* seq_order, int32_t n_seqs, int32_t rot, void* stream) {
+extern "C" int kush_decode_ex(int head_dim, int bits, int group, int dtype, const void* q, void* out,
+                              const void* cache, int64_t block_stride, int64_t head_stride, const void* tail_k,
+                              const int32_t* tail_idx, const int32_t* block_table, const int32_t* seq_lens,
+                              int64_t bt_stride, int32_t hkv, float scale, int32_t n_splits, float* part_ml,
+                              float* part_o, int32_t n_seqs, void* stream, int32_t bt_cols, int32_t* split_sync,
+                              int32_t waves, const int32_t* seq_order, int32_t rot) {
     return decode_impl("kush_decode", head_dim, bits, group, dtype, q, out, cache, block_stride, head_stride, tail_k,
                        tail_idx, block_table, seq_lens, bt_stride, bt_cols, hkv, scale, n_splits, part_ml, part_o,
                        split_sync, waves, seq_order, n_seqs, rot, Append{}, stream);
 }
 
-extern "C" int kush_append_decode(int head_dim, int bits, int group, int dtype, const void* k, const void* v,
-                                  int64_t k_row_stride, int64_t v_row_stride, const void* q, void* out, void* cache,
+// The reference's argument list exactly: no table prefetch, no in-launch merge (n_splits > 1 leaves
+// the partials for kush_combine, as the reference's second launch), the default waves, no rotation.
+extern "C" int kush_decode(int head_dim, int bits, int group, int dtype, const void* q, void* out, const void* cache,
+                           int64_t block_stride, int64_t head_stride, const void* tail_k, const int32_t* tail_idx,
+                           const int32_t* block_table, const int32_t* seq_lens, int64_t bt_stride, int32_t hkv,
+                           float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t n_seqs, void* stream) {
+    return decode_impl("kush_decode", head_dim, bits, group, dtype, q, out, cache, block_stride, head_stride, tail_k,
+                       tail_idx, block_table, seq_lens, bt_stride, 0, hkv, scale, n_splits, part_ml, part_o, nullptr, 0,
+                       nullptr, n_seqs, 0, Append{}, stream);
+}
+
+extern "C" int kush_append_decode(int head_dim, int bits, int group, int dtype, const void* q, void* out, void* cache,
                                   int64_t block_stride, int64_t head_stride, void* tail_k, const int32_t* tail_idx,
-                                  const int32_t* block_table, const int32_t* seq_lens, int64_t bt_stride,
-                                  int32_t bt_cols, int32_t hkv, float scale, int32_t n_splits, float* part_ml,
-                                  float* part_o, int32_t* split_sync, int32_t waves, const int32_t* seq_order,
-                                  int32_t n_seqs, int32_t rot, void* stream) {
+                                  const int32_t* block_table, const int32_t* seq_lens, int64_t bt_stride, int32_t hkv,
+                                  float scale, int32_t n_splits, float* part_ml, float* part_o, int32_t n_seqs,
+                                  void* stream, const void* k, const void* v, int64_t k_row_stride,
+                                  int64_t v_row_stride, int32_t bt_cols, int32_t* split_sync, int32_t waves,
+                                  const int32_t* seq_order, int32_t rot) {
     if (group > 16) return kush_fail(-2, "kush_append_decode: group %d > 16 (use kush_append, then kush_decode)", group);
     if (k == nullptr || v == nullptr) return kush_fail(-2, "kush_append_decode: k and v are required");
     const int64_t e = dtype == 0 ? 4 : 2;
@@ -100,8 +112,8 @@ extern "C" int kush_append_decode(int head_dim, int bits, int group, int dtype, 
                        split_sync, waves, seq_order, n_seqs, rot, Append{k, v, k_row_stride, v_row_stride}, stream);
 }
 
-extern "C" int kush_combine(int head_dim, int group, int dtype, void* out, const float* part_ml, const float* part_o,
-                            int32_t n_splits, int32_t hkv, int32_t n_seqs, int32_t rot, void* stream) {
+extern "C" int kush_combine_ex(int head_dim, int group, int dtype, void* out, const float* part_ml, const float* part_o,
+                               int32_t n_splits, int32_t hkv, int32_t n_seqs, void* stream, int32_t rot) {
     if (n_seqs < 0 || hkv <= 0 || group <= 0 || n_splits <= 0 || rot < 0 || rot > 1)
         return kush_fail(-2, "kush_combine: bad arguments");
     // bits does not matter here: any record format's partials
@@ -113,4 +125,9 @@ extern "C" int kush_combine(int head_dim, int group, int dtype, void* out, const
         kern<<<dim3(n_seqs, hkv), dim3(256), 0, (hipStream_t)stream>>>((IN*)out, part_ml, part_o, n_splits, hkv, group);
         return kush_check_launch("kush_combine");
     });
+}
+
+extern "C" int kush_combine(int head_dim, int group, int dtype, void* out, const float* part_ml, const float* part_o,
+                            int32_t n_splits, int32_t hkv, int32_t n_seqs, void* stream) {
+    return kush_combine_ex(head_dim, group, dtype, out, part_ml, part_o, n_splits, hkv, n_seqs, stream, 0);
 }

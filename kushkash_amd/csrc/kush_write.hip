@@ -132,11 +132,11 @@ static bool rows_aligned(const void* k, const void* v, int64_t k_stride, int64_t
 
 using namespace kush;
 
-extern "C" int kush_append(int head_dim, int bits, int dtype, const void* k, const void* v, int64_t k_stride,
-                           int64_t v_stride, int32_t* seq_lens, int32_t pos_offset, int32_t advance,
-                           const int32_t* tail_idx, void* cache, int64_t block_stride, int64_t head_stride,
-                           void* tail_k, const int32_t* block_table, int64_t bt_stride, int32_t hkv, int32_t n_seqs,
-                           int32_t rot, void* stream) {
+extern "C" int kush_append_ex(int head_dim, int bits, int dtype, const void* k, const void* v, int64_t k_stride,
+                              int64_t v_stride, int32_t* seq_lens, int32_t pos_offset, int32_t advance,
+                              const int32_t* tail_idx, void* cache, int64_t block_stride, int64_t head_stride,
+                              void* tail_k, const int32_t* block_table, int64_t bt_stride, int32_t hkv, int32_t n_seqs,
+                              void* stream, int32_t rot) {
     if (n_seqs < 0 || hkv <= 0 || rot < 0 || rot > 1)
         return kush_fail(-2, "kush_append: bad n_seqs %d / hkv %d / rot %d", n_seqs, hkv, rot);
     return dispatch_shape(head_dim, bits, dtype, "kush_append", [&](auto dd, auto bb, auto in) -> int {
@@ -156,11 +156,11 @@ extern "C" int kush_append(int head_dim, int bits, int dtype, const void* k, con
     });
 }
 
-extern "C" int kush_write(int head_dim, int bits, int dtype, const void* k, const void* v, int64_t k_stride,
-                          int64_t v_stride, const int32_t* query_start_loc, const int32_t* seq_lens,
-                          const int32_t* tail_idx, const int32_t* job_seq, const int32_t* job_page, int32_t n_jobs,
-                          int32_t mode, void* cache, int64_t block_stride, int64_t head_stride, void* tail_k,
-                          const int32_t* block_table, int64_t bt_stride, int32_t hkv, int32_t rot, void* stream) {
+extern "C" int kush_write_ex(int head_dim, int bits, int dtype, const void* k, const void* v, int64_t k_stride,
+                             int64_t v_stride, const int32_t* query_start_loc, const int32_t* seq_lens,
+                             const int32_t* tail_idx, const int32_t* job_seq, const int32_t* job_page, int32_t n_jobs,
+                             int32_t mode, void* cache, int64_t block_stride, int64_t head_stride, void* tail_k,
+                             const int32_t* block_table, int64_t bt_stride, int32_t hkv, void* stream, int32_t rot) {
     if (n_jobs < 0 || hkv <= 0 || mode < 0 || mode > 2 || rot < 0 || rot > 1)
         return kush_fail(-2, "kush_write: bad n_jobs %d / hkv %d / mode %d / rot %d", n_jobs, hkv, mode, rot);
     return dispatch_shape(head_dim, bits, dtype, "kush_write", [&](auto dd, auto bb, auto in) -> int {
@@ -188,4 +188,25 @@ extern "C" int kush_write(int head_dim, int bits, int dtype, const void* k, cons
         }
         return kush_check_launch("kush_write");
     });
+}
+
+// The reference's argument lists exactly (rot = 0): a binding written from the reference's launch
+// arguments works by position.
+extern "C" int kush_append(int head_dim, int bits, int dtype, const void* k, const void* v, int64_t k_stride,
+                           int64_t v_stride, int32_t* seq_lens, int32_t pos_offset, int32_t advance,
+                           const int32_t* tail_idx, void* cache, int64_t block_stride, int64_t head_stride,
+                           void* tail_k, const int32_t* block_table, int64_t bt_stride, int32_t hkv, int32_t n_seqs,
+                           void* stream) {
+    return kush_append_ex(head_dim, bits, dtype, k, v, k_stride, v_stride, seq_lens, pos_offset, advance, tail_idx,
+                          cache, block_stride, head_stride, tail_k, block_table, bt_stride, hkv, n_seqs, stream, 0);
+}
+
+extern "C" int kush_write(int head_dim, int bits, int dtype, const void* k, const void* v, int64_t k_stride,
+                          int64_t v_stride, const int32_t* query_start_loc, const int32_t* seq_lens,
+                          const int32_t* tail_idx, const int32_t* job_seq, const int32_t* job_page, int32_t n_jobs,
+                          int32_t mode, void* cache, int64_t block_stride, int64_t head_stride, void* tail_k,
+                          const int32_t* block_table, int64_t bt_stride, int32_t hkv, void* stream) {
+    return kush_write_ex(head_dim, bits, dtype, k, v, k_stride, v_stride, query_start_loc, seq_lens, tail_idx, job_seq,
+                         job_page, n_jobs, mode, cache, block_stride, head_stride, tail_k, block_table, bt_stride, hkv,
+                         stream, 0);
 }

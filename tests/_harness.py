@@ -73,8 +73,38 @@ def half_ulp(x: float, dtype: torch.dtype) -> float:
     return math.ldexp(1.0, e - p)
 
 
-def out_tol(ref: torch.Tensor, dtype: torch.dtype, base: float = 2e-3) -> float:
-    """Max-abs tolerance of a decode output in `dtype` against an fp32 reference: `base` plus half an
-    ulp of the output dtype at the largest |ref| (the rounding of the output itself; no element of
-    smaller magnitude rounds further)."""
-    return base + half_ulp(float(ref.abs().max()), dtype)
+MANTISSA = {torch.float32: 24, torch.float16: 11, torch.bfloat16: 8}
+
+
+def half_ulp_of(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Elementwise half an ulp of `dtype` at magnitude |x|: 2^(e - p) for |x| in [2^e, 2^(e+1)) and p
+    significant bits (0 at x = 0)."""
+    m, e = torch.frexp(x.double().abs())                   # |x| = m 2^e, m in [0.5, 1)
+    return torch.where(m > 0, torch.ldexp(torch.ones_like(m), e - 1 - MANTISSA[dtype]), torch.zeros_like(m))
+
+
+def out_bound(ref: torch.Tensor, dtype: torch.dtype, base: float = 2e-3, roundings: int = 1) -> torch.Tensor:
+    """Per-element bound on |out_i - ref_i| for a decode output in `dtype` against an fp32 (or wider)
+    reference: `base` (the acceptance bound of the compressed-KV decode: 2e-3 max-abs, fp32
+    accumulation) plus, per rounding of the result to `dtype`, half an ulp at |ref_i| + base -- the
+    largest magnitude the unrounded result can have, so the ulp is never taken from a smaller binade
+    than the one the kernel rounded in. A small output gets the small rounding of its own size, not the
+    rounding of the batch's largest value."""
+    return base + roundings * half_ulp_of(ref.double().abs() + base, dtype)
+
+
+def assert_out_close(out: torch.Tensor, ref: torch.Tensor, dtype: torch.dtype, base: float = 2e-3,
+                     roundings: int = 1, what: str = "") -> float:
+    """Assert |out_i - ref_i| <= out_bound(ref)_i for every element; returns the max-abs error. The
+    message names the worst element against its own bound."""
+    out, ref = out.detach().double().cpu(), ref.detach().double().cpu()
+    assert out.shape == ref.shape, (what, tuple(out.shape), tuple(ref.shape))
+    err = (out - ref).abs()
+    bound = out_bound(ref, dtype, base, roundings)
+    excess = err - bound
+    if bool((excess > 0).any()) or bool(torch.isnan(out).any()):
+        i = int(torch.nan_to_num(excess, nan=float("inf")).flatten().argmax())
+        raise AssertionError(f"{what}: element {i} out {out.flatten()[i].item():.6g} ref {ref.flatten()[i].item():.6g} "
+                             f"err {err.flatten()[i].item():.3e} > bound {bound.flatten()[i].item():.3e} "
+                             f"({int((excess > 0).sum())} elements over; max-abs {err.max().item():.3e})")
+    return err.max().item()

@@ -22,21 +22,62 @@ def lib():
     return _lib.lib()
 
 
-def header_functions() -> dict[str, int]:
-    """name -> parameter count of every function declared in the header."""
+def header_params() -> dict[str, list[str]]:
+    """name -> parameter declarations (type and name) of every function declared in the header."""
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
     out = {}
     for m in re.finditer(r"\b(?:int|const char\s*\*)\s*(kush_\w+)\s*\(([^)]*)\)\s*;", text):
         params = m.group(2).strip()
-        out[m.group(1)] = 0 if params in ("", "void") else len(params.split(","))
+        out[m.group(1)] = [] if params in ("", "void") else [" ".join(x.split()) for x in params.split(",")]
     return out
+
+
+def header_functions() -> dict[str, int]:
+    """name -> parameter count of every function declared in the header."""
+    return {k: len(v) for k, v in header_params().items()}
 
 
 def test_header_declares_the_entry_points():
     fns = header_functions()
-    assert set(fns) == {"kush_append", "kush_write", "kush_decode", "kush_append_decode", "kush_combine", "kush_fwht",
-                        "kush_unpack", "kush_last_error",
-                        "kush_abi_version"}
+    assert set(fns) == {"kush_append", "kush_append_ex", "kush_write", "kush_write_ex", "kush_decode",
+                        "kush_decode_ex", "kush_append_decode", "kush_combine", "kush_combine_ex", "kush_fwht",
+                        "kush_unpack", "kush_last_error", "kush_abi_version"}
+
+
+# The reference's launch argument sets (restated from _cpu.py:12-19 and the
+# kernels' parameter lists, gpu.mojo:207-212, :241-246, :566-572, :469-471), by parameter meaning.
+REFERENCE_ARGS = {
+    "kush_append": ["head_dim", "bits", "dtype", "k", "v", "k_row_stride", "v_row_stride", "seq_lens", "pos_offset",
+                    "advance", "tail_idx", "cache", "block_stride", "head_stride", "tail_k", "block_table",
+                    "bt_row_stride", "hkv", "n_seqs", "stream"],
+    "kush_write": ["head_dim", "bits", "dtype", "k", "v", "k_row_stride", "v_row_stride", "query_start_loc",
+                   "seq_lens", "tail_idx", "job_seq", "job_page", "n_jobs", "mode", "cache", "block_stride",
+                   "head_stride", "tail_k", "block_table", "bt_row_stride", "hkv", "stream"],
+    "kush_decode": ["head_dim", "bits", "group", "dtype", "q", "out", "cache", "block_stride", "head_stride", "tail_k",
+                    "tail_idx", "block_table", "seq_lens", "bt_row_stride", "hkv", "scale", "n_splits", "part_ml",
+                    "part_o", "n_seqs", "stream"],
+    "kush_combine": ["head_dim", "group", "dtype", "out", "part_ml", "part_o", "n_splits", "hkv", "n_seqs", "stream"],
+}
+
+
+def _names(params: list[str]) -> list[str]:
+    return [re.sub(r"[^\w]", "", p.split()[-1].lstrip("*")) for p in params]
+
+
+@pytest.mark.parametrize("name", sorted(REFERENCE_ARGS))
+def test_entry_points_take_the_reference_argument_lists(name):
+    """Each replacing entry point takes exactly the reference's argument list, in its order (a binding
+    written from the reference's launch arguments works by position); its `_ex` variant is that list
+    followed by this library's extensions, after the stream, never inserted mid-list."""
+    params = header_params()
+    assert _names(params[name]) == REFERENCE_ARGS[name]
+    ext = params[name + "_ex"]
+    assert ext[:len(params[name])] == params[name]
+    assert len(ext) > len(params[name])
+    if name == "kush_decode":                  # the fused append + decode starts with the decode list too
+        fused = params["kush_append_decode"]   # (it writes the cache and tail: those lose their const)
+        assert _names(fused[:len(params[name])]) == REFERENCE_ARGS[name]
+        assert fused[-5:] == ext[-5:]
 
 
 def test_library_exports_every_header_symbol(lib):
@@ -54,8 +95,8 @@ def test_abi_version(lib):
 
 def _decode_args(**kw):
     a = dict(head_dim=128, bits=4, group=7, dtype=2, q=None, out=None, cache=None, bs=0, hs=0, tail_k=None,
-             tail_idx=None, bt=None, seq_lens=None, bt_stride=0, bt_cols=0, hkv=4, scale=1.0, n_splits=1, part_ml=None,
-             part_o=None, sync=None, waves=0, seq_order=None, n_seqs=1, rot=0, stream=None)
+             tail_idx=None, bt=None, seq_lens=None, bt_stride=0, hkv=4, scale=1.0, n_splits=1, part_ml=None,
+             part_o=None, n_seqs=1, stream=None, bt_cols=0, sync=None, waves=0, seq_order=None, rot=0)
     a.update(kw)
     return list(a.values())
 
@@ -72,29 +113,35 @@ def _decode_args(**kw):
     (dict(rot=2), -2, "rot"),
 ])
 def test_decode_rejects_bad_arguments(lib, kw, code, msg):
-    assert lib.kush_decode(*_decode_args(**kw)) == code
+    assert lib.kush_decode_ex(*_decode_args(**kw)) == code
     assert msg in lib.kush_last_error().decode()
+    if not {"waves", "rot"} & set(kw):         # the reference-list entry point checks the same arguments
+        assert lib.kush_decode(*_decode_args(**kw)[:21]) == code
+        assert msg in lib.kush_last_error().decode()
 
 
 def test_error_codes_map_to_reference_exceptions(lib):
     with pytest.raises(ValueError, match="unsupported head_dim"):
-        _lib.call("kush_decode", *_decode_args(head_dim=96))
-    with pytest.raises(RuntimeError, match="kush_decode failed \\(-2\\)"):
-        _lib.call("kush_decode", *_decode_args(n_seqs=-1))
+        _lib.call("kush_decode", *_decode_args(head_dim=96)[:21])
+    with pytest.raises(RuntimeError, match="kush_decode_ex failed \\(-2\\)"):
+        _lib.call("kush_decode_ex", *_decode_args(n_seqs=-1))
 
 
 def test_combine_and_writes_reject_bad_arguments(lib):
-    assert lib.kush_combine(128, 7, 2, None, None, None, 0, 4, 1, 0, None) == -2
-    assert lib.kush_combine(96, 7, 2, None, None, None, 2, 4, 1, 0, None) == -1
-    assert lib.kush_combine(128, 7, 2, None, None, None, 2, 4, 1, 2, None) == -2           # rot is 0 or 1
-    assert lib.kush_append(96, 4, 2, None, None, 0, 0, None, 0, 0, None, None, 0, 0, None, None, 0, 4, 1, 0,
-                           None) == -1
-    assert lib.kush_append(128, 4, 2, None, None, 0, 0, None, 0, 0, None, None, 0, 0, None, None, 0, 4, 1, 3,
-                           None) == -2
-    assert lib.kush_write(128, 5, 2, None, None, 0, 0, None, None, None, None, None, 1, 0, None, 0, 0, None, None,
-                          0, 4, 0, None) == -1
-    assert lib.kush_write(128, 4, 2, None, None, 0, 0, None, None, None, None, None, 1, 0, None, 0, 0, None, None,
-                          0, 4, -1, None) == -2
+    assert lib.kush_combine(128, 7, 2, None, None, None, 0, 4, 1, None) == -2
+    assert lib.kush_combine(96, 7, 2, None, None, None, 2, 4, 1, None) == -1
+    assert lib.kush_combine_ex(128, 7, 2, None, None, None, 2, 4, 1, None, 2) == -2         # rot is 0 or 1
+    app = [96, 4, 2, None, None, 0, 0, None, 0, 0, None, None, 0, 0, None, None, 0, 4, 1, None]
+    assert lib.kush_append(*app) == -1
+    assert lib.kush_append_ex(*app, 0) == -1
+    app[0] = 128
+    assert lib.kush_append_ex(*app, 3) == -2
+    wr = [128, 5, 2, None, None, 0, 0, None, None, None, None, None, 1, 0, None, 0, 0, None, None, 0, 4, None]
+    assert lib.kush_write(*wr) == -1
+    wr[1] = 4
+    assert lib.kush_write_ex(*wr, -1) == -2
+    wr[13] = 3
+    assert lib.kush_write(*wr) == -2                                                     # mode 0, 1 or 2
 
 
 def test_ops_is_gpu_only():

@@ -16,7 +16,7 @@ import torch
 import torch.nn.functional as F
 
 import bench
-from _harness import out_tol
+from _harness import assert_out_close
 from kushkash_amd._ops import PAGE, cached_kv
 
 pytestmark = pytest.mark.gpu
@@ -30,9 +30,7 @@ def reference(q, cache, table, n, tail_k, D, bits):
 
 
 def check(out, ref, what):
-    err = (out.float() - ref).abs().max().item()
-    tol = out_tol(ref, torch.bfloat16)
-    assert err <= tol, f"{what}: max-abs {err:.3e} > {tol:.3e}"
+    assert_out_close(out, ref, torch.bfloat16, what=what)
 
 
 def test_c2_full_size():

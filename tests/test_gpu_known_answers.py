@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import kushkash_amd as kk
-from _harness import out_tol
+from _harness import assert_out_close
 
 pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).resolve().parent / "golden" / "known_answers.npz"
@@ -54,7 +54,7 @@ def test_gpu_exact_records_and_decode(golden, D, bits, appends):
         # max-abs 2e-3 at unit output scale; these constructed V reach |485|, where the bound is
         # relative: 2e-3 * max(1, max |ref|) (fp16 weights carry 2^-11 relative rounding)
         scale = max(1.0, float(np.abs(ref).max()))
-        assert np.abs(out - ref).max() <= out_tol(torch.from_numpy(ref), torch.float32, base=2e-3 * scale)
+        assert_out_close(torch.from_numpy(out), torch.from_numpy(ref), torch.float32, base=2e-3 * scale)
 
 
 @pytest.mark.parametrize("case,bits", [("ties", 4), ("const", 4), ("const", 8), ("clamp", 4)])

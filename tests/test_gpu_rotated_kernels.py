@@ -16,7 +16,7 @@ import torch
 import torch.nn.functional as F
 
 import kushkash_amd as kk
-from _harness import half_ulp, out_tol
+from _harness import assert_out_close, half_ulp, out_bound
 from kushkash_amd._ops import PAGE
 from oracle.cpu_ops import OracleOps
 
@@ -122,7 +122,7 @@ def test_rotated_decode_matches_oracle(D, bits, G, dtype, ns, waves, fused_merge
     want = _oracle_rotated_decode(cache, bt, seq_lens, tail_idx, tail_k, q_rot, D, bits, G, D ** -0.5)
     got = out.float().cpu()
     assert torch.equal(got[0], torch.zeros_like(got[0]))                       # empty sequence
-    assert (got - want).abs().max().item() <= out_tol(want, dtype)
+    assert_out_close(got, want, dtype)
     assert int(ops._sync.abs().sum()) == 0
 
 
@@ -146,8 +146,11 @@ def test_kushcache_rotate_in_kernels(bits, dtype):
     out = c.attend(0, q).float()
     ref = F.scaled_dot_product_attention(q[:, :, None].float(), hk.float().repeat_interleave(Hq // Hkv, 1),
                                          hv.float().repeat_interleave(Hq // Hkv, 1), scale=c.scale)[:, :, 0]
-    # q is rotated and rounded to dtype in the kernel; dequantize() rounds its rotation back to dtype
-    assert (out - ref).abs().max().item() <= 2e-3 + 3 * half_ulp(float(ref.abs().max()), dtype) + 2e-3
+    # q is rotated and rounded to dtype in the kernel, and dequantize() rounds its rotation of the
+    # cache back to dtype: errors spread over every dim by a rotation (at the largest |ref|, plus the
+    # keys' rounding as a second 2e-3), then the output's one rounding per element
+    bound = out_bound(ref, dtype, base=4e-3) + 2 * half_ulp(float(ref.abs().max()), dtype)
+    assert bool(((out - ref).abs() <= bound).all()), (out - ref).abs().max().item()
     qc = torch.randn(B, Hq, T, D, generator=g).to(dtype).to(DEV)
     kc = torch.randn(B, Hkv, T, D, generator=g).to(dtype).to(DEV)
     vc = torch.randn(B, Hkv, T, D, generator=g).to(dtype).to(DEV)
