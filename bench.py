@@ -72,6 +72,8 @@ def parse_args(argv=None):
     ap.add_argument("--dim", type=int, default=128)
     ap.add_argument("--bits", type=int, default=4)
     ap.add_argument("--pools", type=int, default=4, help="independent KV pools rotated across steps")
+    ap.add_argument("--dtype", default="bf16", choices=("bf16", "fp16", "fp32"),
+                    help="dtype of q, K, V and the output (the headline line is bf16)")
     ap.add_argument("--splits", type=int, default=0, help="split-K factor (0: Ops.splits policy)")
     ap.add_argument("--waves", type=int, default=0, help="waves per decode workgroup (0: Ops.waves policy)")
     ap.add_argument("--sweep", default="", help="comma list of splits:waves to time (extra lines on stderr)")
@@ -99,7 +101,7 @@ def make_workload(a, dev):
     import kushkash_amd as kk
     from kushkash_amd._ops import Ops, record_bytes
     B, N, Hkv, G, D, bits = a.batch, a.ctx, a.hkv, a.hq // a.hkv, a.dim, a.bits
-    dtype = torch.bfloat16
+    dtype = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[a.dtype]
     pages = -(-N // PAGE)
     RB = record_bytes(D, bits)
     ops = Ops(torch.device(dev), D, bits, G, dtype)
