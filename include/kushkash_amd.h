@@ -144,6 +144,20 @@ int kush_append_decode(int head_dim, int bits, int group, int dtype, const void*
                        const void* k, const void* v, int64_t k_row_stride, int64_t v_row_stride, int32_t bt_cols,
                        int32_t* split_sync, int32_t waves, const int32_t* seq_order, int32_t rot);
 
+/* kush_decode_ex without caller buffers: the split-K merge counters and partials live in a static
+ * device array of the library (64 MiB per device, held until the process ends; its counters are
+ * cleared once, by a fill kernel on `stream`, at the first call on each device). n_splits > 1 needs
+ * n_seqs*hkv*ceil(group/16) <= 65536 counters and 262144 + 4*(head_dim+2)*n_seqs*hkv*n_splits*group
+ * bytes <= 64 MiB (otherwise -2: use kush_decode_ex); the splits are always merged in the launch.
+ * Calls share the array and must not overlap on one device; for graph capture, make the first call
+ * on a device outside the capture. No counterpart in the reference: for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). */
+int kush_decode_noalloc(int head_dim, int bits, int group, int dtype, const void* q, void* out, const void* cache,
+                        int64_t block_stride, int64_t head_stride, const void* tail_k, const int32_t* tail_idx,
+                        const int32_t* block_table, const int32_t* seq_lens, int64_t bt_row_stride, int32_t hkv,
+                        float scale, int32_t n_splits, int32_t n_seqs, void* stream, int32_t bt_cols, int32_t waves,
+                        const int32_t* seq_order, int32_t rot);
+
 /* Walsh-Hadamard rotation of rows of head_dim elements: y[r] = fwht(x[r]) for r < rows (row strides
  * in elements; y may alias x), in the canonical order — butterflies at strides 1, 2, ..., D/2, then
  * one fp32 multiply by 1/sqrt(D), rounded once to dtype — bit-identical to the reference's CPU

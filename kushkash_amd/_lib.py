@@ -43,6 +43,8 @@ SIGNATURES = {
     "kush_decode_ex": _DECODE + _DECODE_EXT,
     # + k, v, k_row_stride, v_row_stride, then the decode extensions
     "kush_append_decode": _DECODE + [_P, _P, _I64, _I64] + _DECODE_EXT,
+    # the decode list without part_ml / part_o, then bt_cols, waves, seq_order, rot (no split_sync)
+    "kush_decode_noalloc": _DECODE[:17] + [_I32, _P, _I32, _I32, _P, _I32],
     "kush_combine": _COMBINE,
     "kush_combine_ex": _COMBINE + [_I32],                        # + rot
     # head_dim, dtype, x, y, x_row_stride, y_row_stride, rows, stream

@@ -1,6 +1,8 @@
 // C entry points of the fused dequant decode attention (kush_decode), the same launch with the
 // step's token appended first (kush_append_decode) and the split-K combine (kush_combine); the
 // kernels and their launch are in kush_decode.h (contract and design notes there).
+#include <mutex>
+
 #include "kush_decode.h"
 
 using namespace kush;
@@ -130,4 +132,88 @@ extern "C" int kush_combine_ex(int head_dim, int group, int dtype, void* out, co
 extern "C" int kush_combine(int head_dim, int group, int dtype, void* out, const float* part_ml, const float* part_o,
                             int32_t n_splits, int32_t hkv, int32_t n_seqs, void* stream) {
     return kush_combine_ex(head_dim, group, dtype, out, part_ml, part_o, n_splits, hkv, n_seqs, stream, 0);
+}
+
+// ------------------------------------------------------------------ allocation-free decode
+// kush_decode_noalloc: kush_decode_ex whose split-K scratch -- the merge counters, then the partials
+// (part_ml, part_o) -- lives in this file-scope device array instead of caller buffers, for callers
+// that cannot allocate (code under HIP graph capture, tight serving loops). Each device holds its
+// own copy for the life of the process; its address is looked up once per device
+// (hipGetSymbolAddress) and only that address is handed to the kernels. The counters must start at
+// zero: a fill kernel clears them at that set-up, and the in-launch merge leaves them zero after
+// every call. Calls that overlap on one device share the array and race.
+namespace {
+
+constexpr size_t SCRATCH_BYTES = size_t(64) << 20;          // per device
+constexpr size_t SCRATCH_SYNC = 1 << 16;                   // int32 merge counters at the front
+constexpr size_t SCRATCH_PART0 = SCRATCH_SYNC * sizeof(int32_t);
+static_assert(SCRATCH_PART0 % 256 == 0, "the partials start aligned");
+
+static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
+
+__global__ __launch_bounds__(256) void zero_words(int32_t* p, int n) {
+    const int i = (int)(blockIdx.x * 256 + threadIdx.x);
+    if (i < n) p[i] = 0;
+}
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch[MAX_DEVICES] = {};
+
+// The device address of `scratch` on the current device (set up on the first call there); nullptr
+// after a failure, which is then reported through kush_fail.
+uint8_t* scratch_on_device(hipStream_t stream) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
+        kush_fail(-3, "kush_decode_noalloc: no current device (or device %d beyond %d)", dev, MAX_DEVICES);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[dev] == nullptr) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || ptr == nullptr) {
+            kush_fail(-3, "kush_decode_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                      hipGetErrorString(e));
+            return nullptr;
+        }
+        zero_words<<<dim3((unsigned)((SCRATCH_SYNC + 255) / 256)), dim3(256), 0, stream>>>((int32_t*)ptr,
+                                                                                           (int)SCRATCH_SYNC);
+        if (kush_check_launch("kush_decode_noalloc (scratch set-up)") != 0) return nullptr;
+        g_scratch[dev] = (uint8_t*)ptr;
+    }
+    return g_scratch[dev];
+}
+
+}  // namespace
+
+extern "C" int kush_decode_noalloc(int head_dim, int bits, int group, int dtype, const void* q, void* out,
+                                   const void* cache, int64_t block_stride, int64_t head_stride, const void* tail_k,
+                                   const int32_t* tail_idx, const int32_t* block_table, const int32_t* seq_lens,
+                                   int64_t bt_stride, int32_t hkv, float scale, int32_t n_splits, int32_t n_seqs,
+                                   void* stream, int32_t bt_cols, int32_t waves, const int32_t* seq_order,
+                                   int32_t rot) {
+    float* part_ml = nullptr;
+    float* part_o = nullptr;
+    int32_t* sync = nullptr;
+    if (n_splits > 1 && n_seqs > 0 && hkv > 0 && group > 0) {
+        const int64_t rows = (int64_t)n_seqs * hkv * n_splits * group;
+        const int64_t counters = (int64_t)n_seqs * hkv * ((group + 15) / 16);
+        const int64_t need = (int64_t)SCRATCH_PART0 + rows * (2 + (int64_t)head_dim) * (int64_t)sizeof(float);
+        if (counters > (int64_t)SCRATCH_SYNC || need > (int64_t)SCRATCH_BYTES)
+            return kush_fail(-2,
+                             "kush_decode_noalloc: %d splits of %d sequences x %d kv heads x %d q heads need %lld "
+                             "bytes of scratch (%lld merge counters); the maximum is %zu bytes (%zu counters): "
+                             "use kush_decode_ex with caller-owned buffers",
+                             n_splits, n_seqs, hkv, group, (long long)need, (long long)counters, SCRATCH_BYTES,
+                             SCRATCH_SYNC);
+        uint8_t* base = scratch_on_device((hipStream_t)stream);
+        if (base == nullptr) return -3;
+        sync = (int32_t*)base;
+        part_ml = (float*)(base + SCRATCH_PART0);
+        part_o = part_ml + 2 * rows;
+    }
+    return decode_impl("kush_decode_noalloc", head_dim, bits, group, dtype, q, out, cache, block_stride, head_stride,
+                       tail_k, tail_idx, block_table, seq_lens, bt_stride, bt_cols, hkv, scale, n_splits, part_ml,
+                       part_o, sync, waves, seq_order, n_seqs, rot, Append{}, stream);
 }

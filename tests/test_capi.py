@@ -40,8 +40,8 @@ def header_functions() -> dict[str, int]:
 def test_header_declares_the_entry_points():
     fns = header_functions()
     assert set(fns) == {"kush_append", "kush_append_ex", "kush_write", "kush_write_ex", "kush_decode",
-                        "kush_decode_ex", "kush_append_decode", "kush_combine", "kush_combine_ex", "kush_fwht",
-                        "kush_unpack", "kush_last_error", "kush_abi_version"}
+                        "kush_decode_ex", "kush_append_decode", "kush_decode_noalloc", "kush_combine",
+                        "kush_combine_ex", "kush_fwht", "kush_unpack", "kush_last_error", "kush_abi_version"}
 
 
 # The reference's launch argument sets (restated from _cpu.py:12-19 and the
