@@ -26,6 +26,9 @@ its mean duration, from HIP events around the graph of decode kernels) and
 
 --config selects the other measured configurations of the path (each prints its own JSON line; the
 default, c2, is the headline):
+  c1        the reference's CPU-runnable case through the KushCache API (batch 1, 8 q / 2 kv heads, D 128,
+            512 tokens, int4, rotation on): pack + one decode, on the GPU, with the oracle behind the same
+            API on the host cores as the CPU baseline
   c3        Llama-3.1-8B decode step, 32 q / 8 kv heads, D 128, int8, batch 128 with ragged contexts
             N_i ~ U[256, 8192] (seed 0): append of one token per sequence (pos_offset -1, the vLLM
             convention) and decode over N_i + 1 tokens, in one launch (--two-launch: append, then decode)
@@ -76,7 +79,8 @@ def parse_args(argv=None):
                     help="dtype of q, K, V and the output (the headline line is bf16)")
     ap.add_argument("--splits", type=int, default=0, help="split-K factor (0: Ops.splits policy)")
     ap.add_argument("--waves", type=int, default=0, help="waves per decode workgroup (0: Ops.waves policy)")
-    ap.add_argument("--sweep", default="", help="comma list of splits:waves to time (extra lines on stderr)")
+    ap.add_argument("--sweep", default="", help="c2: comma list of splits:waves, c4: comma list of splits, "
+                                                "each timed and printed as a JSON line of its own after the main one")
     ap.add_argument("--sequential", action="store_true", help="pages in order instead of a random permutation")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline")
@@ -89,7 +93,7 @@ def parse_args(argv=None):
     ap.add_argument("--two-launch", action="store_true",
                     help="c4-write: the reference's two launches (mode 0, mode 1); c3: append, then decode, "
                          "instead of one fused launch")
-    ap.add_argument("--config", default="c2", choices=("c2", "c3", "c4", "c4-write", "c4-unpack", "c4-fwht"),
+    ap.add_argument("--config", default="c2", choices=("c1", "c2", "c3", "c4", "c4-write", "c4-unpack", "c4-fwht"),
                     help="which configuration to measure (c2: the headline line)")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "decode_c2_traffic.md"),
                     help="rocprofv3 counter summary whose 'traffic_bytes_per_launch' fills roofline.traffic")
@@ -203,7 +207,7 @@ def _timed_replay(g, gw, steps: int) -> float:
 def cpu_baseline(w, budget_s: float):
     """The oracle's decode (C restatement of the reference CPU path, fp32, one task per (sequence,
     kv head)) on the host cores, over a bounded sample of the same workload: the first S_cpu
-    sequences of pool 0 (records copied to host memory). Median of runs after one warm-up."""
+    sequences of pool 0 (records copied to host memory). Median of up to 20 runs after 3 warm-ups."""
     from oracle import cpu_ops
     B, Hkv, G, D = w["B"], w["Hkv"], w["G"], w["D"]
     ncores = len(os.sched_getaffinity(0))
@@ -230,7 +234,8 @@ def cpu_baseline(w, budget_s: float):
     t1 = run(min(S, max(1, ncores)))
     per_seq = t1 / min(S, max(1, ncores))
     n = int(min(S, max(1, budget_s / 4 / max(per_seq, 1e-6))))
-    run(n)                                                       # warm-up
+    for _ in range(3):                                           # warm-ups
+        run(n)
     reps = max(1, min(20, int(budget_s / max(per_seq * n, 1e-6))))
     times = sorted(run(n) for _ in range(reps))
     med = times[len(times) // 2]
@@ -249,24 +254,60 @@ def cpu_baseline(w, budget_s: float):
         pass
     return {"value": round(bytes_ / med / 1e9, 3), "unit": "GB/s", "cores": ncores, "kind": "port",
             "sample": f"{n} of {S} sequences of the same C2 workload (all {Hkv} kv heads, {w['N']} tokens each), "
-                      f"median of {reps} runs after 1 warm-up; {med * 1e6 / n:.0f} us per sequence on {ncores} "
+                      f"median of {reps} runs after 3 warm-ups; {med * 1e6 / n:.0f} us per sequence on {ncores} "
                       f"threads, {t_one * 1e6:.0f} us per sequence on 1 thread; host CPU: {cpu_model}",
             "us_per_step_extrapolated": round(med / frac * 1e6, 1)}
 
 
-def measured_traffic(path: str, workload: str):
-    """HBM bytes per launch of a configuration's main kernel from a committed counter summary (FETCH_SIZE + WRITE_SIZE of the
-    same workload, each scaled by the copy-kernel calibration), or None."""
+_IN = {torch.float32: "float", torch.float16: "_Float16", torch.bfloat16: "kush::bf16_t"}
+
+
+def _b(x) -> str:
+    return "true" if x else "false"
+
+
+def decode_kernel_name(D: int, bits: int, dtype, waves: int, G: int, rot: bool) -> str:
+    """The instantiation kush_decode launches, as rocprofv3 names it: the requested waves unless the
+    configuration's page ring does not fit in LDS (4 KB of block ids + 4 slots per wave of one record
+    each, within 160 KiB), two page streams when G <= 8."""
+    from kushkash_amd._ops import record_bytes
+    nw = waves or 8
+    while nw > 2 and 4 * nw * record_bytes(D, bits) + 4 * 1024 + 16 > 160 * 1024:
+        nw //= 2
+    return f"kush::decode_kernel<{D}, {bits}, {_IN[dtype]}, {nw}, {2 if G <= 8 else 1}, {_b(rot)}>"
+
+
+# the translation unit of each kernel family (its digest covers the unit and its headers)
+UNIT = {"decode_kernel": "kush_decode_inst.hip", "write_kernel": "kush_write.hip", "append_kernel": "kush_write.hip",
+        "unpack_kernel": "kush_unpack.hip", "fwht_kernel": "kush_rotate.hip"}
+
+
+def source_digest(kernel: str) -> str | None:
+    """Digest of the sources the loaded library built `kernel` from (kushkash_amd.build: its
+    translation unit and that unit's headers)."""
+    import importlib
+    import re
+    kbuild = importlib.import_module("kushkash_amd.build")       # the module (the package exports a build())
+    unit = UNIT[re.search(r"kush::(\w+)<", kernel).group(1)]
+    return kbuild.built_digest(unit) or kbuild.source_digest(unit)
+
+
+def measured_traffic(path: str, workload: str, kernel: str):
+    """HBM bytes per launch of a configuration's main kernel from a committed counter summary
+    (FETCH_SIZE + WRITE_SIZE of the same workload, each scaled by the copy-kernel calibration), or
+    None. The summary must name the same workload, the same kernel instantiation and the same
+    source digest as this run's library: bytes counted on another build are never reported."""
     try:
         text = Path(path).read_text()
     except OSError:
         return None
     import re
-    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", text, re.M)
-    w = re.search(r"^workload:\s*(.+)$", text, re.M)
-    if not m or not w or w.group(1).strip() != workload:
+    fields = {k: v.strip() for k, v in re.findall(r"^(workload|kernel|sources|traffic_bytes_per_launch):\s*(.+)$",
+                                                   text, re.M)}
+    if (fields.get("workload") != workload or fields.get("kernel") != kernel
+            or fields.get("sources") != source_digest(kernel) or "traffic_bytes_per_launch" not in fields):
         return None
-    return int(m.group(1))
+    return int(fields["traffic_bytes_per_launch"])
 
 
 def copy_calibration(a) -> None:
@@ -349,18 +390,99 @@ def ragged_cache(ops, lens, room: int, Hkv: int, bias_sigma: float, bias_frac: f
     return cache, table, tail_k, tail_idx
 
 
-def _line(metric, us, alg, config, kernels, extra=None, traffic_md=None):
+def _line(metric, us, alg, config, kernel, extra=None, traffic_md=None):
+    """One JSON line for a configuration; `kernel` is the main kernel's instantiation (rocprofv3's name)."""
     gbs = alg / (us * 1e-6) / 1e9
-    traffic = measured_traffic(str(ROOT / "profiles" / traffic_md), config["workload"]) if traffic_md else None
+    traffic = measured_traffic(str(ROOT / "profiles" / traffic_md), config["workload"], kernel) if traffic_md else None
     res = {"metric": metric, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "us_per_step": round(us, 2),
            "pct_peak_hbm": round(100 * gbs / PEAK_HBM_GBS, 1), "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "data": "synthetic (seeded, generated on the GPU)", "config": config,
            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                        "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic, "kernel": kernels,
-                        "algorithmic_bytes": int(alg)}}
+                        "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic, "kernel": kernel,
+                        "sources": source_digest(kernel), "algorithmic_bytes": int(alg)}}
     if extra:
         res.update(extra)
     print(json.dumps(res), flush=True)
+
+
+def bench_c1(a) -> None:
+    """C1, the reference's CPU-runnable case, through the KushCache API: batch 1, 8 q / 2 kv heads,
+    D 128, page 32, a 512-token context, int4 (rotation on: the default for 4-bit), bf16 K, V, q ~
+    N(0,1) from seed 0 (CPU generator, in that order). One step = pack the context (write) + one decode
+    step (attend) on a reset cache. The GPU line runs the product; the CPU baseline runs the same API
+    calls on the oracle (the C restatement of the reference's CPU path, fp32, as the reference's CPU
+    cache converts its inputs) on the host cores, all threads and one. Each side: median wall time of
+    20 steps after 3 warm-ups, synchronized around each step."""
+    import kushkash_amd as kk
+    from kushkash_amd import cache as cache_mod
+    from kushkash_amd._ops import record_bytes
+    from oracle import cpu_ops
+    B, Hq, Hkv, D, N, bits = 1, 8, 2, 128, 512, 4
+    g = torch.Generator().manual_seed(0)
+    K = torch.randn(B, Hkv, N, D, generator=g).to(torch.bfloat16)
+    V = torch.randn(B, Hkv, N, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(B, Hq, D, generator=g).to(torch.bfloat16)
+
+    def timed(step, sync):
+        for _ in range(3):
+            step()
+        times = []
+        for _ in range(20):
+            sync()
+            t0 = time.perf_counter()
+            step()
+            sync()
+            times.append(time.perf_counter() - t0)
+        return sorted(times)[len(times) // 2]
+
+    gpu = kk.KushCache(1, Hkv, Hq, D, batch_size=B, bits=bits, device="cuda", dtype=torch.bfloat16)
+    Kd, Vd, qd = K.cuda(), V.cuda(), q.cuda()
+
+    def gpu_step():
+        gpu.reset()
+        gpu.write(0, Kd, Vd)
+        gpu.attend(0, qd)
+
+    t_gpu = timed(gpu_step, torch.cuda.synchronize)
+    real = cache_mod.Ops
+    cache_mod.Ops = cpu_ops.OracleOps                 # the CPU baseline leg only: the oracle behind the API
+    try:
+        cpu = kk.KushCache(1, Hkv, Hq, D, batch_size=B, bits=bits, device="cpu", dtype=torch.float32)
+    finally:
+        cache_mod.Ops = real
+    Kc, Vc, qc = K.float(), V.float(), q.float()
+
+    def cpu_step():
+        cpu.reset()
+        cpu.write(0, Kc, Vc)
+        cpu.attend(0, qc)
+
+    ncores = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        ncores = min(ncores, int(os.environ["OMP_NUM_THREADS"]))
+    cpu_ops.set_threads(ncores)
+    torch.set_num_threads(ncores)
+    t_cpu = timed(cpu_step, lambda: None)
+    cpu_ops.set_threads(1)
+    torch.set_num_threads(1)
+    t_cpu1 = timed(cpu_step, lambda: None)
+    cpu_ops.set_threads(ncores)
+    torch.set_num_threads(ncores)
+    RB = record_bytes(D, bits)
+    recs = B * Hkv * (N // PAGE) * RB
+    alg = 2 * B * Hkv * N * D * 2 + 2 * recs + 2 * B * Hq * D * 2      # K, V in; records out, read back; q, out
+    cpu_model = next((l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")), "")
+    _line("C1 pack + decode us/step (KushCache API), int4, 1 x 512 ctx", t_gpu * 1e6, alg,
+          {"workload": f"C1 KushCache API: {Hq} q / {Hkv} kv heads, D {D}, int{bits}, page 32, batch {B} x {N} "
+                       f"tokens, rotation on: write(512 tokens) + attend", "global_batch": B, "seq_len": N},
+          decode_kernel_name(D, bits, torch.bfloat16, gpu.ops.waves(B, Hkv, 1, N // PAGE), Hq // Hkv, False),
+          extra={"cpu_baseline": {"value": round(alg / t_cpu / 1e9, 4), "unit": "GB/s", "cores": ncores,
+                                  "kind": "port", "us_per_step": round(t_cpu * 1e6, 1),
+                                  "us_per_step_1_thread": round(t_cpu1 * 1e6, 1),
+                                  "sample": f"the whole C1 step (write + attend through the KushCache API on the "
+                                            f"oracle, fp32), median of 20 after 3 warm-ups, {ncores} threads and 1; "
+                                            f"host CPU: {cpu_model}"},
+                 "timing": "wall clock, eager API calls, synchronized around each step"})
 
 
 def bench_c3(a) -> None:
@@ -410,8 +532,9 @@ def bench_c3(a) -> None:
                        + (" (two launches)" if a.two_launch else " (one launch)"),
            "global_batch": B, "split_k": ns, "tokens": sum(n1), "sequence_order": "longest first",
            "waves": wv},
-          (f"append_kernel<{D},{bits},bf16> + " if a.two_launch else "fused append + ")
-          + f"decode_kernel<{D},{bits},bf16,{wv}>")
+          decode_kernel_name(D, bits, dtype, wv, G, False), traffic_md="decode_c3_traffic.md",
+          extra={"launches": ("append_kernel, then decode_kernel" if a.two_launch
+                              else "decode_kernel with the append inside")})
 
 
 def bench_c4(a) -> None:
@@ -436,15 +559,12 @@ def bench_c4(a) -> None:
         wv = a.waves or ops.waves(B, Hkv, ns, N // PAGE)
         ms = time_graph(lambda j: ops.decode(q, out, cache, table, sl, tail_idx, tail_k, sm, ns, work, waves=wv),
                         a.steps, a.warmup)
-        if i == 0:
-            _line("decode-attn us/step + achieved HBM GB/s (% peak), int4, bs8 x 131k ctx", ms * 1e3, alg,
-                  {"workload": f"C4 Qwen3-8B layer: {Hq} q / {Hkv} kv heads, D {D}, int{bits}, page 32, "
-                               f"batch {B} x {N} tokens", "global_batch": B, "seq_len": N, "split_k": ns,
-                   "waves": wv},
-                  f"decode_kernel<{D},{bits},bf16,{wv}> (split-K merged in the launch)")
-        else:
-            print(f"C4 splits {ns:4d}: {ms * 1e3:8.2f} us/step  {alg / ms / 1e6:7.1f} GB/s "
-                  f"({100 * alg / ms / 1e6 / PEAK_HBM_GBS:5.1f}% of peak)", file=sys.stderr, flush=True)
+        _line("decode-attn us/step + achieved HBM GB/s (% peak), int4, bs8 x 131k ctx", ms * 1e3, alg,
+              {"workload": f"C4 Qwen3-8B layer: {Hq} q / {Hkv} kv heads, D {D}, int{bits}, page 32, "
+                           f"batch {B} x {N} tokens, splits {ns}, waves {wv}", "global_batch": B, "seq_len": N,
+               "split_k": ns, "waves": wv, "split_k_policy": ns == policy},
+              decode_kernel_name(D, bits, dtype, wv, G, False),
+              traffic_md="decode_c4_traffic.md", extra={"merge": "split-K partials merged inside the launch"})
 
 
 def bench_c4_write(a) -> None:
@@ -483,7 +603,8 @@ def bench_c4_write(a) -> None:
     _line("chunked-prefill write us/step + achieved HBM GB/s (% peak), int4, 8 x 2048 tokens", ms * 1e3, alg,
           {"workload": f"C4 write: {B} x {T} new tokens, {Hkv} kv heads, D {D}, int{bits} (512 page jobs x {Hkv} "
                        f"heads, {launches})", "global_batch": B, "tokens": B * T},
-          f"write_kernel<{D},{bits},bf16> ({launches})", traffic_md="write_c4_traffic.md")
+          f"kush::write_kernel<{D}, {bits}, kush::bf16_t, true, {_b(not a.two_launch)}, {_b(a.rot)}>",
+          traffic_md="write_c4_traffic.md", extra={"launches": launches})
 
 
 def bench_c4_unpack(a) -> None:
@@ -526,9 +647,7 @@ def bench_c4_unpack(a) -> None:
     _line("prefill-unpack us/step + achieved HBM GB/s (% peak), int4, 131k history + 2048 new", ms * 1e3, alg,
           {"workload": f"C4 packed-prefill unpack: 1 x ({N} history + {T} new) tokens, {Hkv} kv heads, D {D}, "
                        f"int{bits}, bf16 kp / vp, rot {int(a.rot)}", "global_batch": 1, "seq_len": rows},
-          f"unpack_kernel<{D},{bits},bf16,vec> ({pages} page items + {T // PAGE} new-row items) x {Hkv} heads, "
-          f"4 tasks per workgroup",
-          extra, traffic_md="unpack_c4_traffic.md")
+          f"kush::unpack_kernel<{D}, {bits}, kush::bf16_t, true>", extra, traffic_md="unpack_c4_traffic.md")
 
 
 def cpu_baseline_unpack(pool, blk, k_new, v_new, D, bits, Hkv, rot, budget_s: float):
@@ -553,13 +672,14 @@ def cpu_baseline_unpack(pool, blk, k_new, v_new, D, bits, Hkv, rot, budget_s: fl
 
     per_page = run(16) / 16
     n = int(min(blk_h.numel(), max(16, budget_s / 4 / max(per_page, 1e-9))))
-    run(n)
+    for _ in range(3):
+        run(n)
     reps = max(1, min(10, int(budget_s / max(per_page * n, 1e-9))))
     med = sorted(run(n) for _ in range(reps))[reps // 2]
     alg = n * Hkv * record_bytes(D, bits) + 2 * n * PAGE * Hkv * D * 4
     return {"value": round(alg / med / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"{n} of {blk_h.numel()} history pages of the same group (all {Hkv} kv heads, fp32 kp / vp, "
-                      f"rot {int(rot)}), median of {reps} runs after 1 warm-up; {med * 1e6 / n:.1f} us per page"}
+                      f"rot {int(rot)}), median of {reps} runs after 3 warm-ups; {med * 1e6 / n:.1f} us per page"}
 
 
 def bench_c4_fwht(a) -> None:
@@ -576,7 +696,7 @@ def bench_c4_fwht(a) -> None:
     alg = 2 * rows * Hkv * D * 2
     _line("fwht us/step + achieved HBM GB/s (% peak), 1,064,960 rows of D 128 bf16", ms * 1e3, alg,
           {"workload": f"C4 key rotation: {rows} tokens x {Hkv} kv heads, D {D}, bf16, in place", "rows": rows * Hkv},
-          f"fwht_kernel<{D},bf16,vec> ({D // 16} lanes per row)", traffic_md="fwht_c4_traffic.md")
+          f"kush::fwht_kernel<{D}, kush::bf16_t, true>", traffic_md="fwht_c4_traffic.md")
 
 
 def main(argv=None):
@@ -592,24 +712,20 @@ def main(argv=None):
         copy_calibration(a)
         return
     if a.config != "c2":
-        {"c3": bench_c3, "c4": bench_c4, "c4-write": bench_c4_write, "c4-unpack": bench_c4_unpack,
+        {"c1": bench_c1, "c3": bench_c3, "c4": bench_c4, "c4-write": bench_c4_write, "c4-unpack": bench_c4_unpack,
          "c4-fwht": bench_c4_fwht}[a.config](a)
         return
     w = make_workload(a, dev)
     ns = a.splits or w["ops"].splits(w["B"], w["Hkv"], w["N"] // PAGE)
     alg = algorithmic_bytes(w)
 
-    for item in [x for x in a.sweep.split(",") if x.strip()]:
-        parts = [int(v) for v in item.split(":")]
-        sns, swv = parts[0], parts[1]
-        msx = time_steps(w, sns, swv, a.steps, a.warmup)
-        print(f"splits {sns:4d} waves {swv:3d}: {msx * 1e3:8.2f} us/step  {alg / msx / 1e6:7.1f} GB/s "
-              f"({100 * alg / msx / 1e6 / PEAK_HBM_GBS:5.1f}% of peak)", file=sys.stderr, flush=True)
-
     wv = a.waves or w["ops"].waves(w["B"], w["Hkv"], ns, w["pages"])
     ms = time_steps(w, ns, wv, a.steps, a.warmup)
-    workload = (f"C2 Qwen2.5-7B decode layer: {a.hq} q / {a.hkv} kv heads, D {a.dim}, int{a.bits}, page 32, "
-                f"batch {a.batch} x {a.ctx} tokens" + (", rotation folded into the kernels" if a.rot else ""))
+    shape = (f"C2 Qwen2.5-7B decode layer: {a.hq} q / {a.hkv} kv heads, D {a.dim}, int{a.bits}, page 32, "
+             f"batch {a.batch} x {a.ctx} tokens" + (", rotation folded into the kernels" if a.rot else "")
+             + ("" if a.dtype == "bf16" else f", {a.dtype}"))
+    workload = f"{shape}, splits {ns}, waves {wv}"
+    kernel = decode_kernel_name(a.dim, a.bits, w["ops"].dtype, wv, w["G"], a.rot)
     ms_dec = ms                                   # one kernel per step: the decode kernel is the step
     gbs = alg / ms / 1e6
     gbs_dec = alg / ms_dec / 1e6
@@ -634,14 +750,22 @@ def main(argv=None):
                    "seq_len": a.ctx, "parallelism": "single GPU", "split_k": ns, "waves": wv, "pools": a.pools},
         "roofline": {"bound": "hbm", "achieved": round(gbs_dec, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs_dec / PEAK_HBM_GBS, 4),
-                     "traffic": measured_traffic(a.traffic, f"{workload}, splits {ns}, waves {wv}"),
-                     "kernel": f"decode_kernel<{a.dim},{a.bits},bf16,{wv}>", "kernel_us": round(ms_dec * 1e3, 2),
+                     "traffic": measured_traffic(a.traffic, workload, kernel),
+                     "kernel": kernel, "sources": source_digest(kernel), "step_us": round(ms_dec * 1e3, 2),
                      "algorithmic_bytes": alg},
         "cpu_baseline": None,
     }
     if not a.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(w, a.cpu_seconds)
     print(json.dumps(res), flush=True)
+
+    for item in [x for x in a.sweep.split(",") if x.strip()]:     # other launch shapes, a line each
+        sns, swv = (int(v) for v in item.split(":"))
+        msx = time_steps(w, sns, swv, a.steps, a.warmup)
+        _line(res["metric"], msx * 1e3, alg, {"workload": f"{shape}, splits {sns}, waves {swv}",
+                                              "global_batch": a.batch, "seq_len": a.ctx, "split_k": sns,
+                                              "waves": swv, "sweep": True},
+              decode_kernel_name(a.dim, a.bits, w["ops"].dtype, swv, w["G"], a.rot))
 
 
 if __name__ == "__main__":

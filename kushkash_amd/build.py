@@ -6,6 +6,7 @@ once per input dtype and rot flag), then linked into kushkash_amd/libkushhip.so.
 """
 from __future__ import annotations
 
+import hashlib
 import os
 import shutil
 import subprocess
@@ -17,6 +18,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 LIB = PKG / "libkushhip.so"
+DIGEST = PKG / "libkushhip.so.digest"          # source digest of the library last built here
 SOURCES = ("kush_capi.hip", "kush_write.hip", "kush_decode.hip", "kush_rotate.hip",
            "kush_unpack.hip", "kush_decode_inst.hip")
 # the decode kernel instantiations: one object per (input dtype, rot)
@@ -46,6 +48,49 @@ FLAGS = [
     "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wno-pass-failed",
 ]
+
+
+def _includes(path: Path, seen: set) -> None:
+    """path and the local headers it includes, transitively (csrc/ and include/)."""
+    import re
+    if path in seen or not path.exists():
+        return
+    seen.add(path)
+    for name in re.findall(r'^\s*#\s*include\s+"([^"]+)"', path.read_text(), re.M):
+        for d in (path.parent, PKG / "csrc", ROOT / "include"):
+            if (d / name).exists():
+                _includes(d / name, seen)
+                break
+
+
+def source_digest(unit: str | None = None) -> str:
+    """16 hex digits of sha256 over what decides the machine code of one translation unit (`unit`, a
+    csrc/*.hip file: it and its local headers, transitively) or of the whole library (None: every
+    source and header), plus the compiler flags and instantiation units. The same sources give the
+    same digest on every machine and rebuild, so a measurement of a kernel taken on one build can be
+    matched to the build that runs later, and stays valid while only other kernels change."""
+    h = hashlib.sha256()
+    if unit is None:
+        files = sorted((PKG / "csrc").glob("*.h")) + sorted((PKG / "csrc").glob("*.hip"))
+        files.append(ROOT / "include" / "kushkash_amd.h")
+    else:
+        seen: set = set()
+        _includes(PKG / "csrc" / unit, seen)
+        files = sorted(seen)
+    for f in files:
+        h.update(f.name.encode() + b"\0" + f.read_bytes() + b"\0")
+    h.update(repr((FLAGS, units())).encode())
+    return h.hexdigest()[:16]
+
+
+def built_digest(unit: str | None = None) -> str | None:
+    """The source digest (of `unit`, or of the whole library) recorded when LIB was built, or None if
+    LIB was not built by build()."""
+    import json
+    try:
+        return json.loads(DIGEST.read_text()).get(unit or "all")
+    except (OSError, ValueError):
+        return None
 
 
 def hipcc() -> str:
@@ -84,6 +129,8 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
         tmp = LIB.with_suffix(".so.tmp")
         _run([hipcc(), *FLAGS, "-o", str(tmp), *objs], verbose)
     os.replace(tmp, LIB)
+    import json
+    DIGEST.write_text(json.dumps({"all": source_digest(), **{u: source_digest(u) for u in SOURCES}}, indent=1) + "\n")
     return LIB
 
 

@@ -34,7 +34,10 @@
  *     over exactly dequantizable records; exp only through those tolerances.
  *   fwht: bit-exact against the canonical torch order (_ops.py:383-395), close to the dense
  *     Hadamard product (tests/test_host.py).
- *   unpack: parity unpinned (no check yet; not on the decode/write hot path).
+ *   unpack: the reference test's fp64 restatement (test_cpu.py:458-477 over _ops.py:398-436:
+ *     dequantize in fp64, round once, then the canonical rotation), records built from chosen
+ *     codes and dyadic scales with closed-form values, and rot = plain unpack then the rotation
+ *     of every history row (tests/test_unpack.py).
  */
 #include <math.h>
 #include <stdint.h>
