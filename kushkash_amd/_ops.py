@@ -3,8 +3,9 @@
 Drop-in for the reference's ``kushkash/_ops.py``: ``Ops`` keeps its constructor, method names,
 argument meaning and error behaviour (``_ops.py:42-213``), but every method runs a hand-written
 gfx950 HIP kernel through the C ABI of ``libkushhip.so`` (include/kushkash_amd.h) on torch's
-current stream. The torch helpers (record dequantization, reference attention, rotation) keep the
-reference's semantics (``_ops.py:217-522``).
+current stream. The reference's torch helpers (record dequantization, attention with log-sum-exp,
+rotation) are importable from here under their reference names; they live in _records, _attention
+and _rotation.
 
 Tensor conventions (as the reference, ``_ops.py:6-15``)
   cache       any tensor whose dim 0 is the block and dim 1 the kv head, each (block, head) record
@@ -430,244 +431,21 @@ class Ops:
                            stream, int(bool(rot)))
 
 
-# ---------------------------------------------------------------- reference / prefill helpers (pure torch)
-def _codes(c: torch.Tensor, bits: int) -> torch.Tensor:
-    """int8 code bytes [..., DC] -> codes [..., D]: int4 dims j < D/2 are the low nibbles, the rest
-    the high nibbles, both sign-extended (arithmetic shifts on int8)."""
-    return torch.cat([(c << 4) >> 4, c >> 4], -1) if bits == 4 else c
-
-
-def dequant_records(rec: torch.Tensor, head_dim: int, bits: int, dtype: torch.dtype, token_major: bool = False,
-                    out: tuple[torch.Tensor | None, torch.Tensor | None] | None = None
-                    ) -> tuple[torch.Tensor | None, torch.Tensor | None]:
-    """Records [..., RB] (uint8) -> K, V [..., 32, D] in dtype: code * scale + bias, both rounded in
-    dtype, as _ops.py:217-251. token_major: records [..., H, RB] -> [..., 32, H, D] contiguous.
-    out: (k, v) contiguous tensors to write into; a None entry skips that half."""
-    D, dc = head_dim, (head_dim if bits == 8 else head_dim // 2)
-    body = PAGE * dc
-    kq = rec[..., :body].view(torch.int8).unflatten(-1, (PAGE, dc))
-    vq = rec[..., body:2 * body].view(torch.int8).unflatten(-1, (PAGE, dc))
-    meta = rec[..., 2 * body:].contiguous().view(torch.float16)
-    ks, kb = meta[..., None, :D], meta[..., None, D:2 * D]
-    vs, vb = meta[..., 2 * D:2 * D + PAGE, None], meta[..., 2 * D + PAGE:2 * D + 2 * PAGE, None]
-    if token_major:
-        kq, vq, ks, kb, vs, vb = (t.transpose(-3, -2) for t in (kq, vq, ks, kb, vs, vb))
-
-    def expand(c, dst):
-        c = _codes(c, bits)
-        if dst is None:
-            return c.to(dtype, memory_format=torch.contiguous_format)
-        if dst.shape != c.shape or dst.dtype != dtype or not dst.is_contiguous():
-            raise ValueError(f"dequant_records(out=): need a contiguous {dtype} {tuple(c.shape)} tensor, "
-                             f"got {dst.dtype} {tuple(dst.shape)}")
-        return dst.copy_(c)
-
-    ko, vo = out if out is not None else (None, None)
-    k = expand(kq, ko).mul_(ks.to(dtype)).add_(kb.to(dtype)) if out is None or ko is not None else None
-    v = expand(vq, vo).mul_(vs.to(dtype)).add_(vb.to(dtype)) if out is None or vo is not None else None
-    return k, v
-
-
-def attn_lse(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, scale: float):
-    """(out fp32, log-sum-exp fp32 [B, Hq, T]) of q [B, Hq, T, D] over k, v [B, Hk, N, D]; GQA by
-    expanding kv heads (_ops.py:254-276). Computed in fp32 (the math path: the score matrix of one
-    call is materialized, so callers bound N per call)."""
-    g = q.shape[1] // k.shape[1]
-    kf, vf = k.float(), v.float()
-    if g > 1:
-        kf, vf = kf.repeat_interleave(g, 1), vf.repeat_interleave(g, 1)
-    s = torch.matmul(q.float(), kf.transpose(-1, -2).contiguous()) * scale
-    if causal:
-        T, N = q.shape[2], k.shape[2]
-        s = s.masked_fill(torch.ones(T, N, dtype=torch.bool, device=q.device).triu(N - T + 1), float("-inf"))
-    lse = torch.logsumexp(s, -1)
-    return torch.matmul(torch.softmax(s, -1), vf), lse
-
-
-def merge(acc, part):
-    """Combine two (out, lse) attention partials over disjoint key sets (_ops.py:279-285)."""
-    if acc is None:
-        return part
-    (o1, l1), (o2, l2) = acc, part
-    lse = torch.logaddexp(l1, l2)
-    return o1 * torch.exp(l1 - lse)[..., None] + o2 * torch.exp(l2 - lse)[..., None], lse
-
-
-def as_records(cache: torch.Tensor) -> torch.Tensor:
-    """Any cache tensor ([blocks, H, ...], contiguous records) as uint8 [blocks, H, RB] (_ops.py:288-292)."""
-    c = cache if cache.dtype == torch.uint8 else cache.view(torch.uint8)
-    return c.flatten(2) if c.dim() > 3 else c
-
-
-def cached_kv(records: torch.Tensor, block_ids: torch.Tensor, n: int, tail_k: torch.Tensor, head_dim: int,
-              bits: int, dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
-    """Reference view of the n cached tokens of B sequences: K, V [B, Hk, n, D] in dtype; full pages
-    dequantized, the partial last page with exact K from tail_k [B, Hk, 32, D] (_ops.py:295-306)."""
-    B, Hk, D = block_ids.shape[0], tail_k.shape[1], head_dim
-    pages = -(-n // PAGE)
-    k, v = dequant_records(records[block_ids[:, :pages].long()], D, bits, dtype)     # [B, p, Hk, 32, D]
-    k = k.permute(0, 2, 1, 3, 4).reshape(B, Hk, pages * PAGE, D)
-    v = v.permute(0, 2, 1, 3, 4).reshape(B, Hk, pages * PAGE, D)[:, :, :n]
-    r = n % PAGE
-    return torch.cat([k[:, :, :n - r], tail_k[:, :, :r].to(dtype)], 2), v
-
-
-def history_attention(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, records: torch.Tensor,
-                      block_ids: torch.Tensor, n_hist: int, tail_k: torch.Tensor,
-                      head_dim: int, bits: int, scale: float, block_bytes: int = 1 << 28) -> torch.Tensor:
-    """Attention of T new queries over n_hist cached tokens plus themselves (causal), history
-    dequantized one block of pages at a time and merged by log-sum-exp (_ops.py:309-339).
-    q [B, Hq, T, D]; k_new, v_new [B, Hk, T, D]; returns [B, Hq, T, D] in q's dtype."""
-    B, Hq, T, D = q.shape
-    Hk = k_new.shape[1]
-    G = Hq // Hk
-    full = n_hist // PAGE
-    acc = None
-    if n_hist:
-        qf = q.reshape(B, Hk, G * T, D)         # history needs no mask: fold the q heads into the query axis
-        step = max(1, block_bytes // (B * Hk * PAGE * D * q.element_size() * 2))
-        for p0 in range(0, full, step):
-            p1 = min(full, p0 + step)
-            k, v = dequant_records(records[block_ids[:, p0:p1].long()], D, bits, q.dtype)
-            k = k.permute(0, 2, 1, 3, 4).reshape(B, Hk, (p1 - p0) * PAGE, D)
-            v = v.permute(0, 2, 1, 3, 4).reshape(B, Hk, (p1 - p0) * PAGE, D)
-            acc = merge(acc, attn_lse(qf, k, v, False, scale))
-        r = n_hist % PAGE
-        if r:
-            v = dequant_records(records[block_ids[:, full].long()], D, bits, q.dtype)[1][:, :, :r]
-            acc = merge(acc, attn_lse(qf, tail_k[:, :, :r].to(q.dtype), v, False, scale))
-        acc = (acc[0].reshape(B, Hq, T, D), acc[1].reshape(B, Hq, T))
-    acc = merge(acc, attn_lse(q, k_new.to(q.dtype), v_new.to(q.dtype), True, scale))
-    return acc[0].to(q.dtype)
-
-
+# ---------------------------------------------------------------- page bookkeeping
 def pages_touched(ctx: int, total: int) -> range:
-    """Logical pages written when positions [ctx, total) are added (_ops.py:342-344)."""
-    return range(ctx // PAGE, (total - 1) // PAGE + 1) if total > ctx else range(0)
-
-
-_HADAMARD: dict = {}
-
-
-def rotation_enabled(bits: int, rotate: bool | None = None) -> bool:
-    """Whether K, V and q are Hadamard-rotated before they meet the cache. None: KUSHKASH_ROTATE
-    (auto | 1 | 0; auto = on for 4-bit, off for 8-bit) (_ops.py:350-359)."""
-    if rotate is not None:
-        return bool(rotate)
-    env = os.environ.get("KUSHKASH_ROTATE", "auto")
-    if env not in ("auto", "0", "1"):
-        raise ValueError(f"KUSHKASH_ROTATE must be auto, 0 or 1, got {env}")
-    return bits == 4 if env == "auto" else env == "1"
-
-
-def hadamard(head_dim: int, device) -> torch.Tensor:
-    """Orthonormal symmetric Walsh-Hadamard matrix [D, D] in fp32 (H @ H = I), Sylvester order,
-    cached per device (_ops.py:362-377)."""
-    key = (head_dim, str(device))
-    if key not in _HADAMARD:
-        if head_dim < 1 or head_dim & (head_dim - 1):
-            raise ValueError(f"Hadamard rotation needs a power-of-2 head_dim, got {head_dim}")
-        i = torch.arange(head_dim)
-        # H[i, j] = (-1)^popcount(i & j) is the Sylvester construction
-        bits = (i[:, None] & i[None, :])
-        parity = torch.zeros_like(bits)
-        while bool(bits.any()):
-            parity ^= bits & 1
-            bits = bits >> 1
-        h = (1 - 2 * parity).double() / math.sqrt(head_dim)
-        _HADAMARD[key] = h.to(torch.float32).to(device)
-    return _HADAMARD[key]
-
-
-FWHT_SCALE_BITS = {64: 0x3E000000, 128: 0x3DB504F3, 256: 0x3D800000}   # fp32 1/sqrt(D) (quant.mojo:101-110)
-
-
-def fwht_reference(x: torch.Tensor) -> torch.Tensor:
-    """Canonical Walsh-Hadamard evaluation in torch fp32: butterflies over strides 1, 2, ..., D/2
-    in that order, then one multiply by fp32 1/sqrt(D) (quant.mojo:90-99, _ops.py:383-395)."""
-    D = x.shape[-1]
-    y = x.float().reshape(-1, D).clone()
-    h = 1
-    while h < D:
-        y = y.view(-1, D // (2 * h), 2, h)
-        a, b = y[:, :, 0], y[:, :, 1]
-        y = torch.stack((a + b, a - b), 2).reshape(-1, D)
-        h *= 2
-    scale = torch.tensor([FWHT_SCALE_BITS[D]], dtype=torch.int32).view(torch.float32).to(y.device)
-    return (y * scale).view(x.shape)
-
-
-def _signs(head_dim: int, device, dtype: torch.dtype) -> torch.Tensor:
-    """sqrt(D) H: the same matrix with entries +-1, exact in every dtype."""
-    key = ("signs", head_dim, str(device), dtype)
-    if key not in _HADAMARD:
-        _HADAMARD[key] = torch.sign(hadamard(head_dim, device)).to(dtype)
-    return _HADAMARD[key]
-
-
-def _overlaps(a: torch.Tensor, b: torch.Tensor) -> bool:
-    """Whether the byte spans of two strided tensors intersect (conservative)."""
-    if a.device != b.device or a.numel() == 0 or b.numel() == 0:
-        return False
-
-    def span(t):
-        lo = t.data_ptr()
-        return lo, lo + (1 + sum((n - 1) * st for n, st in zip(t.shape, t.stride()))) * t.element_size()
-    (a0, a1), (b0, b1) = span(a), span(b)
-    return a0 < b1 and b0 < a1
-
-
-_EXACT_SUMS = {torch.float16: ("fp16_reduced_precision_reduction", "fp16_accumulation"),
-               torch.bfloat16: ("bf16_reduced_precision_reduction",)}
-
-
-def _exact_gemm_sums(dtype: torch.dtype) -> list:
-    """Switch off GEMM sums in fp16 / bf16 for `dtype` (torch exposes the flags under the cublas
-    name on ROCm too); returns what undo_exact_sums() needs to restore them (_ops.py:461-486)."""
-    undo = []
-    for name in _EXACT_SUMS.get(dtype, ()):
-        get = getattr(torch._C, "_get_cublas_allow_" + name, None)
-        put = getattr(torch._C, "_set_cublas_allow_" + name, None)
-        if get is None or put is None:
-            continue
-        state = get()
-        state = tuple(state) if isinstance(state, (tuple, list)) else (state,)
-        if state[0]:
-            put(False, *state[1:])
-            undo.append((put, state))
-    return undo
-
-
-def undo_exact_sums(undo: list) -> None:
-    for put, state in reversed(undo):
-        put(*state)
-
-
-def rotate(x: torch.Tensor, h: torch.Tensor | None, dtype: torch.dtype | None = None,
-           out: torch.Tensor | None = None) -> torch.Tensor:
-    """x @ h over the last dim, contiguous, in `dtype` (default x's); h None: x unchanged. One GEMM
-    in the output dtype with the +-1 matrix (exact) and 1/sqrt(D) as the GEMM's fp32 alpha, so the
-    exact orthonormal product is rounded once (_ops.py:489-518). out: contiguous, x's element count,
-    `dtype`, not overlapping x. H is symmetric and H @ H = I: the same call rotates back."""
-    if h is None:
-        y = x if dtype is None else x.to(dtype)
-        return y if out is None else out.copy_(y.reshape(out.shape))
-    dtype = dtype or x.dtype
-    D = h.shape[0]
-    x2 = x.to(dtype).reshape(-1, D)
-    if out is not None:
-        if out.numel() != x2.numel() or not out.is_contiguous() or out.dtype != dtype:
-            raise ValueError("rotate(out=): out must be contiguous, in the output dtype, with x's element count")
-        if _overlaps(out, x2):
-            raise ValueError("rotate(out=): out overlaps x")
-    undo = _exact_gemm_sums(dtype) if x2.is_cuda else []
-    try:
-        y = torch.addmm(x2, x2, _signs(D, h.device, dtype), beta=0, alpha=1.0 / math.sqrt(D),
-                        out=None if out is None else out.view(-1, D))
-    finally:
-        undo_exact_sums(undo)
-    return out if out is not None else y.view(x.shape)
+    """Logical pages that receive tokens when positions [ctx, total) are added: from the page holding
+    position ctx through the one holding total - 1 (_ops.py:342-344)."""
+    if total <= ctx:
+        return range(0)
+    return range(ctx // PAGE, (total - 1) // PAGE + 1)
 
 
 def default_scale(head_dim: int) -> float:
     return 1.0 / math.sqrt(head_dim)
+
+
+# The reference's _ops module also holds its torch helpers; they live in their own modules here and
+# keep their reference names on this one.
+from ._attention import attn_lse, history_attention, merge  # noqa: E402
+from ._records import as_records, cached_kv, dequant_records  # noqa: E402
+from ._rotation import FWHT_SCALE_BITS, fwht_reference, hadamard, rotate, rotation_enabled  # noqa: E402

@@ -1,16 +1,25 @@
-"""KushCache: paged, quantized KV cache (int4 / int8) with fused decode attention, for equal-length
-batches. Same public API as the reference's ``kushkash/cache.py`` (KushCache, MemoryStats); the
-kernels behind it are the gfx950 HIP kernels of ``Ops``.
+"""KushCache: a paged int4 / int8 KV cache with fused decode attention, for a batch whose sequences
+advance together (the Hugging Face integration and kushkash_amd.generate), on the gfx950 kernels of
+Ops. Public API and semantics: the reference's KushCache and MemoryStats (kushkash/cache.py:43-246).
 
-Memory per layer
-    pool     uint8 [pages, Hkv, RB]       one record per (page, kv head): codes + scales
-    tail_k   [B, Hkv, 32, D]              K of the page being filled, exact (model dtype); its V rows
-                                          are already final in the page's record
-Shared by all layers: block_table int32 [B, max_pages] (logical -> physical page).
-With rotation on (rotate=, KUSHKASH_ROTATE) pages and tail hold K H and V H (Hadamard H); every
-public method takes and returns unrotated tensors. The rotation is the reference's GEMM by default;
-rotate_in_kernels=True folds it into the kernels instead (the canonical Walsh-Hadamard transform
-inside the write, append and decode launches: no rotation GEMMs per step).
+Storage
+    pool         uint8 [L, blocks, Hkv, RB]   per layer, one record per (block, kv head)
+    tail_k       [L, B, Hkv, 32, D]           per layer, the exact K of each sequence's partial page
+                                              (kernel dtype); that page's V rows are final in its record
+    seq_lens     int32 [L, B]                 per layer, tokens cached, on the device (kernels read it)
+    block_table  int32 [B, pages]             shared by the layers: logical page -> block
+    tail_idx     int32 [B]                    sequence b uses tail slot b
+
+Page map. All sequences hold the same number of pages, so the map is a closed form: logical page p of
+sequence b is block p * B + b. The B blocks of one logical page are adjacent (a chunk write's jobs
+of one page touch neighbouring records), the table never changes once written, and growing the cache
+only appends blocks: the pool is reallocated with the old blocks as its prefix.
+
+Rotation. With rotation on (rotate=, KUSHKASH_ROTATE; on for 4-bit by default) the records and the
+tail hold K H and V H for the Hadamard matrix H: K, V and q are rotated on the way in and the
+decode output on the way out, by a torch product (the reference's rotation) or, with
+rotate_in_kernels=True, inside the write, append and decode kernels. Every public method takes and
+returns unrotated tensors.
 """
 from __future__ import annotations
 
@@ -18,23 +27,28 @@ from dataclasses import dataclass
 
 import torch
 
-from ._ops import (PAGE, Ops, as_records, cached_kv, default_scale, hadamard, history_attention, record_bytes,
-                   rotate, rotation_enabled)
+from ._attention import unpacked_history_attention
+from ._ops import PAGE, Ops, default_scale, pages_touched, record_bytes
+from ._records import cached_kv
+from ._rotation import hadamard, rotate, rotation_enabled
 
-_GPU_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+_KERNEL_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
 
 @dataclass
 class MemoryStats:
-    tokens: int            # tokens cached per sequence
-    quantized_bytes: int   # page records in use, all layers
-    tail_bytes: int        # exact K tails, all layers
-    reserved_bytes: int    # pool capacity incl. unused pages
-    fp16_bytes: int        # what an fp16 cache of the same content would take
+    """Bytes a KushCache holds (cache.py:23-40): its records in use, its exact K tails, what it has
+    reserved, and what an fp16 cache of the same tokens would take."""
+    tokens: int
+    quantized_bytes: int
+    tail_bytes: int
+    reserved_bytes: int
+    fp16_bytes: int
 
     @property
     def ratio(self) -> float:
-        """fp16 bytes / bytes used, including the exact K tails (cache.py:34-40)."""
+        """fp16 bytes per byte in use (records + tails; the tails are a whole page per sequence and
+        layer from the start, so short contexts compress less). int4 at D 128 tends to 3.46x."""
         used = self.quantized_bytes + self.tail_bytes
         return self.fp16_bytes / used if used else float("nan")
 
@@ -42,19 +56,17 @@ class MemoryStats:
 class KushCache:
     """
     Args:
-        num_layers, num_kv_heads, num_q_heads, head_dim: model attention shape.
-        batch_size: sequences per batch (they advance together).
+        num_layers, num_kv_heads, num_q_heads, head_dim: the model's attention shape.
+        batch_size: sequences per batch; they advance together.
         bits: 4 or 8.
-        device: "cuda[:i]" (the ROCm device).
-        dtype: dtype of q / k / v given to the cache and of the attention output.
-        max_length: optional per-sequence capacity hint; pools grow on demand otherwise.
-        scale: softmax scale (default 1/sqrt(head_dim)).
-        rotate: Hadamard-rotate K, V and q inside the cache. None: KUSHKASH_ROTATE (auto: on for
-            4-bit, off for 8-bit). Inputs and outputs stay unrotated.
-        rotate_in_kernels: with rotation on, rotate inside the kernels (canonical Walsh-Hadamard
-            transform, as Ops.fwht) instead of with a GEMM before and after them. No counterpart in
-            the reference; the rotated values differ from the GEMM's only in rounding.
-    Contract: kushkash/cache.py:43-246.
+        device: the ROCm device ("cuda[:i]").
+        dtype: dtype of q, k, v handed in and of the attention output.
+        max_length: per-sequence capacity to reserve up front (the pool grows on demand otherwise).
+        scale: softmax scale (default 1 / sqrt(head_dim)).
+        rotate: Hadamard rotation inside the cache; None reads KUSHKASH_ROTATE (auto: on for 4-bit).
+        rotate_in_kernels: with rotation on, let the kernels rotate (canonical Walsh-Hadamard
+            transform) instead of a torch product around them; no counterpart in the reference, the
+            stored values differ from the product's only in rounding.
     """
 
     def __init__(self, num_layers: int, num_kv_heads: int, num_q_heads: int, head_dim: int, *,
@@ -63,218 +75,227 @@ class KushCache:
                  rotate: bool | None = None, rotate_in_kernels: bool = False):
         if bits not in (4, 8):
             raise ValueError("bits must be 4 or 8")
-        if num_q_heads % num_kv_heads:
+        if num_kv_heads < 1 or num_q_heads % num_kv_heads:
             raise ValueError("num_q_heads must be a multiple of num_kv_heads")
         self.L, self.H, self.D, self.B = num_layers, num_kv_heads, head_dim, batch_size
         self.G = num_q_heads // num_kv_heads
         self.bits = bits
         self.RB = record_bytes(head_dim, bits)
-        self.device = torch.device(device)
         self.dtype = dtype
-        self.scale = float(scale) if scale is not None else default_scale(head_dim)
-        self.gpu = self.device.type == "cuda"
+        self.scale = default_scale(head_dim) if scale is None else float(scale)
+        device = torch.device(device)
+        self.gpu = device.type == "cuda"
         if self.gpu:
-            if dtype not in _GPU_DTYPES:
-                raise ValueError(f"dtype must be one of {_GPU_DTYPES}")
-            if self.device.index is None:
-                self.device = torch.device("cuda", torch.cuda.current_device())
-        self.kdtype = dtype if self.gpu else torch.float32            # kernel / tail dtype
-        self.ops = Ops(self.device, head_dim, bits, self.G, self.kdtype)
-        self.rot = hadamard(head_dim, self.device) if rotation_enabled(bits, rotate) else None
-        self.krot = bool(rotate_in_kernels) and self.rot is not None      # rotation folded into the kernels
-        self._work = torch.empty(0, dtype=torch.float32, device=self.device)
-        pages0 = max(1, -(-(max_length or 4 * PAGE) // PAGE))
-        self._pages = 0
-        self.pool = torch.empty(0, dtype=torch.uint8, device=self.device)
-        self._alloc_pages(batch_size * pages0)
-        self.block_table = torch.zeros(batch_size, pages0, dtype=torch.int32, device=self.device)
+            if dtype not in _KERNEL_DTYPES:
+                raise ValueError(f"dtype must be one of {_KERNEL_DTYPES}")
+            device = torch.device("cuda", torch.cuda.current_device() if device.index is None else device.index)
+        self.device = device
+        self.kdtype = dtype if self.gpu else torch.float32        # what the kernels and the tails hold
+        self.ops = Ops(device, head_dim, bits, self.G, self.kdtype)
+        self.rot = hadamard(head_dim, device) if rotation_enabled(bits, rotate) else None
+        self.krot = self.rot is not None and bool(rotate_in_kernels)
+        self.profile: list | None = None                          # a list: attend_chunk records event pairs
         self.tail_k = torch.zeros(num_layers, batch_size, num_kv_heads, PAGE, head_dim, dtype=self.kdtype,
-                                  device=self.device)
-        self.tail_idx = torch.arange(batch_size, dtype=torch.int32, device=self.device)
-        self.seq_lens = torch.zeros(num_layers, batch_size, dtype=torch.int32, device=self.device)
-        self._len = [0] * num_layers            # host mirror of seq_lens (all sequences equal)
-        self._mapped = 0                        # logical pages mapped per sequence
-        self._next = 0                          # bump allocator over physical pages
-        self._frozen_ns = 0                     # split-K fixed by freeze() (graph capture)
+                                  device=device)
+        self.tail_idx = torch.arange(batch_size, dtype=torch.int32, device=device)
+        self.seq_lens = torch.zeros(num_layers, batch_size, dtype=torch.int32, device=device)
+        self.pool = torch.zeros(num_layers, 0, num_kv_heads, self.RB, dtype=torch.uint8, device=device)
+        self.block_table = torch.zeros(batch_size, 0, dtype=torch.int32, device=device)
+        self._work = torch.zeros(0, dtype=torch.float32, device=device)
+        self._tokens = [0] * num_layers                           # host copy of seq_lens (equal across the batch)
+        self._splits = 0                                          # > 0 once freeze() fixed the split count
         self._capacity = 0
-        self.profile: list | None = None        # set to [] to record attend_chunk events
+        self._reserve(-(-(max_length or 4 * PAGE) // PAGE))
 
-    # ---------------------------------------------------------------- page management
-    def _alloc_pages(self, n: int) -> None:
-        """(Re)allocate the pool for n physical pages, keeping the existing ones."""
-        new = torch.zeros(self.L, n, self.H, self.RB, dtype=torch.uint8, device=self.device)
-        if self._pages:
-            new[:, :self._pages] = self.pool
-        self.pool, self._pages = new, n
+    # ---------------------------------------------------------------- pages
+    @property
+    def pages(self) -> int:
+        """Logical pages per sequence the pool holds."""
+        return self.block_table.shape[1]
 
-    def _map(self, need: int) -> None:
-        """Map logical pages [0, need) of every sequence to physical pages from a bump allocator;
-        pages are never freed before reset(), so table entries stay valid (cache.py:106-126)."""
-        if need <= self._mapped:
+    def _reserve(self, pages: int) -> None:
+        """Make room for `pages` logical pages per sequence: blocks [0, pages * B), the old ones kept in
+        place, and the table's closed-form entries."""
+        if pages <= self.pages:
             return
-        if self._frozen_ns:
+        if self._splits:
             raise RuntimeError(f"cache capacity {self._capacity} exceeded (set a larger max_length)")
-        add = need - self._mapped
-        if self._next + add * self.B > self._pages:
-            self._alloc_pages(max(2 * self._pages, self._next + add * self.B))
-        if need > self.block_table.shape[1]:
-            bt = torch.zeros(self.B, max(need, 2 * self.block_table.shape[1]), dtype=torch.int32, device=self.device)
-            bt[:, :self.block_table.shape[1]] = self.block_table
-            self.block_table = bt
-        ids = torch.arange(self._next, self._next + add * self.B, dtype=torch.int32, device=self.device)
-        self.block_table[:, self._mapped:need] = ids.view(self.B, add)
-        self._next += add * self.B
-        self._mapped = need
+        pages = max(pages, self.pages + self.pages // 2)
+        old = self.pool
+        self.pool = torch.zeros(self.L, pages * self.B, self.H, self.RB, dtype=torch.uint8, device=self.device)
+        self.pool[:, :old.shape[1]] = old
+        page = torch.arange(pages, dtype=torch.int32, device=self.device)
+        seq = torch.arange(self.B, dtype=torch.int32, device=self.device)
+        self.block_table = (page[None, :] * self.B + seq[:, None]).contiguous()
 
-    # ---------------------------------------------------------------- public API
-    def length(self, layer: int = 0) -> int:
-        return self._len[layer]
+    def _ensure_work(self, splits: int) -> None:
+        need = self.B * self.H * splits * self.G * (self.D + 2)
+        if splits > 1 and self._work.numel() < need:
+            self._work = torch.empty(need, dtype=torch.float32, device=self.device)
 
-    def write(self, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
-        """Append T new tokens for every sequence. k, v: [B, Hkv, T, D]. T == 1 takes the append
-        kernel (which advances seq_lens itself); a longer chunk takes the ragged write with one job
-        per (sequence, logical page) touched, seq_lens already counting the new tokens
-        (cache.py:132-162)."""
-        B, H, T, D = k.shape
-        if (B, H, D) != (self.B, self.H, self.D) or v.shape != k.shape:
-            raise ValueError(f"expected k, v of shape [{self.B}, {self.H}, T, {self.D}], got {tuple(k.shape)}")
-        if T == 0:
-            return
-        n = self._len[layer]
-        self._map(-(-(n + T) // PAGE))                 # incl. the partial page (it holds its V rows)
-        if not self.krot:
-            k, v = rotate(k, self.rot, self.kdtype), rotate(v, self.rot, self.kdtype)
-        k = k.transpose(1, 2).to(self.kdtype)          # kernel rows: [B*T, H, D], head stride D
-        v = v.transpose(1, 2).to(self.kdtype)
-        if k.stride(-1) != 1 or k.stride(-2) != D or k.stride(0) != T * k.stride(1) or v.stride() != k.stride():
-            k, v = k.contiguous(), v.contiguous()
-        k, v = k.reshape(B * T, H, D), v.reshape(B * T, H, D)
-        args = dict(cache=self.pool[layer], block_table=self.block_table, tail_k=self.tail_k[layer])
-        if self.krot:
-            args["rot"] = True
-        if T == 1:
-            self.ops.append(k, v, self.seq_lens[layer], self.tail_idx, pos_offset=0, advance=True, **args)
-        else:
-            self.seq_lens[layer].fill_(n + T)
-            pages = torch.arange(n // PAGE, (n + T - 1) // PAGE + 1, dtype=torch.int32, device=self.device)
-            job_seq = torch.arange(B, dtype=torch.int32, device=self.device).repeat_interleave(pages.numel())
-            qsl = torch.arange(B + 1, dtype=torch.int32, device=self.device) * T
-            self.ops.write(k, v, qsl, self.seq_lens[layer], self.tail_idx, job_seq, pages.repeat(B), **args)
-        self._len[layer] = n + T
+    # ---------------------------------------------------------------- rotation
+    def _inward(self, x: torch.Tensor) -> torch.Tensor:
+        """x in the kernel dtype, rotated by H unless the kernels rotate (or the cache does not)."""
+        return x.to(self.kdtype) if self.krot or self.rot is None else rotate(x, self.rot, self.kdtype)
 
-    def attend(self, layer: int, q: torch.Tensor) -> torch.Tensor:
-        """Decode attention of one query token per sequence over the whole cache. q: [B, Hq, D]
-        (q head i uses kv head i // G); returns [B, Hq, D] in self.dtype. Split-K partials go to
-        `_work` (only grows; freeze() fixes it for graph capture) (cache.py:164-183)."""
-        if self._len[layer] == 0:
-            raise RuntimeError("attend() on an empty cache")
-        return self._decode(layer, q, None, None)
+    def _outward(self, x: torch.Tensor) -> torch.Tensor:
+        """A decode output of the kernels in the model dtype, rotated back unless the kernels did."""
+        return x.to(self.dtype) if self.krot or self.rot is None else rotate(x, self.rot, self.dtype)
 
-    def append_attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
-        """write(layer, k, v) of one token per sequence, then attend(layer, q), with the append done
-        inside the decode launch (Ops.append_decode): one launch fewer per decode step. k, v: [B, Hkv,
-        1, D]; q: [B, Hq, D]. The same cache contents and outputs as the two calls. No reference
-        counterpart (its attention backends call write, then attend)."""
-        B, H, T, D = k.shape
-        if (B, H, T, D) != (self.B, self.H, 1, self.D) or v.shape != k.shape:
-            raise ValueError(f"expected k, v of shape [{self.B}, {self.H}, 1, {self.D}], got {tuple(k.shape)}")
-        n = self._len[layer]
-        self._map(-(-(n + 1) // PAGE))
-        if not self.krot:
-            k, v = rotate(k, self.rot, self.kdtype), rotate(v, self.rot, self.kdtype)
-        k = k.to(self.kdtype).reshape(B, H, D).contiguous()
-        v = v.to(self.kdtype).reshape(B, H, D).contiguous()
-        self.seq_lens[layer].add_(1)                   # the kernel appends at seq_lens - 1 (counted)
-        self._len[layer] = n + 1
-        return self._decode(layer, q, k, v)
-
-    def _decode(self, layer: int, q: torch.Tensor, k: torch.Tensor | None, v: torch.Tensor | None) -> torch.Tensor:
-        q = (q.to(self.kdtype) if self.krot else rotate(q, self.rot, self.kdtype)).contiguous()
-        out = torch.empty_like(q)
-        pages = (self._capacity if self._frozen_ns else self._len[layer]) // PAGE
-        ns = self._frozen_ns or self.ops.splits(self.B, self.H, pages)
-        if ns > 1:
-            need = self.B * self.H * ns * self.G * (2 + self.D)
-            if self._work.numel() < need:
-                self._work = torch.empty(need, dtype=torch.float32, device=self.device)
-        # GPU: the waves per workgroup from the cached length (the block table may be wider)
-        kw = {"waves": self.ops.waves(self.B, self.H, ns, pages)} if self.gpu else {}
-        if self.krot:
-            kw["rot"] = True
-        args = (self.pool[layer], self.block_table, self.seq_lens[layer], self.tail_idx, self.tail_k[layer], self.scale,
-                ns, self._work)
-        if k is None:
-            self.ops.decode(q, out, *args, **kw)
-        else:
-            self.ops.append_decode(k, v, q, out, *args, **kw)
-        return out.to(self.dtype) if self.krot else rotate(out, self.rot, self.dtype)
-
-    def attend_chunk(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                     block_bytes: int = 1 << 28) -> torch.Tensor:
-        """Attention of a chunk of T queries over the cached history plus the chunk itself (causal),
-        before the chunk is written. q: [B, Hq, T, D]; k, v: [B, Hkv, T, D] (cache.py:185-201)."""
-        prof = self.profile is not None and q.is_cuda
-        if prof:
-            ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            ev[0].record()
-        q, k, v = self._rotate(q), self._rotate(k), self._rotate(v)
-        out = history_attention(q, k, v, as_records(self.pool[layer]), self.block_table, self._len[layer],
-                                self.tail_k[layer], self.D, self.bits, self.scale, block_bytes)
-        out = self._rotate(out)
-        if prof:
-            ev[1].record()
-            self.profile.append(ev)
-        return out
-
-    def dequantize(self, layer: int) -> tuple[torch.Tensor, torch.Tensor]:
-        """Reference: the cached K, V of `layer` as [B, Hkv, n, D] in self.dtype, rotated back if the
-        cache rotates. Testing only (cache.py:203-208)."""
-        k, v = cached_kv(self.pool[layer], self.block_table, self._len[layer], self.tail_k[layer], self.D,
-                         self.bits, self.dtype)
-        return self._rotate(k), self._rotate(v)
-
-    def _rotate(self, x: torch.Tensor) -> torch.Tensor:
-        """x rotated (or rotated back: the rotation is its own inverse) the way the cache's contents are:
-        the reference's GEMM, or with rotate_in_kernels the kernels' Walsh-Hadamard transform."""
+    def _unrotate(self, x: torch.Tensor) -> torch.Tensor:
+        """Stored (rotated) values back in the model's basis, by the rotation that stored them: H is its
+        own inverse, as a product or as the kernels' Walsh-Hadamard transform."""
+        if self.rot is None:
+            return x
         if not self.krot:
             return rotate(x, self.rot)
         y = self.ops.fwht(x.to(self.kdtype).reshape(-1, self.D).contiguous())
         return y.view(x.shape).to(x.dtype)
 
-    # ---------------------------------------------------------------- graph-capture support
+    def _rows(self, x: torch.Tensor) -> torch.Tensor:
+        """[B, H, T, D] -> the kernels' rows [B * T, H, D] (head stride D) in the kernel dtype, rotated
+        for a product-rotated cache. A model's K / V usually are a transpose of exactly that layout."""
+        B, H, T, D = x.shape
+        x = x.transpose(1, 2)
+        if self.rot is not None and not self.krot:
+            return rotate(x, self.rot, self.kdtype).view(B * T, H, D)
+        x = x.to(self.kdtype)
+        return (x if x.is_contiguous() else x.contiguous()).view(B * T, H, D)
+
+    # ---------------------------------------------------------------- writes and attention
+    def length(self, layer: int = 0) -> int:
+        return self._tokens[layer]
+
+    def write(self, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Append T tokens to every sequence; k, v [B, Hkv, T, D]. One token takes the append kernel,
+        which also counts it in seq_lens; a chunk takes the ragged write over every page it touches,
+        seq_lens counting the chunk beforehand (cache.py:132-162)."""
+        B, H, T, D = k.shape
+        if (B, H, D) != (self.B, self.H, self.D) or v.shape != k.shape:
+            raise ValueError(f"expected k, v of shape [{self.B}, {self.H}, T, {self.D}], got {tuple(k.shape)}")
+        if T == 0:
+            return
+        n = self._tokens[layer]
+        self._reserve(-(-(n + T) // PAGE))
+        kw = {"rot": True} if self.krot else {}
+        dst = dict(cache=self.pool[layer], block_table=self.block_table, tail_k=self.tail_k[layer])
+        kr, vr = self._rows(k), self._rows(v)
+        if T == 1:
+            self.ops.append(kr, vr, self.seq_lens[layer], self.tail_idx, pos_offset=0, advance=True, **dst, **kw)
+        else:
+            self.seq_lens[layer].fill_(n + T)
+            touched = pages_touched(n, n + T)
+            pages = torch.arange(touched.start, touched.stop, dtype=torch.int32, device=self.device)
+            seqs = torch.arange(B, dtype=torch.int32, device=self.device)
+            starts = seqs * T
+            qsl = torch.cat([starts, starts[-1:] + T])
+            self.ops.write(kr, vr, qsl, self.seq_lens[layer], self.tail_idx,
+                           seqs.repeat_interleave(len(touched)), pages.repeat(B), **dst, **kw)
+        self._tokens[layer] = n + T
+
+    def attend(self, layer: int, q: torch.Tensor) -> torch.Tensor:
+        """Decode attention of one query per sequence over all its cached tokens. q [B, Hq, D] (q head i
+        reads kv head i // G); returns [B, Hq, D] in self.dtype (cache.py:164-183). Split-K partials
+        go to a work buffer that only grows (freeze() sizes it for graph capture)."""
+        if self._tokens[layer] == 0:
+            raise RuntimeError("attend() on an empty cache")
+        return self._decode(layer, q)
+
+    def append_attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        """write() of one token per sequence (k, v [B, Hkv, 1, D]) then attend(layer, q), the append done
+        by the decode launch itself (Ops.append_decode): the same records, tails and output as the two
+        calls, one launch fewer per decode step. No reference counterpart."""
+        if k.shape != (self.B, self.H, 1, self.D) or v.shape != k.shape:
+            raise ValueError(f"expected k, v of shape [{self.B}, {self.H}, 1, {self.D}], got {tuple(k.shape)}")
+        n = self._tokens[layer]
+        self._reserve(-(-(n + 1) // PAGE))
+        token = (self._rows(k), self._rows(v))
+        self.seq_lens[layer].add_(1)                     # the fused append writes at seq_lens - 1
+        self._tokens[layer] = n + 1
+        return self._decode(layer, q, token)
+
+    def _decode(self, layer: int, q: torch.Tensor, token=None) -> torch.Tensor:
+        qk = self._inward(q).contiguous()
+        out = torch.empty_like(qk)
+        pages = (self._capacity if self._splits else self._tokens[layer]) // PAGE
+        splits = self._splits or self.ops.splits(self.B, self.H, pages)
+        self._ensure_work(splits)
+        kw = {"rot": True} if self.krot else {}
+        if self.gpu:                                     # waves by the cached length (the table is wider)
+            kw["waves"] = self.ops.waves(self.B, self.H, splits, pages)
+        args = (self.pool[layer], self.block_table, self.seq_lens[layer], self.tail_idx, self.tail_k[layer],
+                self.scale, splits, self._work)
+        if token is None:
+            self.ops.decode(qk, out, *args, **kw)
+        else:
+            self.ops.append_decode(token[0], token[1], qk, out, *args, **kw)
+        return self._outward(out)
+
+    def attend_chunk(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                     block_bytes: int = 1 << 28) -> torch.Tensor:
+        """Attention of a chunk of T queries over the cached history plus the chunk itself (causal),
+        before the chunk is written; q [B, Hq, T, D], k, v [B, Hkv, T, D] -> [B, Hq, T, D]
+        (cache.py:185-201). The history is unpacked a block of pages at a time by the unpack kernel,
+        rotated back in that kernel when the cache rotates, so the attention itself runs on the
+        unrotated q and chunk; extra memory stays within ~block_bytes at any history length."""
+        timing = self.profile is not None and q.is_cuda
+        if timing:
+            ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            ev[0].record()
+        out = unpacked_history_attention(self.ops, q, k, v, self.pool[layer], self.block_table, self._tokens[layer],
+                                         self.tail_k[layer], self.tail_idx, self.scale, self.rot is not None,
+                                         block_bytes)
+        if timing:
+            ev[1].record()
+            self.profile.append(ev)
+        return out
+
+    def dequantize(self, layer: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """Reference view: the cached K, V of `layer` as [B, Hkv, n, D] in self.dtype, dequantized by
+        torch and rotated back; materializes the whole history (cache.py:203-208). Testing only."""
+        k, v = cached_kv(self.pool[layer], self.block_table, self._tokens[layer], self.tail_k[layer], self.D,
+                         self.bits, self.dtype)
+        return self._unrotate(k), self._unrotate(v)
+
+    # ---------------------------------------------------------------- graph capture
     def freeze(self, max_tokens: int) -> None:
-        """Pre-map pages for `max_tokens` per sequence and fix the split-K factor, so decode steps
-        allocate nothing on the host and can be captured in a HIP graph (cache.py:211-221)."""
+        """Reserve pages for max_tokens per sequence and fix the split count, so that decode steps
+        allocate nothing and can be captured in a HIP graph (cache.py:211-221)."""
         if not self.gpu:
             raise RuntimeError("freeze() is for the GPU path")
-        self._map(-(-max_tokens // PAGE))
-        self._frozen_ns = self.ops.splits(self.B, self.H, max_tokens // PAGE)
-        need = self.B * self.H * self._frozen_ns * self.G * (2 + self.D)
-        if self._work.numel() < need:
-            self._work = torch.empty(need, dtype=torch.float32, device=self.device)
+        self._reserve(-(-max_tokens // PAGE))
+        self._splits = self.ops.splits(self.B, self.H, max_tokens // PAGE)
+        self._ensure_work(self._splits)
         self._capacity = max_tokens
 
     def advance(self, steps: int = 1) -> None:
-        """Host bookkeeping after replaying `steps` captured decode steps (the append kernel inside
-        the graph advances the device seq_lens)."""
-        if max(self._len) + steps > self._capacity:
+        """Count `steps` replayed decode steps on the host (inside the graph the append kernel counts
+        them on the device)."""
+        if max(self._tokens) + steps > self._capacity:
             raise RuntimeError(f"cache capacity {self._capacity} exceeded")
-        self._len = [n + steps for n in self._len]
+        self._tokens = [n + steps for n in self._tokens]
+
+    def lengths(self) -> list[int]:
+        """The host-side token counts of every layer (a copy)."""
+        return list(self._tokens)
+
+    def set_lengths(self, tokens: list[int]) -> None:
+        """Restore host-side token counts taken by lengths() (a graph capture records calls without
+        running them)."""
+        if len(tokens) != self.L:
+            raise ValueError(f"expected {self.L} lengths")
+        self._tokens = [int(n) for n in tokens]
 
     def reset(self) -> None:
-        """Drop all tokens (keeps the allocated pools)."""
-        self._len = [0] * self.L
+        """Drop every token; the pool, table and tails stay allocated, and the split count is free again."""
+        self._tokens = [0] * self.L
         self.seq_lens.zero_()
-        self._mapped = 0
-        self._next = 0
-        self._frozen_ns = 0
+        self._splits = 0
+        self._capacity = 0
 
     def memory(self) -> MemoryStats:
-        n = max(self._len)
-        return MemoryStats(
-            tokens=n,
-            quantized_bytes=self.L * self.B * -(-n // PAGE) * self.H * self.RB,
-            tail_bytes=self.tail_k.numel() * self.tail_k.element_size(),
-            reserved_bytes=self.pool.numel() + self.tail_k.numel() * self.tail_k.element_size(),
-            fp16_bytes=self.L * self.B * self.H * n * self.D * 2 * 2,
-        )
+        n = max(self._tokens)
+        tails = self.tail_k.numel() * self.tail_k.element_size()
+        return MemoryStats(tokens=n, quantized_bytes=self.L * self.B * self.H * -(-n // PAGE) * self.RB,
+                           tail_bytes=tails, reserved_bytes=self.pool.numel() + tails,
+                           fp16_bytes=2 * self.L * self.B * self.H * n * self.D * 2)

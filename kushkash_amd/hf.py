@@ -1,23 +1,22 @@
-"""Hugging Face transformers (>= 5.0) entry point: a transformers ``Cache`` backed by a KushCache and
-the "kushkash" attention function that writes to it and attends over it with the HIP kernels.
-Contract: kushkash/hf.py:1-220 (same public names, arguments and error behaviour).
+"""Hugging Face transformers (>= 5.0) entry point: KushHFCache, a transformers Cache over a KushCache,
+and the "kushkash" attention function that writes each new K / V chunk into it and attends over it
+with the gfx950 kernels. Public names, arguments and error types: the reference's hf.py (hf.py:1-220).
 
     import kushkash_amd as kk
-    model = kk.enable(model)                                  # validate, register, select "kushkash"
+    model = kk.enable(model)                         # check the config, register and select "kushkash"
     out = model.generate(**inputs, past_key_values=kk.KushHFCache(model.config, bits=4), max_new_tokens=256)
 
-Per layer, transformers calls ``Cache.update`` and then the attention function with the same new
-K/V chunk. ``KushHFCache.update`` stores nothing: it creates the KushCache on first use and leaves
-itself in a thread-local slot, which the attention function takes (the attention interface passes
-no cache). The attention function then, by the chunk's length T and the cached length n:
-  T = 1          append the token and decode over the cache, in one launch (KushCache.append_attend);
-  T > 1, n = 0   exact causal attention over the prompt, then the ragged write of the prompt;
-  T > 1, n > 0   attention over the dequantized history, one page block at a time, plus the chunk
-                 (causal), merged by log-sum-exp (KushCache.attend_chunk); then the write.
+How a layer's call flows. transformers calls Cache.update(k, v, layer) and then the attention function
+with the same k and v tensors. KushHFCache.update stores nothing; it attaches a route -- (cache,
+layer) -- to the key tensor, and the attention function reads the route off the key it receives. No
+state outlives the call: a forward without a KushHFCache carries no route and is refused. The
+attention function then picks by the chunk length T and the tokens n already cached:
+    T = 1          append the token and decode, one kernel launch (KushCache.append_attend);
+    T > 1, n = 0   causal attention over the prompt itself, then the chunk write;
+    T > 1, n > 0   attention over the history (unpacked a block at a time by the unpack kernel) and
+                   the chunk (causal), merged by log-sum-exp (KushCache.attend_chunk); then the write.
 """
 from __future__ import annotations
-
-import threading
 
 import torch
 import torch.nn.functional as F
@@ -25,26 +24,30 @@ from torch.nn.attention import SDPBackend, sdpa_kernel
 from transformers import AttentionInterface, AttentionMaskInterface
 from transformers.cache_utils import Cache, CacheLayerMixin
 
-from ._ops import attn_lse
+from ._attention import self_attention_blocks
 from .cache import KushCache
 
 NAME = "kushkash"
-_handoff = threading.local()        # .cache: the KushHFCache whose update() ran last on this thread
+_ROUTE = "_kushkash_route"          # attribute of the key tensor that update() hands to the attention
 
 
 def _text_config(config):
     return config.get_text_config() if hasattr(config, "get_text_config") else config
 
 
-class _KushLayer(CacheLayerMixin):
-    """One layer's view of the shared KushCache (hf.py:34-80). It holds no tensors: lengths come
-    from the KushCache, and the operations a quantized page cache cannot do raise."""
+def _refuse(what: str):
+    raise NotImplementedError(f"kushkash: {what} is not supported by a quantized page cache")
+
+
+class _PagedLayer(CacheLayerMixin):
+    """One layer's face of the shared KushCache for transformers (hf.py:34-80): it holds no tensors,
+    reports the cached length, and refuses what a quantized page cache cannot do."""
     is_sliding = False
     is_croppable = False
 
-    def __init__(self, owner: "KushHFCache", layer: int):
+    def __init__(self, owner: "KushHFCache", index: int):
         super().__init__()
-        self.owner, self.layer = owner, layer
+        self.owner, self.index = owner, index
 
     def lazy_initialization(self, key_states, value_states):
         self.is_initialized = True
@@ -53,31 +56,17 @@ class _KushLayer(CacheLayerMixin):
         return key_states, value_states
 
     def get_seq_length(self) -> int:
-        kv = self.owner.kv
-        return 0 if kv is None else kv.length(self.layer)
+        return self.owner.tokens(self.index)
 
     def get_mask_sizes(self, query_length: int) -> tuple[int, int]:
-        # sizes only: kush_mask never builds a mask (causal over everything cached plus the chunk)
-        return self.get_seq_length() + query_length, 0
+        return self.get_seq_length() + query_length, 0     # sizes only: no mask is ever built
 
     def get_max_length(self) -> int:
-        return -1                                   # pages are mapped on demand
+        return -1                                           # the pool grows on demand
 
     def reset(self) -> None:
-        if self.layer == 0 and self.owner.kv is not None:
+        if self.index == 0 and self.owner.kv is not None:   # one reset for the whole cache
             self.owner.kv.reset()
-
-    def reorder_cache(self, beam_idx):
-        raise NotImplementedError("kushkash: beam search is not supported")
-
-    def crop(self, max_length):
-        raise NotImplementedError("kushkash: cropping (assisted / speculative decoding) is not supported")
-
-    def batch_repeat_interleave(self, repeats):
-        raise NotImplementedError("kushkash: batch expansion is not supported; pass num_return_sequences=1")
-
-    def batch_select_indices(self, indices):
-        raise NotImplementedError("kushkash: batch selection is not supported")
 
     def offload(self):
         pass
@@ -85,19 +74,30 @@ class _KushLayer(CacheLayerMixin):
     def prefetch(self):
         pass
 
+    def reorder_cache(self, beam_idx):
+        _refuse("beam search")
+
+    def crop(self, max_length):
+        _refuse("cropping (assisted or speculative decoding)")
+
+    def batch_repeat_interleave(self, repeats):
+        _refuse("batch expansion (use num_return_sequences=1)")
+
+    def batch_select_indices(self, indices):
+        _refuse("batch selection")
+
 
 class KushHFCache(Cache):
-    """Drop-in for transformers' DynamicCache (hf.py:83-119).
+    """A transformers Cache to pass as past_key_values in place of DynamicCache (hf.py:83-119).
 
     Args:
-        config: the model config (the text config of a multimodal model is used).
+        config: the model config (for a multimodal model, its text config is used).
         bits: 4 (default) or 8.
-        max_length: optional per-sequence capacity hint (pages are mapped on demand otherwise).
+        max_length: per-sequence capacity to reserve (the pool grows on demand otherwise).
         rotate: Hadamard rotation inside the cache (None: KUSHKASH_ROTATE; auto = on for 4-bit).
-        rotate_in_kernels: fold that rotation into the write and decode kernels (KushCache's option of
-            the same name; no reference counterpart).
-    The KushCache itself is created by the first update(), on the device and in the dtype of the
-    model's K/V (a GPU device: the kernels run on the GPU only).
+        rotate_in_kernels: let the kernels do that rotation (KushCache's option; no reference counterpart).
+    The KushCache is created by the first update(), with the batch size, device and dtype of the
+    model's keys (a GPU device: the kernels run on the GPU only).
     """
 
     def __init__(self, config, bits: int = 4, max_length: int | None = None, rotate: bool | None = None,
@@ -108,118 +108,126 @@ class KushHFCache(Cache):
         self.head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
         self.bits, self.max_length, self.rotate, self.rotate_in_kernels = bits, max_length, rotate, rotate_in_kernels
         self.kv: KushCache | None = None
-        super().__init__(layers=[_KushLayer(self, i) for i in range(self.num_layers)])
+        super().__init__(layers=[_PagedLayer(self, i) for i in range(self.num_layers)])
+
+    def tokens(self, layer: int) -> int:
+        return 0 if self.kv is None else self.kv.length(layer)
 
     def update(self, key_states, value_states, layer_idx, *args, **kwargs):
-        """Called by transformers right before the attention function of layer `layer_idx`; the chunk
-        is written by that function, so it is returned unchanged."""
+        """Called right before layer `layer_idx`'s attention: creates the KushCache on first use and
+        routes the chunk to the attention function, which writes it; returns k, v unchanged."""
         if self.kv is None:
             B, H, _, D = key_states.shape
             self.kv = KushCache(self.num_layers, H, self.num_q_heads, D, batch_size=B, bits=self.bits,
                                 device=key_states.device, dtype=key_states.dtype, max_length=self.max_length,
                                 rotate=self.rotate, rotate_in_kernels=self.rotate_in_kernels)
         self.layers[layer_idx].is_initialized = True
-        _handoff.cache = self
+        setattr(key_states, _ROUTE, (self, layer_idx))
         return key_states, value_states
 
     def memory(self):
-        """MemoryStats of the KushCache (None before the first forward)."""
+        """MemoryStats of the KushCache, or None before the first forward."""
         return None if self.kv is None else self.kv.memory()
 
 
-def prompt_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float) -> torch.Tensor:
-    """Causal attention of a prompt over itself (nothing cached yet): q [B, Hq, T, D], k, v
-    [B, Hkv, T, D] -> [B, Hq, T, D] in q's dtype (hf.py:122-129). fp32 inputs use the fp32 product
-    path (attn_lse). fp16 / bf16 take torch's fused SDPA, restricted to its flash and
-    memory-efficient kernels, with K/V expanded to the q heads; where neither applies the fp32
-    path runs instead, so torch's half-precision math fallback (batched products over transposed
-    views) is never used."""
-    if q.dtype != torch.float32:
+def prompt_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
+                     block_bytes: int = 1 << 28) -> torch.Tensor:
+    """Causal attention of a prompt over itself when nothing is cached yet: q [B, Hq, T, D], k, v
+    [B, Hkv, T, D] -> [B, Hq, T, D] in q's dtype (hf.py:122-129). Half-precision inputs go to torch's
+    fused attention, limited to its flash and memory-efficient kernels (K / V expanded to the q heads);
+    everything else, and any input those kernels refuse, to fp32 products over blocks of keys whose
+    memory stays within block_bytes. torch's half-precision math path (batched products over
+    transposed views) is never taken."""
+    if q.dtype in (torch.float16, torch.bfloat16):
         g = q.shape[1] // k.shape[1]
-        ke, ve = (k.repeat_interleave(g, 1), v.repeat_interleave(g, 1)) if g > 1 else (k, v)
+        ke = k.repeat_interleave(g, 1) if g > 1 else k
+        ve = v.repeat_interleave(g, 1) if g > 1 else v
         try:
             with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
                 return F.scaled_dot_product_attention(q, ke, ve, is_causal=True, scale=scale)
         except RuntimeError:
             pass
-    return attn_lse(q, k, v, True, scale)[0].to(q.dtype)
+    return self_attention_blocks(q, k, v, scale, block_bytes)[0].to(q.dtype)
 
 
-def _check_start(kv: KushCache, position_ids) -> None:
-    """A multi-token chunk must continue the sequence the cache holds (hf.py:132-147): generate() on a
-    cache that already holds another sequence would attend to it silently. Checked on layer 0 of a
-    multi-token forward (one host read), never on decode steps; skipped on an empty cache and
-    without 2-D position ids."""
+def _continues(kv: KushCache, position_ids) -> None:
+    """A multi-token chunk on a non-empty cache must start at the cache's length (hf.py:132-147):
+    otherwise the cache holds another sequence (a KushHFCache reused for a new prompt) and attending
+    to it would be silently wrong. One host read, on layer 0 of multi-token forwards only; an empty
+    cache (a RoPE offset is fine there) and non-2-D position ids are not checked."""
     held = kv.length(0)
-    if held == 0 or position_ids is None or position_ids.dim() != 2:
-        return
-    start = int(position_ids[0, 0])
-    if start != held:
-        raise RuntimeError(f"kushkash: this KushHFCache holds {held} tokens, but the new input starts at position "
-                           f"{start}, not {held}. A cache only continues the sequence it holds (for another turn, "
-                           f"pass the earlier ids plus the new ones). Use a new KushHFCache, or cache.reset(), for "
-                           f"another prompt.")
+    if held and position_ids is not None and position_ids.dim() == 2:
+        first = int(position_ids[0, 0])
+        if first != held:
+            raise RuntimeError(f"kushkash: this KushHFCache holds {held} tokens, so new input must start at position "
+                               f"{held}, but it starts at {first}. Pass the earlier tokens plus the new ones to "
+                               f"continue the conversation, or start another prompt with a new KushHFCache (or "
+                               f"cache.reset()).")
 
 
 def kush_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
-    """The "kushkash" attention function (hf.py:150-177). query [B, Hq, T, D]; key, value: the new
-    chunk [B, Hkv, T, D]. Returns ([B, T, Hq, D], None)."""
-    owner: KushHFCache | None = getattr(_handoff, "cache", None)
-    _handoff.cache = None                           # one update() per attention call
-    if owner is None or owner.kv is None:
-        raise RuntimeError("kushkash attention needs past_key_values=KushHFCache(...) (and use_cache=True)")
-    kv, layer = owner.kv, module.layer_idx
+    """The "kushkash" attention function (hf.py:150-177): query [B, Hq, T, D]; key, value the new chunk
+    [B, Hkv, T, D]; returns ([B, T, Hq, D], None)."""
+    route = getattr(key, _ROUTE, None)
+    if route is None or route[0].kv is None:
+        raise RuntimeError("kushkash attention runs on a KushHFCache: pass past_key_values=KushHFCache(...) "
+                           "and use_cache=True")
+    delattr(key, _ROUTE)
+    kv, layer = route[0].kv, route[1]
     if scaling is not None:
         kv.scale = float(scaling)
     T = query.shape[2]
     if T == 1:
         return kv.append_attend(layer, query[:, :, 0], key, value).unsqueeze(1), None
     if layer == 0:
-        _check_start(kv, kwargs.get("position_ids"))
-    if kv.length(layer) == 0:
-        out = prompt_attention(query, key, value, kv.scale)
-    else:
+        _continues(kv, kwargs.get("position_ids"))
+    if kv.length(layer):
         out = kv.attend_chunk(layer, query, key, value)
+    else:
+        out = prompt_attention(query, key, value, kv.scale)
     kv.write(layer, key, value)
     return out.transpose(1, 2).contiguous(), None
 
 
 def kush_mask(batch_size, q_length, kv_length, *args, attention_mask=None, **kwargs):
-    """The "kushkash" mask function (hf.py:180-186): no mask is built, the kernels are causal by
-    construction. A padded batch is refused on multi-token calls; decode steps are not checked
-    (that would read the mask back every token)."""
-    if (attention_mask is not None and q_length > 1 and attention_mask.dim() == 2
-            and not bool(attention_mask.all())):
-        raise NotImplementedError("kushkash: padded batches are not supported; batch equal-length prompts")
+    """The "kushkash" mask function (hf.py:180-186): no mask is built (the kernels are causal by
+    construction). A padded batch is refused where it shows, on multi-token calls; decode steps are
+    not checked (that would read the mask back on every token)."""
+    padded = (attention_mask is not None and q_length > 1 and attention_mask.dim() == 2
+              and not bool(attention_mask.all()))
+    if padded:
+        raise NotImplementedError("kushkash: padded batches are not supported; batch prompts of equal length")
     return None
 
 
-def _window_binds(cfg) -> bool:
-    """Whether the config's attention window can exclude tokens (hf.py:189-206): layer_types decide
-    when present (a window applies only to "sliding_attention" layers); without them, the legacy
-    use_sliding_window flag, or a sliding_window below max_position_embeddings (a window with no
-    maximum to compare against counts as binding)."""
-    types = getattr(cfg, "layer_types", None)
-    if types:
-        return any(t != "full_attention" for t in types)
+def _window_can_bind(cfg) -> bool:
+    """Whether an attention window of the config can hide tokens (hf.py:189-206). Per-layer types, when
+    given, decide alone (a window applies to "sliding_attention" layers only). Without them: the
+    use_sliding_window flag, or a positive sliding_window shorter than max_position_embeddings (with
+    no maximum to compare against, a window is taken to bind)."""
+    kinds = getattr(cfg, "layer_types", None)
+    if kinds:
+        return any(kind != "full_attention" for kind in kinds)
     if getattr(cfg, "use_sliding_window", False):
         return True
-    window = getattr(cfg, "sliding_window", None)
-    if not window:
-        return False
+    window = getattr(cfg, "sliding_window", None) or 0
     limit = getattr(cfg, "max_position_embeddings", None)
-    return limit is None or window < limit
+    return window > 0 and (limit is None or window < limit)
+
+
+# (test on the text config, what is refused): attention these kernels do not compute (hf.py:209-216)
+_UNSUPPORTED = (
+    (_window_can_bind, "sliding-window / hybrid attention layers"),
+    (lambda cfg: bool(getattr(cfg, "attn_logit_softcapping", None)), "attention logit softcapping"),
+    (lambda cfg: bool(getattr(cfg, "kv_lora_rank", None)), "MLA (latent KV) attention"),
+)
 
 
 def _check_config(config) -> None:
-    """Refuse the attention variants the kernels do not compute (hf.py:209-216)."""
     cfg = _text_config(config)
-    if _window_binds(cfg):
-        raise NotImplementedError("kushkash: sliding-window / hybrid attention layers are not supported")
-    if getattr(cfg, "attn_logit_softcapping", None):
-        raise NotImplementedError("kushkash: attention logit softcapping is not supported")
-    if getattr(cfg, "kv_lora_rank", None):
-        raise NotImplementedError("kushkash: MLA (latent KV) models are not supported")
+    for test, what in _UNSUPPORTED:
+        if test(cfg):
+            _refuse(what)
 
 
 def register() -> None:
@@ -228,7 +236,8 @@ def register() -> None:
 
 
 def enable(model):
-    """Validate the model's config, register the "kushkash" attention and select it; returns the model."""
+    """Check the model's config, register the "kushkash" attention and mask functions and select them;
+    returns the model."""
     _check_config(model.config)
     register()
     model.set_attn_implementation(NAME)

@@ -134,3 +134,32 @@ def test_rotation_lowers_attention_error_gpu():
     err = rotation_errors(lambda rot: kk.KushCache(1, 2, 8, 128, batch_size=1, bits=4, device=DEV,
                                                    dtype=torch.float32, rotate=rot), DEV)
     assert err[True][0] < 0.9 * err[False][0] and err[True][1] < 0.9 * err[False][1], err
+
+
+def test_attend_chunk_memory_is_bounded():
+    """A 1,024-token prefill chunk over 131,072 cached tokens (Qwen3-8B width: 32 q / 8 kv heads, D 128,
+    int4, bf16, batch 1): attend_chunk allocates at most 1 GB beyond the cache while it runs (the score
+    matrix of the whole history alone would be 17 GB in fp32), and its output matches the torch
+    reference path over the same records (history_attention: torch dequantization, key blocks merged by
+    log-sum-exp) -- both attend over the same bf16 K / V values, so only fp32 summation order differs."""
+    from kushkash_amd._ops import history_attention
+    B, Hq, Hkv, D, N, T = 1, 32, 8, 128, 131072, 1024
+    g = torch.Generator(device=DEV)
+    g.manual_seed(11)
+    c = kk.KushCache(1, Hkv, Hq, D, batch_size=B, bits=4, device=DEV, dtype=torch.bfloat16, rotate=False,
+                     max_length=N + T)
+    for t0 in range(0, N, 16384):
+        c.write(0, torch.randn(B, Hkv, 16384, D, generator=g, device=DEV).to(torch.bfloat16),
+                torch.randn(B, Hkv, 16384, D, generator=g, device=DEV).to(torch.bfloat16))
+    q = torch.randn(B, Hq, T, D, generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, T, D, generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, T, D, generator=g, device=DEV).to(torch.bfloat16)
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    out = c.attend_chunk(0, q, k, v)
+    torch.cuda.synchronize()
+    extra = torch.cuda.max_memory_allocated() - base
+    assert extra <= 1 << 30, f"attend_chunk took {extra / 2**20:.0f} MiB beyond the cache"
+    ref = history_attention(q, k, v, c.pool[0], c.block_table, N, c.tail_k[0], D, 4, c.scale)
+    assert_out_close(out, ref.float(), torch.bfloat16, base=1e-3, roundings=2, what="attend_chunk vs the torch path")

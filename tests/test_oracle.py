@@ -5,14 +5,15 @@ over the dequantized cache (tests/test_cpu.py:79-96), the quantization error bou
 (tests/test_cpu.py:99-106), chunk attention over the history (tests/test_cpu.py:207-222) and the
 ragged vLLM-style simulation (tests/test_ragged.py)."""
 import random
+from dataclasses import dataclass, field
 
 import pytest
 import torch
 import torch.nn.functional as F
 
-from _harness import oracle_cache, ref_dequant, ref_quantize, split_record
-from kushkash_amd._ops import (PAGE, as_records, cached_kv, dequant_records, hadamard, history_attention,
-                               pages_touched, record_bytes)
+from _harness import oracle_cache, ref_quantize, split_record
+from kushkash_amd._ops import (PAGE, as_records, cached_kv, hadamard, history_attention, pages_touched,
+                               record_bytes)
 from oracle.cpu_ops import OracleOps
 
 
@@ -143,128 +144,157 @@ def test_decode_threads_agree():
     assert torch.equal(one, many)
 
 
-class Sim:
-    """Minimal vLLM-like host over the oracle's raw Ops (tests/test_ragged.py:27-135): a block pool
-    with a padded block stride, per-request block tables with a padded row stride, permuted tail
-    slots, V rows as a strided view into a fused qkv buffer, vLLM positions (seq_lens already counts
-    the new tokens)."""
+@dataclass
+class _Request:
+    """One request of the ragged host: its blocks (logical page order), tail slot, and every token it
+    has cached, exactly (the ground truth the stored records and tails are checked against)."""
+    slot: int
+    blocks: list = field(default_factory=list)
+    k: list = field(default_factory=list)            # [H, D] rows, one per cached token
+    v: list = field(default_factory=list)
 
-    def __init__(self, D, bits, H, G, n_req, n_blocks=96, max_blocks=16, pad=48):
+    @property
+    def n(self) -> int:
+        return len(self.k)
+
+
+class RaggedHost:
+    """A vLLM-like host over the oracle's raw Ops, restating the semantics the reference checks in
+    tests/test_ragged.py: blocks taken from a shuffled free list of a pool whose block stride is
+    padded, a block table with a padded row stride, tail slots that are a permutation with spares,
+    V rows read through a strided view of a fused qkv buffer, and vLLM's positions (seq_lens already
+    counts the step's tokens). Each step runs the decodes first (append + decode) and then the
+    chunked prefills (attention over history and chunk, then the ragged write)."""
+
+    def __init__(self, D: int, bits: int, H: int, G: int, n_req: int, n_blocks: int = 96, pad: int = 48):
         self.D, self.bits, self.H, self.G = D, bits, H, G
         rb = record_bytes(D, bits)
-        raw = torch.zeros(n_blocks, H * rb + pad, dtype=torch.uint8)
-        self.cache = raw[:, :H * rb].view(n_blocks, H, PAGE, rb // PAGE)
+        storage = torch.zeros(n_blocks, H * rb + pad, dtype=torch.uint8)
+        self.pool = storage[:, :H * rb].view(n_blocks, H, PAGE, rb // PAGE)     # strided vLLM-style view
         self.ops = OracleOps("cpu", D, bits, G)
-        free = list(range(n_blocks))
-        random.Random(0).shuffle(free)
-        self.free = free
-        self.bt = torch.zeros(n_req, max_blocks, dtype=torch.int32)
-        self.lens = [0] * n_req
-        self.tail_idx = torch.tensor(random.Random(1).sample(range(n_req + 3), n_req), dtype=torch.int32)
+        self.free = random.Random(0).sample(range(n_blocks), n_blocks)
+        slots = random.Random(1).sample(range(n_req + 3), n_req)
+        self.reqs = [_Request(slot=s) for s in slots]
         self.tail_k = torch.zeros(n_req + 3, H, PAGE, D)
-        self.exact = [(torch.zeros(H, 0, D), torch.zeros(H, 0, D)) for _ in range(n_req)]
+        self.width = 16                                     # block-table columns per request
 
-    def ensure_blocks(self, r, total):
-        for p in range(-(-total // PAGE)):
-            if p >= -(-self.lens[r] // PAGE):
-                self.bt[r, p] = self.free.pop()
+    # ---------------------------------------------------------------- host bookkeeping
+    def _table(self, ids: list) -> torch.Tensor:
+        """The requests' block ids as an int32 table view with a padded row stride."""
+        t = torch.zeros(len(ids), self.width + 5, dtype=torch.int32)[:, :self.width]
+        for row, r in enumerate(ids):
+            t[row, :len(self.reqs[r].blocks)] = torch.tensor(self.reqs[r].blocks, dtype=torch.int32)
+        return t
 
-    def history(self, r, n):
-        ts = int(self.tail_idx[r])
-        k, v = cached_kv(as_records(self.cache), self.bt[r:r + 1], n, self.tail_k[ts:ts + 1], self.D, self.bits,
-                         torch.float32)
+    def _grow(self, r: int, total: int) -> None:
+        while len(self.reqs[r].blocks) * PAGE < total:
+            self.reqs[r].blocks.append(self.free.pop())
+
+    def _stored(self, r: int, n: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """The first n tokens of request r as the cache holds them, K, V [H, n, D]."""
+        req = self.reqs[r]
+        k, v = cached_kv(as_records(self.pool), self._table([r]), n, self.tail_k[req.slot:req.slot + 1], self.D,
+                         self.bits, torch.float32)
         return k[0], v[0]
 
-    def step(self, reqs, qlens):
-        rows_k, rows_v, qsl, seq_lens = [], [], [0], []
-        for r, ql in zip(reqs, qlens):
-            rows_k.append(torch.randn(ql, self.H, self.D))
-            rows_v.append(torch.randn(ql, self.H, self.D))
-            qsl.append(qsl[-1] + ql)
-            self.ensure_blocks(r, self.lens[r] + ql)
-            seq_lens.append(self.lens[r] + ql)
-        k_all = torch.cat(rows_k)
-        qkv = torch.zeros(k_all.shape[0], 3 * self.H * self.D)
-        qkv[:, 2 * self.H * self.D:] = torch.cat(rows_v).flatten(1)
-        v_all = qkv[:, 2 * self.H * self.D:].view(-1, self.H, self.D)
-        q_all = torch.randn(k_all.shape[0], self.H * self.G, self.D)
-        W = self.bt.shape[1]
-        bt = torch.zeros(len(reqs), W + 7, dtype=torch.int32)[:, :W]
-        bt[:] = self.bt[reqs]
-        sl = torch.tensor(seq_lens, dtype=torch.int32)
-        ti = self.tail_idx[reqs].contiguous()
-        nd = next((i for i, ql in enumerate(qlens) if ql != 1), len(qlens))
-        outs = torch.empty_like(q_all)
-        refs = {}
-        if nd:
-            self.ops.append(k_all[:nd], v_all[:nd], sl[:nd], ti[:nd], self.cache, bt[:nd], self.tail_k,
-                            pos_offset=-1, advance=False)
-            self.ops.decode(q_all[:nd].contiguous(), outs[:nd], self.cache, bt[:nd], sl[:nd], ti[:nd],
-                            self.tail_k, self.D ** -0.5)
-            for i in range(nd):
-                refs[i] = self.history(reqs[i], seq_lens[i])
-        rec = as_records(self.cache)
-        for i in range(nd, len(reqs)):
-            r, a, b = reqs[i], qsl[i], qsl[i + 1]
-            ts = int(ti[i])
-            hk, hv = self.history(r, self.lens[r])
-            refs[i] = (torch.cat([hk, k_all[a:b].permute(1, 0, 2)], 1),
-                       torch.cat([hv, v_all[a:b].permute(1, 0, 2)], 1))
-            o = history_attention(q_all[a:b].permute(1, 0, 2).unsqueeze(0), k_all[a:b].permute(1, 0, 2).unsqueeze(0),
-                                  v_all[a:b].permute(1, 0, 2).unsqueeze(0), rec, bt[i:i + 1], self.lens[r],
-                                  self.tail_k[ts:ts + 1], self.D, self.bits, self.D ** -0.5, block_bytes=1)
-            outs[a:b] = o[0].permute(1, 0, 2)
-        if nd < len(reqs):
-            jobs = [(i, p) for i in range(nd, len(reqs)) for p in pages_touched(self.lens[reqs[i]], seq_lens[i])]
-            js = torch.tensor([j[0] for j in jobs], dtype=torch.int32)
-            jp = torch.tensor([j[1] for j in jobs], dtype=torch.int32)
-            self.ops.write(k_all, v_all, torch.tensor(qsl, dtype=torch.int32), sl, ti, js, jp, self.cache, bt,
-                           self.tail_k)
-        for i, r in enumerate(reqs):
-            a, b = qsl[i], qsl[i + 1]
-            K, V = refs[i]
-            mask = torch.ones(b - a, K.shape[1], dtype=torch.bool).tril(diagonal=K.shape[1] - (b - a))
-            ref = F.scaled_dot_product_attention(q_all[a:b].permute(1, 0, 2), K.repeat_interleave(self.G, 0),
-                                                 V.repeat_interleave(self.G, 0), attn_mask=mask)
-            err = (outs[a:b] - ref.permute(1, 0, 2)).norm() / ref.norm()
-            assert err < 2e-5, (r, self.lens[r], b - a, float(err))
-            self.lens[r] = seq_lens[i]
-        for i, r in enumerate(reqs):                 # stored state == ground truth
-            a, b = qsl[i], qsl[i + 1]
-            ek, ev = self.exact[r]
-            ek = torch.cat([ek, k_all[a:b].permute(1, 0, 2)], 1)
-            ev = torch.cat([ev, v_all[a:b].permute(1, 0, 2)], 1)
-            self.exact[r] = (ek, ev)
-            n = seq_lens[i]
-            ts, rr, full = int(self.tail_idx[r]), n % PAGE, n // PAGE
-            assert torch.equal(self.tail_k[ts, :, :rr], ek[:, full * PAGE:])
-            if rr:
-                v = dequant_records(as_records(self.cache)[self.bt[r, full].long()], self.D, self.bits,
-                                    torch.float32)[1]
-                assert torch.allclose(v[:, :rr], ref_dequant(ev[:, full * PAGE:], self.bits, 2), atol=1e-5)
-            if full:
-                k, v = dequant_records(as_records(self.cache)[self.bt[r, :full].long()], self.D, self.bits,
-                                       torch.float32)
-                rk = ref_dequant(ek[:, :full * PAGE].reshape(self.H, full, PAGE, self.D).transpose(0, 1), self.bits, 2)
-                rv = ref_dequant(ev[:, :full * PAGE].reshape(self.H, full, PAGE, self.D).transpose(0, 1), self.bits, 3)
-                assert torch.allclose(k, rk, atol=1e-5) and torch.allclose(v, rv, atol=1e-5)
+    # ---------------------------------------------------------------- one step
+    def step(self, ids: list, qlens: list) -> None:
+        H, D, G = self.H, self.D, self.G
+        starts = [0]
+        for q in qlens:
+            starts.append(starts[-1] + q)
+        rows = starts[-1]
+        k = torch.randn(rows, H, D)
+        fused = torch.zeros(rows, 3 * H * D)                 # V lives in the last third of a qkv buffer
+        fused[:, 2 * H * D:] = torch.randn(rows, H * D)
+        v = fused[:, 2 * H * D:].view(rows, H, D)
+        q = torch.randn(rows, H * G, D)
+        before = [self.reqs[r].n for r in ids]
+        for r, ql in zip(ids, qlens):
+            self._grow(r, self.reqs[r].n + ql)
+        table = self._table(ids)
+        lens = torch.tensor([n + ql for n, ql in zip(before, qlens)], dtype=torch.int32)
+        slots = torch.tensor([self.reqs[r].slot for r in ids], dtype=torch.int32)
+        n_dec = next((i for i, ql in enumerate(qlens) if ql > 1), len(qlens))     # decodes come first
+        out = torch.zeros_like(q)
+        expect = {}
+        if n_dec:
+            self.ops.append(k[:n_dec], v[:n_dec], lens[:n_dec], slots[:n_dec], self.pool, table[:n_dec],
+                            self.tail_k, pos_offset=-1, advance=False)
+            self.ops.decode(q[:n_dec].contiguous(), out[:n_dec], self.pool, table[:n_dec], lens[:n_dec],
+                            slots[:n_dec], self.tail_k, D ** -0.5)
+            for i in range(n_dec):                            # the appended token is part of the cache
+                expect[i] = self._stored(ids[i], int(lens[i]))
+        for i in range(n_dec, len(ids)):
+            a, b = starts[i], starts[i + 1]
+            hk, hv = self._stored(ids[i], before[i])
+            chunk_k, chunk_v = k[a:b].transpose(0, 1), v[a:b].transpose(0, 1)
+            expect[i] = (torch.cat([hk, chunk_k], 1), torch.cat([hv, chunk_v], 1))
+            slot = self.reqs[ids[i]].slot
+            o = history_attention(q[a:b].transpose(0, 1)[None], chunk_k[None], chunk_v[None], as_records(self.pool),
+                                  table[i:i + 1], before[i], self.tail_k[slot:slot + 1], D, self.bits, D ** -0.5,
+                                  block_bytes=1)
+            out[a:b] = o[0].transpose(0, 1)
+        if n_dec < len(ids):
+            jobs = [(i, pg) for i in range(n_dec, len(ids)) for pg in pages_touched(before[i], int(lens[i]))]
+            self.ops.write(k, v, torch.tensor(starts, dtype=torch.int32), lens, slots,
+                           torch.tensor([j for j, _ in jobs], dtype=torch.int32),
+                           torch.tensor([pg for _, pg in jobs], dtype=torch.int32), self.pool, table, self.tail_k)
+        for i, r in enumerate(ids):
+            a, b = starts[i], starts[i + 1]
+            want = _attention64(q[a:b], *expect[i], G, D ** -0.5)
+            err = float((out[a:b].double() - want).norm() / want.norm())
+            assert err < 2e-5, (r, before[i], b - a, err)
+            self.reqs[r].k += list(k[a:b])
+            self.reqs[r].v += list(v[a:b])
+            self._check_stored(r)
+
+    def _check_stored(self, r: int) -> None:
+        """Tail rows hold the partial page's exact K; every full page's record is the reference test's
+        quantization of the exact tokens (codes, scales, biases bit for bit: K per channel over the
+        page, V per token), and the partial page's V rows too."""
+        req, D, bits = self.reqs[r], self.D, self.bits
+        K, V = torch.stack(req.k, 1), torch.stack(req.v, 1)          # [H, n, D]
+        full, part = req.n // PAGE, req.n % PAGE
+        assert torch.equal(self.tail_k[req.slot, :, :part], K[:, full * PAGE:])
+        recs = as_records(self.pool)
+        for pg in range(full + (1 if part else 0)):
+            kq, ks, kb, vq, vs, vb = split_record(recs[req.blocks[pg]], D, bits)
+            n = PAGE if pg < full else part
+            rows = slice(pg * PAGE, pg * PAGE + n)
+            cv, sv, bv = ref_quantize(V[:, rows], bits, dim=2)
+            assert torch.equal(vq[:, :n], cv) and torch.equal(vs[:, :n], sv[..., 0]) and torch.equal(vb[:, :n], bv[..., 0])
+            if pg < full:
+                ck, sk, bk = ref_quantize(K[:, rows], bits, dim=1)
+                assert torch.equal(kq, ck) and torch.equal(ks, sk[:, 0]) and torch.equal(kb, bk[:, 0])
+
+
+def _attention64(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, G: int, scale: float) -> torch.Tensor:
+    """float64 attention of the T queries q [T, H*G, D] -- the last T of the n keys K, V [H, n, D], each
+    seeing the keys up to its own position -- as [T, H*G, D]."""
+    T, n = q.shape[0], K.shape[1]
+    Kx, Vx = K.double().repeat_interleave(G, 0), V.double().repeat_interleave(G, 0)
+    s = torch.einsum("thd,hjd->htj", q.double(), Kx) * scale
+    visible = torch.arange(n)[None, :] <= (torch.arange(T)[:, None] + n - T)
+    s = s.masked_fill(~visible, float("-inf"))
+    return torch.einsum("htj,hjd->thd", torch.softmax(s, -1), Vx)
 
 
 @pytest.mark.parametrize("D,G", [(64, 3), (128, 4)])
 @pytest.mark.parametrize("bits", [4, 8])
 def test_ragged_mixed_batches(bits, D, G):
-    """Chunked prefill and decode mixed in one step over scattered blocks (tests/test_ragged.py:139-151)."""
+    """Chunked prefill and decode mixed in one step over scattered blocks (tests/test_ragged.py:139-151):
+    two first steps of chunks of different sizes, then 40 random steps of decodes plus chunks."""
     torch.manual_seed(0)
     rng = random.Random(2)
-    sim = Sim(D, bits, H=2, G=G, n_req=5)
-    sim.step([0, 1, 2], [70, 33, 5])
-    sim.step([3, 4], [31, 64])
+    host = RaggedHost(D, bits, H=2, G=G, n_req=5)
+    host.step([0, 1, 2], [70, 33, 5])
+    host.step([3, 4], [31, 64])
     for _ in range(40):
         dec = [r for r in range(5) if rng.random() < 0.7]
         chk = [r for r in range(5) if r not in dec and rng.random() < 0.5]
-        if not dec + chk:
-            continue
-        sim.step(dec + chk, [1] * len(dec) + [rng.randint(2, 40) for _ in chk])
+        if dec or chk:
+            host.step(dec + chk, [1] * len(dec) + [rng.randint(2, 40) for _ in chk])
 
 
 def test_rotation_lowers_attention_error():
