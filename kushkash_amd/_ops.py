@@ -66,6 +66,12 @@ class KernelConfig:
                 "fwht": f"fwht_kernel<{D},{IN}>", "unpack": f"unpack_kernel<{D},{B},{IN}>"}
 
 
+def _require(ok: bool, message: str) -> None:
+    """The reference's argument errors are ValueErrors (_ops.py:109-168)."""
+    if not ok:
+        raise ValueError(message)
+
+
 def _validate_default() -> bool:
     return os.environ.get("KUSHKASH_AMD_VALIDATE", "0") not in ("", "0")
 
@@ -252,13 +258,11 @@ class Ops:
         (_ops.py:104-126); out (contiguous, x's shape and dtype) may be x. H @ H = I, so it also
         rotates back. Same rotation as rotate(x, hadamard(D)) up to fp32 rounding."""
         D = self.D
-        if x.shape[-1] != D or not x.is_contiguous():
-            raise ValueError(f"fwht: x must be contiguous with last dim {D}")
+        _require(x.shape[-1] == D and x.is_contiguous(), f"fwht: x needs {D} contiguous elements per row")
+        _require(x.dtype == self.dtype, f"fwht: x is {x.dtype}; these kernels were built for {self.dtype}")
         out = torch.empty_like(x) if out is None else out
-        if out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
-            raise ValueError("fwht: out must be contiguous, with x's shape and dtype")
-        if x.dtype != self.dtype:
-            raise ValueError(f"fwht: x is {x.dtype}, these kernels take {self.dtype}")
+        _require(out.is_contiguous() and out.shape == x.shape and out.dtype == x.dtype,
+                 "fwht: out must be a contiguous tensor of x's shape and dtype")
         self._on_device(x=x, out=out)
         rows = x.numel() // D
         if rows:
@@ -275,31 +279,27 @@ class Ops:
         and the new chunk (row j of k_new / v_new [n, Hkv, D] -> row new_dst[j]). int32 index tensors. rot:
         rotate history back (canonical Walsh-Hadamard); new rows are copied as they are. Dequantization:
         fma(code, scale, bias) in fp32, rounded once to kp's dtype. Rows no entry names stay untouched."""
-        H, D = kp.shape[1], self.D
+        H, D = kp.shape[1] if kp.dim() == 3 else -1, self.D
         n_pages, n_tail, n_new = page_blk.numel(), tail_blk.numel(), new_dst.numel()
-        for t in (page_blk, page_dst, tail_blk, tail_info, new_dst):
-            if t.dtype != torch.int32 or not t.is_contiguous():
-                raise ValueError("unpack: index tensors must be contiguous int32")
-        if not (kp.is_contiguous() and vp.is_contiguous() and kp.shape == vp.shape and kp.dim() == 3
-                and kp.shape[2] == D):
-            raise ValueError("unpack: kp / vp must be contiguous [rows, Hkv, D]")
-        for t in (k_new, v_new):
-            if t.dim() != 3 or t.shape[1:] != (H, D) or t.stride(2) != 1 or t.stride(1) != D:
-                raise ValueError("unpack: k_new / v_new must be [n, Hkv, D] with unit dim stride and head stride D")
-        if tail_info.numel() != 3 * n_tail or k_new.shape[0] < n_new or v_new.shape[0] < n_new:
-            raise ValueError("unpack: tail_info must hold 3 ints per partial page; k_new / v_new one row per new_dst")
-        if page_dst.numel() != n_pages:
-            raise ValueError("unpack: page_dst must hold one row per page_blk entry")
+        index = (page_blk, page_dst, tail_blk, tail_info, new_dst)
+        _require(all(t.dtype == torch.int32 and t.is_contiguous() for t in index),
+                 "unpack: page_blk, page_dst, tail_blk, tail_info and new_dst must be contiguous int32")
+        _require(kp.dim() == 3 and kp.shape[2] == D and vp.shape == kp.shape and kp.is_contiguous()
+                 and vp.is_contiguous(), f"unpack: kp and vp must be contiguous [rows, Hkv, {D}] of one shape")
+        _require(all(t.dim() == 3 and t.shape[1:] == (H, D) and t.stride(2) == 1 and t.stride(1) == D
+                     for t in (k_new, v_new)),
+                 f"unpack: k_new and v_new must be [n, {H}, {D}] rows (unit dim stride, head stride {D})")
+        _require(page_dst.numel() == n_pages, "unpack: page_dst needs one destination row per page_blk entry")
+        _require(tail_info.numel() == 3 * n_tail, "unpack: tail_info needs (first row, tokens, slot) per tail_blk entry")
+        _require(k_new.shape[0] >= n_new and v_new.shape[0] >= n_new, "unpack: k_new and v_new need a row per new_dst entry")
         for t in (tail_k, k_new, v_new, kp, vp):
-            if t.dtype != self.dtype:
-                raise ValueError(f"unpack: tail_k, k_new, v_new, kp, vp must be {self.dtype}, got {t.dtype}")
+            _require(t.dtype == self.dtype, f"unpack: tail_k, k_new, v_new, kp and vp must be {self.dtype}, got {t.dtype}")
         bs, hs = _byte_strides(cache)
-        if cache.dim() < 2 or cache.shape[1] < H:
-            raise ValueError("cache must be [blocks, >= Hkv, ...]")
-        if (cache.data_ptr() | bs | hs) % 16:
-            raise ValueError("cache records must be 16-byte aligned (pointer, block and head strides)")
-        if tail_k.dim() != 4 or tail_k.shape[1:] != (H, PAGE, D) or not tail_k.is_contiguous():
-            raise ValueError(f"tail_k must be contiguous [slots, {H}, {PAGE}, {D}]")
+        _require(cache.dim() >= 2 and cache.shape[1] >= H, "cache must be [blocks, >= Hkv, ...]")
+        _require((cache.data_ptr() | bs | hs) % 16 == 0,
+                 "cache records must start 16-byte aligned (pointer, block and head strides)")
+        _require(tail_k.dim() == 4 and tail_k.shape[1:] == (H, PAGE, D) and tail_k.is_contiguous(),
+                 f"tail_k must be contiguous [slots, {H}, {PAGE}, {D}]")
         self._on_device(cache=cache, page_blk=page_blk, page_dst=page_dst, tail_blk=tail_blk, tail_info=tail_info,
                         tail_k=tail_k, k_new=k_new, v_new=v_new, new_dst=new_dst, kp=kp, vp=vp)
         if n_pages + n_tail + n_new == 0:

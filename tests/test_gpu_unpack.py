@@ -112,8 +112,8 @@ def test_packed_prefill_matches_attend_chunk():
     full pages and a partial one, K from the tail slot) followed by its new chunk -- unpacks to the
     exact dequantization of those records (bit for bit, the fp64 restatement), and attention per
     sequence over its packed rows, causal from the history's end, agrees with attend_chunk over the
-    same cache. attend_chunk dequantizes with the reference's torch path, in bf16 (code * scale and
-    + bias each rounded), so the two differ by that rounding: max-abs within 2e-2."""
+    same cache. attend_chunk unpacks its history blocks with the same kernel but rotates them back and
+    blocks the keys differently, so the two differ by rounding: max-abs within 2e-2."""
     import torch.nn.functional as F
     from _unpack_fixture import unpack_torch
     from kushkash_amd._ops import PAGE
