@@ -581,6 +581,140 @@ __device__ __forceinline__ float fetch(const float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Two or four consecutive partial floats past the local L2 (64-bit relaxed agent-scope loads).
+__device__ __forceinline__ void fetch2(const float* p, float& a, float& b) {
+    const uint64_t v = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    a = __uint_as_float((uint32_t)v);
+    b = __uint_as_float((uint32_t)(v >> 32));
+}
+__device__ __forceinline__ f4 fetch4(const float* p) {
+    float a, b, c, d;
+    fetch2(p, a, b);
+    fetch2(p + 2, c, d);
+    return f4{a, b, c, d};
+}
+
+// (m, l) of two disjoint key sets in log2 units folded into one: the sums rescaled to the larger
+// max; a side over no keys (m = -inf) adds nothing.
+__device__ __forceinline__ void fold_ml(float& m, float& l, float m2, float l2) {
+    const float M = __builtin_fmaxf(m, m2);
+    const float a = m == -__builtin_inff() ? 0.0f : l * __builtin_amdgcn_exp2f(m - M);
+    const float b = m2 == -__builtin_inff() ? 0.0f : l2 * __builtin_amdgcn_exp2f(m2 - M);
+    m = M;
+    l = a + b;
+}
+
+// LDS floats the split merge needs: m and l of every (split, head), each head's (M, L), and the
+// threads' partial sums.
+__host__ __device__ constexpr int merge_red_offset(int NS, int gn) {      // 16-byte aligned partial sums
+    return (2 * NS * gn + 2 * 16 + 3) & ~3;
+}
+__host__ __device__ constexpr int merge_smem_floats(int NS, int gn, int NW) {
+    return merge_red_offset(NS, gn) + NW * WAVE * 4;
+}
+
+// Merge of the NS split partials of one (sequence, kv head) -- rows (base + z) * G + g of part_ml
+// [..][2] and part_o [..][D] -- for the heads g0 .. g0 + gn - 1 (gn <= 16), by the NW * 64 threads of
+// the calling workgroup, in a fixed order (the same bits on every call), with many loads in flight
+// instead of one dependent chain per split:
+//   1. every (split, head)'s (m, l) is loaded (batches of independent loads) into smem; per head,
+//      ZG1 = T / gn thread groups fold the splits zg, zg + ZG1, ... and the groups' results fold in
+//      group order into (M_g, L_g);
+//   2. out[g][d..d+3] = sum_z exp2(m_z - M_g) o_z[g][d..d+3] / L_g: thread j owns output quad j % NQ
+//      over the splits z = j / NQ + k ZG (ZG = T / NQ groups), loads in batches, summed in z order;
+//      the groups' sums add in group order.
+// emit(g, d, f4) receives each merged quad (zeros for a head no split saw). smem holds
+// merge_smem_floats(NS, gn, NW) floats. Ends with the workgroup synchronized.
+template <int D, int NW, typename Emit>
+__device__ void merge_splits(const float* __restrict__ part_ml, const float* __restrict__ part_o, int64_t base,
+                             int NS, int G, int g0, int gn, float* smem, Emit&& emit) {
+    constexpr int T = NW * WAVE, NQ1 = D / 4, B = 8;
+    const int t = (int)threadIdx.x;
+    const int P = NS * gn;
+    float* const ms = smem;                        // [NS][gn]
+    float* const ls = smem + P;                    // [NS][gn]
+    float* const ML = smem + 2 * P;                // [16][2]
+    float* const red = smem + merge_red_offset(NS, gn);   // [T][4]
+    for (int p0 = t; p0 < P; p0 += B * T) {
+        float bm[B], bl[B];
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const int p = p0 + u * T;
+            bm[u] = -__builtin_inff();
+            bl[u] = 0.0f;
+            if (p < P) fetch2(part_ml + 2 * ((base + p / gn) * G + g0 + p % gn), bm[u], bl[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+            const int p = p0 + u * T;
+            if (p < P) {
+                ms[p] = bm[u];
+                ls[p] = bl[u];
+            }
+        }
+    }
+    __syncthreads();
+    const int ZG1 = T / gn;
+    if (t < gn * ZG1) {
+        const int g = t % gn, zg = t / gn;
+        float m = -__builtin_inff(), l = 0.0f;
+        for (int z = zg; z < NS; z += ZG1) fold_ml(m, l, ms[z * gn + g], ls[z * gn + g]);
+        red[2 * t] = m;
+        red[2 * t + 1] = l;
+    }
+    __syncthreads();
+    if (t < gn) {
+        float m = -__builtin_inff(), l = 0.0f;
+        for (int zg = 0; zg < ZG1; ++zg) fold_ml(m, l, red[2 * (zg * gn + t)], red[2 * (zg * gn + t) + 1]);
+        ML[2 * t] = m;
+        ML[2 * t + 1] = l;
+    }
+    __syncthreads();
+
+    const int NQ = gn * NQ1;                       // output quads
+    const int ZG = NQ >= T ? 1 : T / NQ;           // split groups
+    for (int j = t; j < NQ * ZG; j += T) {
+        const int q = j % NQ, zg = j / NQ, g = q / NQ1, d = 4 * (q % NQ1);
+        const float M = ML[2 * g], L = ML[2 * g + 1];
+        f4 acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (M > -__builtin_inff()) {
+            for (int z0 = zg; z0 < NS; z0 += B * ZG) {
+                f4 v[B];
+                float wz[B];
+#pragma unroll
+                for (int u = 0; u < B; ++u) {
+                    const int z = z0 + u * ZG;
+                    v[u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+                    wz[u] = 0.0f;
+                    if (z < NS) {
+                        const float mzg = ms[z * gn + g];
+                        if (mzg > -__builtin_inff()) {
+                            v[u] = fetch4(part_o + ((base + z) * G + g0 + g) * D + d);
+                            wz[u] = __builtin_amdgcn_exp2f(mzg - M);
+                        }
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < B; ++u) acc += wz[u] * v[u];
+            }
+        }
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        if (ZG == 1) {
+            emit(g, d, acc * inv);
+        } else {
+            *reinterpret_cast<f4*>(red + 4 * j) = acc * inv;
+        }
+    }
+    __syncthreads();
+    if (ZG > 1 && t < NQ) {
+        f4 sum = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int zg = 0; zg < ZG; ++zg) sum += *reinterpret_cast<const f4*>(red + 4 * (zg * NQ + t));
+        emit(t / NQ1, 4 * (t % NQ1), sum);
+    }
+    __syncthreads();
+}
+
 // grid (S, Hkv, n_splits * ceil(G / 16)), block NW * 64. Registers are budgeted for two waves per SIMD
 // (amdgpu_waves_per_eu(2); the library is built with MFMA accumulators in VGPRs): with a 512-register
 // budget the 4-wave variant used 236 VGPRs + 76 AGPRs and spent 46 v_accvgpr moves per page in its
@@ -1023,7 +1157,20 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     __syncthreads();
     if (!*last_flag) return;
     const int64_t base = ((int64_t)s * H + h) * NS;
-    for (int i = threadIdx.x; i < Gc * D; i += NW * WAVE) {
+    if (merge_smem_floats(NS, Gc, NW) * 4 <= 2 * NW * R::SLOT) {      // the idle first ring holds the scratch
+        merge_splits<D, NW>(part_ml, part_o, base, NS, G, g0, Gc, reinterpret_cast<float*>(ringA),
+                            [&](int g, int d, f4 v) {
+                                if constexpr (ROT) {
+                                    *reinterpret_cast<f4*>(ostage + g * D + d) = v;
+                                } else {
+#pragma unroll
+                                    for (int i = 0; i < 4; ++i) out[qbase + g * D + d + i] = from_f32<IN>(v[i]);
+                                }
+                            });
+        if constexpr (ROT) store_rotated<D, IN, NW * WAVE>(out + qbase, ostage, Gc, out_vec);
+        return;
+    }
+    for (int i = threadIdx.x; i < Gc * D; i += NW * WAVE) {      // one dependent chain per split (large NS)
         const int g = g0 + i / D, d = i % D;
         float Mg = -__builtin_inff();
         for (int zz = 0; zz < NS; ++zz) Mg = __builtin_fmaxf(Mg, fetch(part_ml + 2 * ((base + zz) * G + g)));
@@ -1072,30 +1219,48 @@ __device__ __forceinline__ float combine_one(const float* __restrict__ part_ml, 
     return L > 0.0f ? o / L : 0.0f;
 }
 
-// grid (S, Hkv), block 256: merge split-K partials (M, L, unnormalized O) into the output.
-// M is in log2 units. Splits with no tokens (M = -inf) are skipped (gpu.mojo:469-491). ROT: the
-// merged rows, 16 heads at a time, are rotated back through LDS before their one rounding.
+// grid (S, Hkv), block 256: merge split-K partials (M, L, unnormalized O) into the output, 16 heads
+// at a time. M is in log2 units; splits with no tokens (M = -inf) add nothing (gpu.mojo:469-491).
+// parallel: merge_splits over the dynamic LDS (merge_smem_floats(NS, 16, 4) floats at most); else one
+// dependent chain per element (very large NS). ROT: each chunk's merged rows are rotated back through
+// LDS before their one rounding.
 template <int D, typename IN, bool ROT>
 __global__ __launch_bounds__(256) void combine_kernel(IN* __restrict__ out, const float* __restrict__ part_ml,
-                                                      const float* __restrict__ part_o, int NS, int H, int G) {
+                                                      const float* __restrict__ part_o, int NS, int H, int G,
+                                                      int parallel) {
+    extern __shared__ float merge_lds[];
+    __shared__ float stage[ROT ? 16 * D : 1];
     const int s = blockIdx.x, h = blockIdx.y;
     const int64_t base = ((int64_t)s * H + h) * NS;
     IN* const orow = out + ((int64_t)s * H + h) * G * D;
-    if constexpr (ROT) {
-        __shared__ float stage[16 * D];
-        const bool vec = (((uintptr_t)out) & 15) == 0;
-        for (int g0 = 0; g0 < G; g0 += 16) {
-            const int gn = min(16, G - g0);
-            for (int i = threadIdx.x; i < gn * D; i += 256)
-                stage[i] = combine_one(part_ml, part_o, base, NS, G, D, g0 + i / D, i % D);
+    const bool vec = (((uintptr_t)out) & 15) == 0;
+    for (int g0 = 0; g0 < G; g0 += 16) {
+        const int gn = min(16, G - g0);
+        if (parallel) {
+            merge_splits<D, 4>(part_ml, part_o, base, NS, G, g0, gn, merge_lds, [&](int g, int d, f4 v) {
+                if constexpr (ROT) {
+                    *reinterpret_cast<f4*>(stage + g * D + d) = v;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) orow[(int64_t)(g0 + g) * D + d + i] = from_f32<IN>(v[i]);
+                }
+            });
+        } else {
+            for (int i = threadIdx.x; i < gn * D; i += 256) {
+                const float val = combine_one(part_ml, part_o, base, NS, G, D, g0 + i / D, i % D);
+                if constexpr (ROT) {
+                    stage[i] = val;
+                } else {
+                    orow[(int64_t)g0 * D + i] = from_f32<IN>(val);
+                }
+            }
             __syncthreads();
+        }
+        if constexpr (ROT) {
             store_rotated<D, IN, 256>(orow + (int64_t)g0 * D, stage, gn, vec);
             __syncthreads();
         }
-        return;
     }
-    for (int i = threadIdx.x; i < G * D; i += 256)
-        orow[i] = from_f32<IN>(combine_one(part_ml, part_o, base, NS, G, D, i / D, i % D));
 }
 
 // Launch of one decode configuration. Defined (and instantiated) only in kush_decode_inst.hip, compiled

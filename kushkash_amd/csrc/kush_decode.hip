@@ -124,7 +124,11 @@ extern "C" int kush_combine_ex(int head_dim, int group, int dtype, void* out, co
         using IN = decltype(in);
         if (n_seqs == 0) return 0;
         auto kern = rot ? combine_kernel<D, IN, true> : combine_kernel<D, IN, false>;
-        kern<<<dim3(n_seqs, hkv), dim3(256), 0, (hipStream_t)stream>>>((IN*)out, part_ml, part_o, n_splits, hkv, group);
+        // the parallel merge when its LDS scratch fits in 48 KB of dynamic LDS
+        const int64_t lds = (int64_t)merge_smem_floats(n_splits, group < 16 ? group : 16, 4) * 4;
+        const int parallel = lds <= 48 * 1024;
+        kern<<<dim3(n_seqs, hkv), dim3(256), parallel ? (size_t)lds : 0, (hipStream_t)stream>>>(
+            (IN*)out, part_ml, part_o, n_splits, hkv, group, parallel);
         return kush_check_launch("kush_combine");
     });
 }

@@ -115,3 +115,22 @@ def test_c4_full_size(c4, ns, merge, monkeypatch):
                ns, work, waves=waves)
     check(out, c4["ref"], f"C4 ns={ns} {merge}")
     assert int(ops._sync.abs().sum()) == 0
+
+
+@pytest.mark.parametrize("ns", [0, 64])
+def test_c4_repeated_steps_are_bit_identical(c4, ns):
+    """The same C4 decode step twice gives the same bits: every wave count sums a fixed set of pages in
+    a fixed order, and the split merge folds the splits in a fixed order (reference: gpu.mojo:566-807
+    assigns pages to warps statically)."""
+    ops, B, Hkv, G, D, N = c4["ops"], c4["B"], c4["Hkv"], c4["G"], c4["D"], c4["N"]
+    ns = ns or ops.splits(B, Hkv, N // PAGE)
+    waves = ops.waves(B, Hkv, ns, N // PAGE)
+    work = torch.empty(B * Hkv * ns * G * (D + 2), dtype=torch.float32, device=DEV)
+    outs = []
+    for _ in range(3):
+        out = torch.empty_like(c4["q"])
+        ops.decode(c4["q"], out, c4["cache"], c4["table"], c4["sl"], c4["tail_idx"], c4["tail_k"],
+                   1.0 / math.sqrt(D), ns, work, waves=waves)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
