@@ -619,11 +619,11 @@ __host__ __device__ constexpr int merge_smem_floats(int NS, int gn, int NW) {
 // the calling workgroup, in a fixed order (the same bits on every call), with many loads in flight
 // instead of one dependent chain per split:
 //   1. every (split, head)'s (m, l) is loaded (batches of independent loads) into smem; per head,
-//      ZG1 = T / gn thread groups fold the splits zg, zg + ZG1, ... and the groups' results fold in
-//      group order into (M_g, L_g);
+//      ZG1 = min(T / gn, NS) thread groups fold the splits zg, zg + ZG1, ... and the groups' results
+//      fold in group order into (M_g, L_g);
 //   2. out[g][d..d+3] = sum_z exp2(m_z - M_g) o_z[g][d..d+3] / L_g: thread j owns output quad j % NQ
-//      over the splits z = j / NQ + k ZG (ZG = T / NQ groups), loads in batches, summed in z order;
-//      the groups' sums add in group order.
+//      over the splits z = j / NQ + k ZG (ZG = min(T / NQ, NS) groups), loads in batches, summed in z
+//      order; the groups' sums add in group order.
 // emit(g, d, f4) receives each merged quad (zeros for a head no split saw). smem holds
 // merge_smem_floats(NS, gn, NW) floats. Ends with the workgroup synchronized.
 template <int D, int NW, typename Emit>
@@ -655,7 +655,7 @@ __device__ void merge_splits(const float* __restrict__ part_ml, const float* __r
         }
     }
     __syncthreads();
-    const int ZG1 = T / gn;
+    const int ZG1 = max(1, min(T / gn, NS));       // split groups of phase 1 (no more than splits)
     if (t < gn * ZG1) {
         const int g = t % gn, zg = t / gn;
         float m = -__builtin_inff(), l = 0.0f;
@@ -673,7 +673,7 @@ __device__ void merge_splits(const float* __restrict__ part_ml, const float* __r
     __syncthreads();
 
     const int NQ = gn * NQ1;                       // output quads
-    const int ZG = NQ >= T ? 1 : T / NQ;           // split groups
+    const int ZG = NQ >= T ? 1 : max(1, min(T / NQ, NS));     // split groups of phase 2
     for (int j = t; j < NQ * ZG; j += T) {
         const int q = j % NQ, zg = j / NQ, g = q / NQ1, d = 4 * (q % NQ1);
         const float M = ML[2 * g], L = ML[2 * g + 1];

@@ -45,25 +45,37 @@ __global__ __launch_bounds__(256) void advance_kernel(int32_t* seq_lens, int pos
     }
 }
 
-// grid (n_jobs, Hkv), block write_threads<D>(): the write's mode 0. Job j covers logical page job_page[j] of
-// sequence job_seq[j], whose new rows [qsl[s], qsl[s+1]) sit at positions [ctx, seq_lens[s]):
-// write the page's new V rows and, if the page is complete, quantize its K (older rows from the
-// tail, newer from the chunk). Mode 1 (tail_kernel) then stashes the new K rows of still-partial
-// pages in the tail: two launches, so no tail is read and written by the same one.
+// Page tasks per chunk-write workgroup (256 threads): neighbouring kv heads of one page side by side.
+// A chunk write has thousands of small page tasks that the dispatcher starts over ~10 us; two per
+// workgroup halve the dispatches (C4 write 17.05 -> 16.86 us). More per workgroup lose: every
+// task then waits at each barrier for the slowest of them (8 per workgroup: 19.3 -> 20.3 us).
+template <int D>
+constexpr int write_tpb() { return 256 / write_threads<D>(); }
+
+// grid (ceil(n_jobs * Hkv / TPB)), block TPB * write_threads<D>(): the write's mode 0, task i =
+// (job i / Hkv, kv head i % Hkv). Job j covers logical page job_page[j] of sequence job_seq[j],
+// whose new rows [qsl[s], qsl[s+1]) sit at positions [ctx, seq_lens[s]): write the page's new V rows
+// and, if the page is complete, quantize its K (older rows from the tail, newer from the chunk).
+// Mode 1 (tail_kernel) then stashes the new K rows of still-partial pages in the tail: two
+// launches, so no tail is read and written by the same one.
 // FUSE (mode 2): mode 1 in the same launch. A sequence's tail is read only by the job of its first
 // touched page (page ctx / 32, when ctx % 32 != 0 and the page completes) and written only for its
 // last page (seq_lens / 32, when left partial). When both happen on different pages, the first
-// page's job writes the tail after its own reads (same workgroup, behind page_task's last barrier);
+// page's job writes the tail after its own reads (same task, behind page_task's last barrier);
 // otherwise the partial page's job does. Needs a job for every page the chunk touches.
 // Contract: gpu.mojo:241-276, cpu.mojo:273-304.
 template <int D, int BITS, typename IN, bool VEC, bool FUSE, bool ROT>
-__global__ __launch_bounds__(write_threads<D>()) void write_kernel(
+__global__ __launch_bounds__(256) void write_kernel(
     const IN* __restrict__ k, const IN* __restrict__ v, int64_t k_stride, int64_t v_stride,
     const int32_t* __restrict__ qsl, const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ tail_idx,
-    const int32_t* __restrict__ job_seq, const int32_t* __restrict__ job_page, uint8_t* __restrict__ cache,
+    const int32_t* __restrict__ job_seq, const int32_t* __restrict__ job_page, int n_jobs, uint8_t* __restrict__ cache,
     int64_t bs, int64_t hs, IN* __restrict__ tail_k, const int32_t* __restrict__ block_table, int64_t bt_stride, int H) {
-    __shared__ __align__(16) uint8_t lds[tile_bytes<D, IN>()];
-    const int j = blockIdx.x, h = blockIdx.y;
+    constexpr int TH = write_threads<D>(), TPB = write_tpb<D>();
+    __shared__ __align__(16) uint8_t lds[TPB * tile_bytes<D, IN>()];
+    const int sub = (int)threadIdx.x / TH, tid = (int)threadIdx.x % TH;
+    const int64_t task = (int64_t)blockIdx.x * TPB + sub;
+    const bool live = task < (int64_t)n_jobs * H;      // a task past the end still passes the barriers
+    const int j = live ? (int)(task / H) : 0, h = live ? (int)(task % H) : 0;
     const int s = job_seq[j];
     const int ps = job_page[j] * PAGE;
     const int q0 = qsl[s];
@@ -75,23 +87,22 @@ __global__ __launch_bounds__(write_threads<D>()) void write_kernel(
     const int64_t hoff = (int64_t)h * D;
     {
         uint8_t* rec = cache + (int64_t)block_table[(int64_t)s * bt_stride + ps / PAGE] * bs + (int64_t)h * hs;
-        const int hi = ps + PAGE < total ? ps + PAGE : total;
+        const int hi = !live ? lo : (ps + PAGE < total ? ps + PAGE : total);
         int split = ctx - ps;                               // K rows before it come from the tail
         split = split < 0 ? 0 : (split > PAGE ? PAGE : split);
-        page_task<D, BITS, IN, VEC, write_threads<D>(), ROT>(tail, k + (int64_t)(q0 + ps + split - ctx) * k_stride + hoff,
-                                                        k_stride, split, complete,
-                                                        v + (int64_t)(q0 + lo - ctx) * v_stride + hoff, v_stride,
-                                                        lo - ps, hi - ps, rec, lds);
+        page_task<D, BITS, IN, VEC, TH, ROT, true>(tail, k + (int64_t)(q0 + ps + split - ctx) * k_stride + hoff,
+                                                   k_stride, split, live && complete,
+                                                   v + (int64_t)(q0 + lo - ctx) * v_stride + hoff, v_stride, lo - ps,
+                                                   hi - ps, rec, lds + sub * tile_bytes<D, IN>(), tid);
     }
     if constexpr (FUSE) {
         const int last = total / PAGE, first = ctx / PAGE;
         const int owner = (ctx % PAGE != 0 && last != first) ? first : last;
-        if (total % PAGE != 0 && ps / PAGE == owner) {
+        if (live && total % PAGE != 0 && ps / PAGE == owner) {
             const int pl = last * PAGE;
             const int lo2 = pl > ctx ? pl : ctx;
-            stash_rows<D, IN, VEC, ROT, write_threads<D>()>(tail + (lo2 - pl) * D,
-                                                             k + (int64_t)(q0 + lo2 - ctx) * k_stride + hoff, k_stride,
-                                                             total - lo2, threadIdx.x);
+            stash_rows<D, IN, VEC, ROT, TH>(tail + (lo2 - pl) * D, k + (int64_t)(q0 + lo2 - ctx) * k_stride + hoff,
+                                            k_stride, total - lo2, tid);
         }
     }
 }
@@ -177,9 +188,11 @@ extern "C" int kush_write_ex(int head_dim, int bits, int dtype, const void* k, c
                 {{write_kernel<D, BITS, IN, true, false, false>, write_kernel<D, BITS, IN, true, false, true>},
                  {write_kernel<D, BITS, IN, true, true, false>, write_kernel<D, BITS, IN, true, true, true>}}};
             auto kern = table[vec][mode == 2][rot];
-            kern<<<dim3(n_jobs, hkv), dim3(write_threads<D>()), 0, st>>>(
+            constexpr int TPB = write_tpb<D>();
+            const int64_t tasks = (int64_t)n_jobs * hkv;
+            kern<<<dim3((unsigned)((tasks + TPB - 1) / TPB)), dim3(TPB * write_threads<D>()), 0, st>>>(
                 (const IN*)k, (const IN*)v, k_stride, v_stride, query_start_loc, seq_lens, tail_idx, job_seq, job_page,
-                (uint8_t*)cache, block_stride, head_stride, (IN*)tail_k, block_table, bt_stride, hkv);
+                n_jobs, (uint8_t*)cache, block_stride, head_stride, (IN*)tail_k, block_table, bt_stride, hkv);
         } else {
             auto kern = rot ? (vec ? tail_kernel<D, IN, true, true> : tail_kernel<D, IN, false, true>)
                             : (vec ? tail_kernel<D, IN, true, false> : tail_kernel<D, IN, false, false>);
