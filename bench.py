@@ -95,6 +95,9 @@ def parse_args(argv=None):
                          "instead of one fused launch")
     ap.add_argument("--config", default="c2", choices=("c1", "c2", "c3", "c4", "c4-write", "c4-unpack", "c4-fwht"),
                     help="which configuration to measure (c2: the headline line)")
+    ap.add_argument("--timeline", type=int, default=0, metavar="N",
+                    help="c2: run on libkushhip_timeline.so and print N launches' per-workgroup phase times by XCD "
+                         "(bf16, no rotation)")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "decode_c2_traffic.md"),
                     help="rocprofv3 counter summary whose 'traffic_bytes_per_launch' fills roofline.traffic")
     return ap.parse_args(argv)
@@ -699,6 +702,77 @@ def bench_c4_fwht(a) -> None:
           f"kush::fwht_kernel<{D}, kush::bf16_t, true>", traffic_md="fwht_c4_traffic.md")
 
 
+def bench_timeline(a) -> None:
+    """C2 decode on the timeline build (kushkash_amd/libkushhip_timeline.so: the same kernels, wave 0 of
+    each workgroup timestamping five phases, kush_decode.h KUSH_TIMELINE): after `--warmup` eager steps
+    per probed launch, one launch is recorded and summarized as markdown -- each phase's spread over
+    the workgroups (us from the first workgroup's start), and per XCD the page-loop time (first pair
+    landed -> pages done), the pages-done times and the shader clock over the loop."""
+    import ctypes
+    import importlib
+    import numpy as np
+    from kushkash_amd import _lib
+    kbuild = importlib.import_module("kushkash_amd.build")
+    if a.dtype != "bf16" or a.rot:
+        raise SystemExit("--timeline: the timeline build instruments the bf16, unrotated decode only")
+    if not kbuild.TIMELINE_LIB.exists():
+        raise SystemExit(f"--timeline: {kbuild.TIMELINE_LIB.name} is not built; run `python -m kushkash_amd.build`")
+    _lib.LIB = kbuild.TIMELINE_LIB
+    _lib.lib.cache_clear()
+    read = _lib.lib().kush_timeline_read
+    read.argtypes, read.restype = [ctypes.c_void_p, ctypes.c_int64], ctypes.c_int32
+    w = make_workload(a, "cuda:0")
+    ops, B, Hkv, G, D = w["ops"], w["B"], w["Hkv"], w["G"], w["D"]
+    ns = a.splits or ops.splits(B, Hkv, w["N"] // PAGE)
+    wv = a.waves or ops.waves(B, Hkv, ns, w["pages"])
+    kernel = decode_kernel_name(a.dim, a.bits, ops.dtype, wv, G, False)
+    out = torch.empty_like(w["q"])
+    work = torch.empty(max(1, B * Hkv * ns * G * (D + 2)), dtype=torch.float32, device="cuda:0")
+    sm = 1.0 / math.sqrt(D)
+
+    def step(i):
+        ops.decode(w["q"], out, w["cache"], w["tables"][i % len(w["tables"])], w["seq_lens"], w["tail_idx"],
+                   w["tail_k"], sm, ns, work, waves=wv)
+
+    rows = B * Hkv * ns                       # workgroups of the launch (G <= 16: one head chunk)
+    print(f"workload: C2 decode layer, {a.hq} q / {a.hkv} kv heads, D {a.dim}, int{a.bits}, batch {B} x {a.ctx} "
+          f"tokens, splits {ns}, waves {wv}\nkernel: {kernel}\nsources: {source_digest(kernel)}\n"
+          f"clocks: wall 100 MHz (s_memrealtime), shader clock (s_memtime); {rows} workgroups", flush=True)
+    for rep in range(a.timeline):
+        for i in range(a.warmup):
+            step(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        step(1)
+        e1.record()
+        torch.cuda.synchronize()
+        buf = np.zeros((rows, 8), dtype=np.int64)
+        rc = read(buf.ctypes.data_as(ctypes.c_void_p), rows)
+        if rc != 0:
+            raise RuntimeError(f"kush_timeline_read failed ({rc})")
+        t = buf.astype(np.float64)
+        us = (t[:, :5] - t[:, 0].min()) / 100.0
+        loop = us[:, 3] - us[:, 2]
+        mhz = (t[:, 6] - t[:, 5]) / np.maximum(loop, 1e-3)
+        xcd = t[:, 7].astype(int)
+        pct = lambda x, p: float(np.percentile(x, p))
+        print(f"\nlaunch {rep + 1} of {a.timeline}: HIP-event time {e0.elapsed_time(e1) * 1e3:.2f} us, first "
+              f"workgroup start -> last output stored {us[:, 4].max():.2f} us\n\n"
+              "| phase (us from the first start) | min | p10 | p50 | p90 | max |\n|---|---|---|---|---|---|")
+        for name, k in (("start", 0), ("prologue done", 1), ("first page pair landed", 2), ("pages done", 3),
+                        ("output stored", 4)):
+            x = us[:, k]
+            print(f"| {name} | {x.min():.2f} | {pct(x, 10):.2f} | {pct(x, 50):.2f} | {pct(x, 90):.2f} | {x.max():.2f} |")
+        print("\n| XCD | workgroups | page loop p10 / p50 / max (us) | pages done p50 / max (us) | "
+              "shader clock p50 (MHz) |\n|---|---|---|---|---|")
+        for x in range(8):
+            m = xcd == x
+            if m.any():
+                print(f"| {x} | {int(m.sum())} | {pct(loop[m], 10):.2f} / {pct(loop[m], 50):.2f} / {loop[m].max():.2f} | "
+                      f"{pct(us[m, 3], 50):.2f} / {us[m, 3].max():.2f} | {pct(mhz[m], 50):.0f} |", flush=True)
+
+
 def main(argv=None):
     a = parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -710,6 +784,11 @@ def main(argv=None):
     dev = "cuda:0"
     if a.calibrate_copy:
         copy_calibration(a)
+        return
+    if a.timeline:
+        if a.config != "c2":
+            raise SystemExit("--timeline instruments the c2 decode")
+        bench_timeline(a)
         return
     if a.config != "c2":
         {"c1": bench_c1, "c3": bench_c3, "c4": bench_c4, "c4-write": bench_c4_write, "c4-unpack": bench_c4_unpack,

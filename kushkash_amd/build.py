@@ -19,10 +19,17 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 LIB = PKG / "libkushhip.so"
 DIGEST = PKG / "libkushhip.so.digest"          # source digest of the library last built here
+# A profiling copy of the library: the same objects with the bf16 / rot 0 decode instantiations
+# recompiled with -DKUSH_TIMELINE (per-workgroup phase timestamps and XCD ids, kush_decode.h), read by
+# `python bench.py --timeline`. The product never loads it.
+TIMELINE_LIB = PKG / "libkushhip_timeline.so"
 SOURCES = ("kush_capi.hip", "kush_write.hip", "kush_decode.hip", "kush_rotate.hip",
            "kush_unpack.hip", "kush_decode_inst.hip")
 # the decode kernel instantiations: one object per (input dtype, rot)
 DECODE_INST = [{"KUSH_INST_IN": t, "KUSH_INST_ROT": r} for t in ("float", "_Float16", "kush::bf16_t") for r in (0, 1)]
+
+
+TIMELINE_UNIT = ("kush_decode_inst.hip", {"KUSH_INST_IN": "kush::bf16_t", "KUSH_INST_ROT": 0})
 
 
 def units() -> list[tuple[str, dict]]:
@@ -113,22 +120,27 @@ def _run(cmd: list[str], verbose: bool) -> None:
 
 
 def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compile every HIP source for gfx950 into LIB (always recompiles; objects in parallel, then one
-    link); returns the path."""
-    jobs = jobs or max(1, min(len(units()), int(os.environ.get("MAX_JOBS", 0)) or os.cpu_count() or 1))
+    """Compile every HIP source for gfx950 into LIB, and TIMELINE_LIB from the same objects with the
+    timeline unit instrumented (always recompiles; objects in parallel, then the links); returns LIB."""
+    todo = units() + [(TIMELINE_UNIT[0], dict(TIMELINE_UNIT[1], KUSH_TIMELINE=1))]
+    jobs = jobs or max(1, min(len(todo), int(os.environ.get("MAX_JOBS", 0)) or os.cpu_count() or 1))
     compile_flags = [f for f in FLAGS if f != "-shared"]
     with tempfile.TemporaryDirectory(prefix="kushkash_amd_build_") as tmpdir:
         objs, cmds = [], []
-        for i, (src, defs) in enumerate(units()):
+        for i, (src, defs) in enumerate(todo):
             obj = str(Path(tmpdir) / f"{i:02d}_{Path(src).stem}.o")
             objs.append(obj)
             cmds.append([hipcc(), *compile_flags, *(f"-D{k}={v}" for k, v in defs.items()), f"-I{ROOT / 'include'}",
                          "-c", str(PKG / "csrc" / src), "-o", obj])
         with ThreadPoolExecutor(jobs) as ex:
             list(ex.map(lambda c: _run(c, verbose), cmds))
-        tmp = LIB.with_suffix(".so.tmp")
-        _run([hipcc(), *FLAGS, "-o", str(tmp), *objs], verbose)
-    os.replace(tmp, LIB)
+        product = objs[:-1]
+        swap = units().index(TIMELINE_UNIT)
+        timeline = product[:swap] + objs[-1:] + product[swap + 1:]
+        for dst, parts in ((LIB, product), (TIMELINE_LIB, timeline)):
+            tmp = dst.with_suffix(".so.tmp")
+            _run([hipcc(), *FLAGS, "-o", str(tmp), *parts], verbose)
+            os.replace(tmp, dst)
     import json
     DIGEST.write_text(json.dumps({"all": source_digest(), **{u: source_digest(u) for u in SOURCES}}, indent=1) + "\n")
     return LIB

@@ -43,6 +43,33 @@
 
 namespace kush {
 
+// Timeline build (-DKUSH_TIMELINE: the instrumented copy of one instantiation unit linked into
+// libkushhip_timeline.so, never the product library). Wave 0 of each workgroup records, per launch,
+// the 100 MHz wall clock at five points -- 0 start, 1 prologue done (first page DMAs about to go out),
+// 2 its first page pair landed, 3 its pages done, 4 its output stored -- in slots 0-4 of the
+// workgroup's row of 8, the shader clock at points 2 and 3 in slots 5 and 6, and the XCD it ran on
+// (hardware register XCC_ID) in slot 7. Rows beyond TIMELINE_ROWS are not recorded. The stores are
+// ordinary vector stores of wave 0 (every lane the same value).
+#ifdef KUSH_TIMELINE
+constexpr int TIMELINE_ROWS = 1 << 16;
+static __device__ long long g_timeline[TIMELINE_ROWS * 8];
+__device__ __forceinline__ void timeline_mark(int k) {
+    if (__builtin_amdgcn_readfirstlane(threadIdx.x) < WAVE) {    // wave 0: a wave-uniform branch
+        const long long row = ((long long)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+        if (row < TIMELINE_ROWS) {
+            long long* const r = g_timeline + row * 8;
+            r[k] = wall_clock64();
+            if (k == 0) r[7] = __builtin_amdgcn_s_getreg((3 << 11) | 20);     // XCC_ID bits [3:0]
+            if (k == 2) r[5] = clock64();
+            if (k == 3) r[6] = clock64();
+        }
+    }
+}
+#define KUSH_MARK(k) timeline_mark(k)
+#else
+#define KUSH_MARK(k) ((void)0)
+#endif
+
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
@@ -757,6 +784,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     float* const l_l = m_l + NW * 16;
     int* const last_flag = reinterpret_cast<int*>(l_l + NW * 16);
 
+    KUSH_MARK(0);
     const int lane = threadIdx.x & (WAVE - 1);
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);   // wave-uniform: scalar page loop
     const int r16 = lane & 15, q = lane >> 4;
@@ -919,6 +947,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         const float sa = rs * TWO24;                             // x = sa s + kx
         int pa = w, pb = NW + w;                                         // the pairs in slots (0, 1), (2, 3)
         __syncthreads();
+        KUSH_MARK(1);
         KUSH_ISSUE_PAIR(sl0, sl1, pa)
         KUSH_ISSUE_PAIR(sl2, sl3, pb)
 
@@ -931,6 +960,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     {                                                                                              \
         if ((P) >= pairs) break;                                                                   \
         KUSH_WAIT_VM(2 * R::DMA);                                                                  \
+        if ((P) == 0) KUSH_MARK(2);                                                                \
         const int nx = (P) + 2 * NW;                     /* this wave's pair after next */          \
         int2 id2;                                                                                  \
         if constexpr (ST == 2) {                                                                   \
@@ -977,6 +1007,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
 #undef KUSH_STEP
 #undef KUSH_ISSUE_PAIR
     }
+    KUSH_MARK(3);
 
     // partial last page (last split only): V rows from its record, staged by one wave in its slot 0;
     // exact fp32 K . q scores from the tail, spread over all waves (lane: token lane % 32, heads
@@ -1134,6 +1165,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         __syncthreads();
         store_rotated<D, IN, NW * WAVE>(out + qbase, ostage, Gc, out_vec);
     }
+    KUSH_MARK(4);
     if (NS > 1 && w == 0 && q == 0 && r16 < Gc) {
         publish(part_ml + 2 * pb, M);
         publish(part_ml + 2 * pb + 1, L);

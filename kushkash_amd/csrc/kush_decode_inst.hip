@@ -28,3 +28,13 @@ __attribute__((used)) void* const launchers[] = {
 
 }  // namespace
 }  // namespace kush
+
+#ifdef KUSH_TIMELINE
+// Timeline build only: copies the first `rows` rows (8 int64 each) of this unit's timeline records
+// to host memory `dst` (kush_decode.h, KUSH_TIMELINE). 0 on success, else the HIP error code.
+extern "C" int kush_timeline_read(void* dst, int64_t rows) {
+    if (rows < 0 || rows > kush::TIMELINE_ROWS) return (int)hipErrorInvalidValue;
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(kush::g_timeline), (size_t)rows * 8 * sizeof(long long), 0,
+                                    hipMemcpyDeviceToHost);
+}
+#endif

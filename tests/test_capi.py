@@ -88,6 +88,21 @@ def test_library_exports_every_header_symbol(lib):
     assert set(_lib.SIGNATURES) == set(header_functions())
 
 
+def test_timeline_build_is_the_library_plus_its_reader(lib):
+    """libkushhip_timeline.so (bench.py --timeline) exports every entry point of the header and the
+    timeline reader; the product library has no reader (its kernels record nothing)."""
+    import importlib
+    kbuild = importlib.import_module("kushkash_amd.build")
+    if not kbuild.TIMELINE_LIB.exists():
+        kushkash_amd.build()
+    tl = ctypes.CDLL(str(kbuild.TIMELINE_LIB))
+    for name in header_functions():
+        assert hasattr(tl, name), name
+    assert tl.kush_abi_version() == _lib.ABI_VERSION
+    assert hasattr(tl, "kush_timeline_read")
+    assert not hasattr(ctypes.CDLL(str(_lib.LIB)), "kush_timeline_read")
+
+
 def test_abi_version(lib):
     m = re.search(r"ABI revision of this header \((\d+)\)", HEADER.read_text())
     assert m and int(m.group(1)) == lib.kush_abi_version() == _lib.ABI_VERSION
