@@ -704,10 +704,11 @@ def bench_c4_fwht(a) -> None:
 
 def bench_timeline(a) -> None:
     """C2 decode on the timeline build (kushkash_amd/libkushhip_timeline.so: the same kernels, wave 0 of
-    each workgroup timestamping five phases, kush_decode.h KUSH_TIMELINE): after `--warmup` eager steps
-    per probed launch, one launch is recorded and summarized as markdown -- each phase's spread over
-    the workgroups (us from the first workgroup's start), and per XCD the page-loop time (first pair
-    landed -> pages done), the pages-done times and the shader clock over the loop."""
+    each workgroup timestamping five phases and each wave its pages done, kush_decode.h KUSH_TIMELINE):
+    after `--warmup` eager steps per probed launch, one launch is recorded and summarized as markdown --
+    each phase's spread over the workgroups (us from the first workgroup's start), how far apart the
+    waves of a workgroup finish their pages, and per XCD the page-loop time (first pair landed -> pages
+    done), the pages-done times and the shader clock over the loop."""
     import ctypes
     import importlib
     import numpy as np
@@ -747,7 +748,7 @@ def bench_timeline(a) -> None:
         step(1)
         e1.record()
         torch.cuda.synchronize()
-        buf = np.zeros((rows, 8), dtype=np.int64)
+        buf = np.zeros((rows, 16), dtype=np.int64)
         rc = read(buf.ctypes.data_as(ctypes.c_void_p), rows)
         if rc != 0:
             raise RuntimeError(f"kush_timeline_read failed ({rc})")
@@ -764,6 +765,13 @@ def bench_timeline(a) -> None:
                         ("output stored", 4)):
             x = us[:, k]
             print(f"| {name} | {x.min():.2f} | {pct(x, 10):.2f} | {pct(x, 50):.2f} | {pct(x, 90):.2f} | {x.max():.2f} |")
+        wd = (t[:, 8:8 + wv] - t[:, 0].min()) / 100.0       # every wave's pages done
+        spread = wd.max(1) - wd.min(1)
+        last = np.bincount(wd.argmax(1), minlength=wv)
+        print(f"\nwaves' pages done within a workgroup: spread (last - first) p50 {pct(spread, 50):.2f}, p90 "
+              f"{pct(spread, 90):.2f}, max {spread.max():.2f} us; mean lag behind the workgroup's first wave, by wave: "
+              + ", ".join(f"{(wd[:, i] - wd.min(1)).mean():.2f}" for i in range(wv))
+              + "; last to finish, by wave: " + ", ".join(str(int(c)) for c in last))
         print("\n| XCD | workgroups | page loop p10 / p50 / max (us) | pages done p50 / max (us) | "
               "shader clock p50 (MHz) |\n|---|---|---|---|---|")
         for x in range(8):

@@ -44,30 +44,39 @@
 namespace kush {
 
 // Timeline build (-DKUSH_TIMELINE: the instrumented copy of one instantiation unit linked into
-// libkushhip_timeline.so, never the product library). Wave 0 of each workgroup records, per launch,
-// the 100 MHz wall clock at five points -- 0 start, 1 prologue done (first page DMAs about to go out),
-// 2 its first page pair landed, 3 its pages done, 4 its output stored -- in slots 0-4 of the
-// workgroup's row of 8, the shader clock at points 2 and 3 in slots 5 and 6, and the XCD it ran on
-// (hardware register XCC_ID) in slot 7. Rows beyond TIMELINE_ROWS are not recorded. The stores are
-// ordinary vector stores of wave 0 (every lane the same value).
+// libkushhip_timeline.so, never the product library). Each workgroup has a row of TIMELINE_COLS
+// int64 per launch. Wave 0 records the 100 MHz wall clock at five points -- 0 start, 1 prologue done
+// (first page DMAs about to go out), 2 its first page pair landed, 3 its pages done, 4 output stored --
+// in slots 0-4, the shader clock at points 2 and 3 in slots 5 and 6, and the XCD it ran on (hardware
+// register XCC_ID) in slot 7; every wave w records the wall clock at which it consumed its last page
+// pair (before the workgroup's barrier; the last window's, with several) in slot 8 + w. Rows
+// beyond TIMELINE_ROWS are not recorded. The stores are ordinary vector stores (every lane of the
+// wave the same value).
 #ifdef KUSH_TIMELINE
-constexpr int TIMELINE_ROWS = 1 << 16;
-static __device__ long long g_timeline[TIMELINE_ROWS * 8];
+constexpr int TIMELINE_ROWS = 1 << 16, TIMELINE_COLS = 16;
+static __device__ long long g_timeline[TIMELINE_ROWS * TIMELINE_COLS];
+__device__ __forceinline__ long long* timeline_row() {
+    const long long row = ((long long)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+    return row < TIMELINE_ROWS ? g_timeline + row * TIMELINE_COLS : nullptr;
+}
 __device__ __forceinline__ void timeline_mark(int k) {
-    if (__builtin_amdgcn_readfirstlane(threadIdx.x) < WAVE) {    // wave 0: a wave-uniform branch
-        const long long row = ((long long)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
-        if (row < TIMELINE_ROWS) {
-            long long* const r = g_timeline + row * 8;
-            r[k] = wall_clock64();
-            if (k == 0) r[7] = __builtin_amdgcn_s_getreg((3 << 11) | 20);     // XCC_ID bits [3:0]
-            if (k == 2) r[5] = clock64();
-            if (k == 3) r[6] = clock64();
-        }
+    long long* const r = timeline_row();
+    if (__builtin_amdgcn_readfirstlane(threadIdx.x) < WAVE && r != nullptr) {   // wave 0: wave-uniform
+        r[k] = wall_clock64();
+        if (k == 0) r[7] = __builtin_amdgcn_s_getreg((3 << 11) | 20);         // XCC_ID bits [3:0]
+        if (k == 2) r[5] = clock64();
+        if (k == 3) r[6] = clock64();
     }
 }
+__device__ __forceinline__ void timeline_wave_done() {
+    long long* const r = timeline_row();
+    if (r != nullptr) r[8 + __builtin_amdgcn_readfirstlane(threadIdx.x) / WAVE] = wall_clock64();
+}
 #define KUSH_MARK(k) timeline_mark(k)
+#define KUSH_MARK_WAVE() timeline_wave_done()
 #else
 #define KUSH_MARK(k) ((void)0)
+#define KUSH_MARK_WAVE() ((void)0)
 #endif
 
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
@@ -991,6 +1000,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
                 KUSH_STEP(sl0, sl1, pa)
                 KUSH_STEP(sl2, sl3, pb)
             }
+            KUSH_MARK_WAVE();
             KUSH_WAIT_VM(0);                                     // drain the trailing (empty) issues
             __syncthreads();                                     // table and rings idle
             wb += WIN;
@@ -1072,11 +1082,13 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         }
     }
 
-    // Merge the waves (and, ST = 2, the two streams of a head: columns c and c ^ 8). Every wave
-    // rescales its O to the workgroup max of its head, adds a head's two stream columns (one DPP
-    // move; columns 0-7 then hold the sums) and stores it in the idle rings (region of wave ww: 16 D
-    // floats, dims d as [d / 4][column][d % 4], one 16-byte store per lane and tile); after one
-    // barrier, wave w sums tiles w, w + NW, ... over the waves and writes them out.
+    // Merge the waves (and, ST = 2, the two streams of a head: columns c and c ^ 8). After one
+    // barrier every wave has the workgroup max M and denominator L of its columns' heads from the
+    // waves' (m, l); it scales its O by exp2(m - M) (and, without splits, by 1 / L) and stores all 16
+    // columns in the idle rings (region of wave ww: 16 D floats, dims d as [d / 4][column][d % 4],
+    // one 16-byte store per lane and tile). After a second barrier wave w sums tiles w, w + NW, ...
+    // over the waves (and a head's two stream columns) and writes them out. No lane shuffles or
+    // masked stores: on one wave per SIMD this tail is latency-bound.
     constexpr int OBYTES = 16 * D * 4;
     static_assert(NW * OBYTES <= 2 * NW * R::SLOT, "the merge needs 16 D floats per wave in the first array");
     l_run = rows_sum(l_run);
@@ -1087,65 +1099,70 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     }
     __syncthreads();                                             // rings idle, m_l / l_l complete
     const int rx = ST == 2 ? (r16 ^ 8) : r16;                    // the other stream's column of this head
+    // M and the softmax denominator of this column's head: every wave's (and stream's) l at the
+    // workgroup max. A column that saw no token holds m = -inf and l = 0, and exp2(-inf) = 0, so no
+    // term needs a branch and all the LDS reads go out together (the sum keeps its order)
+    float mv[NW][ST], lv[NW][ST];
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww)
+#pragma unroll
+        for (int c2 = 0; c2 < ST; ++c2) {
+            mv[ww][c2] = m_l[ww * 16 + (c2 ? rx : r16)];
+            lv[ww][c2] = l_l[ww * 16 + (c2 ? rx : r16)];
+        }
     float M = -__builtin_inff();
 #pragma unroll
-    for (int ww = 0; ww < NW; ++ww) M = __builtin_fmaxf(M, __builtin_fmaxf(m_l[ww * 16 + r16], m_l[ww * 16 + rx]));
-    {
-        const float f = m_run == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m_run - M);
-        uint8_t* reg = ringA + w * OBYTES;
+    for (int ww = 0; ww < NW; ++ww)
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            f4 v;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                v[i] = __builtin_fmaf(o[dt][i], dt < NLO ? TWO24 : TWO20, vb_run) * f;
-                if constexpr (ST == 2) v[i] += lane_xor<8>(v[i]);   // the head's two streams (column c ^ 8)
-            }
-            if (ST == 1 || r16 < 8) *reinterpret_cast<f4*>(reg + (((4 * dt + q) * 16 + r16) * 4) * 4) = v;
-        }
-    }
-    // softmax denominator of head r16: every wave's (and stream's) l at the workgroup max. A column
-    // that saw no token holds m = -inf and l = 0, and exp2(-inf) = 0, so no term needs a branch and
-    // all the LDS reads go out together (the sum keeps its order)
+        for (int c2 = 0; c2 < ST; ++c2) M = __builtin_fmaxf(M, mv[ww][c2]);
     float L = 0.0f;
     if (M > -__builtin_inff()) {
-        float mv[NW][ST], lv[NW][ST];
-#pragma unroll
-        for (int ww = 0; ww < NW; ++ww)
-#pragma unroll
-            for (int c2 = 0; c2 < ST; ++c2) {
-                mv[ww][c2] = m_l[ww * 16 + (c2 ? rx : r16)];
-                lv[ww][c2] = l_l[ww * 16 + (c2 ? rx : r16)];
-            }
 #pragma unroll
         for (int ww = 0; ww < NW; ++ww)
 #pragma unroll
             for (int c2 = 0; c2 < ST; ++c2) L += lv[ww][c2] * __builtin_amdgcn_exp2f(mv[ww][c2] - M);
     }
-    __syncthreads();
     const float inv_l = L > 0.0f ? 1.0f / L : 0.0f;
+    {
+        // split partials stay unnormalized (L goes out beside them)
+        const float f = m_run == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m_run - M) * (NS == 1 ? inv_l : 1.0f);
+        uint8_t* reg = ringA + w * OBYTES;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            f4 v;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = __builtin_fmaf(o[dt][i], dt < NLO ? TWO24 : TWO20, vb_run) * f;
+            *reinterpret_cast<f4*>(reg + (((4 * dt + q) * 16 + r16) * 4) * 4) = v;
+        }
+    }
+    __syncthreads();
     const int64_t pb = (((int64_t)s * H + h) * NS + z) * G + g0 + r16;   // partials row of head r16
     const bool out_vec = (((uintptr_t)out) & 15) == 0;
-    const int hcol = ST == 2 ? (r16 & 7) : r16;                  // the column holding head r16's sum
+    const int hcol = ST == 2 ? (r16 & 7) : r16;                  // the (first) column of head r16
     float* const ostage = reinterpret_cast<float*>(ringB + AL::Q_OFF);   // ROT: [16][D] output rows
     for (int dt = w; dt < DT; dt += NW) {
-        f4 part[NW];                                             // every wave's piece, read together
+        f4 part[NW][ST];                                         // every wave's pieces, read together
 #pragma unroll
         for (int ww = 0; ww < NW; ++ww)
-            part[ww] = *reinterpret_cast<const f4*>(ringA + ww * OBYTES + (((4 * dt + q) * 16 + hcol) * 4) * 4);
+#pragma unroll
+            for (int c2 = 0; c2 < ST; ++c2)
+                part[ww][c2] = *reinterpret_cast<const f4*>(ringA + ww * OBYTES +
+                                                            (((4 * dt + q) * 16 + hcol + 8 * c2) * 4) * 4);
         f4 acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int ww = 0; ww < NW; ++ww) acc += part[ww];
+        for (int ww = 0; ww < NW; ++ww)
+#pragma unroll
+            for (int c2 = 0; c2 < ST; ++c2) acc += part[ww][c2];
         if (r16 < Gc) {
             const int d0 = 16 * dt + 4 * q;
             if (ROT && NS == 1) {                                // fp32 rows, rotated below
-                *reinterpret_cast<f4*>(ostage + r16 * D + d0) = acc * inv_l;
+                *reinterpret_cast<f4*>(ostage + r16 * D + d0) = acc;
             } else if (NS == 1) {
                 IN* dst = out + qbase + r16 * D + d0;
                 if (out_vec) {                                   // one 8- or 16-byte store
                     IN v4[4];
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) v4[i] = from_f32<IN>(acc[i] * inv_l);
+                    for (int i = 0; i < 4; ++i) v4[i] = from_f32<IN>(acc[i]);
                     if constexpr (sizeof(IN) == 2) {
                         *reinterpret_cast<u2*>(dst) = __builtin_bit_cast(u2, v4);
                     } else {
@@ -1153,7 +1170,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
                     }
                 } else {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) dst[i] = from_f32<IN>(acc[i] * inv_l);
+                    for (int i = 0; i < 4; ++i) dst[i] = from_f32<IN>(acc[i]);
                 }
             } else {
 #pragma unroll

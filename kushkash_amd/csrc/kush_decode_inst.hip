@@ -30,11 +30,11 @@ __attribute__((used)) void* const launchers[] = {
 }  // namespace kush
 
 #ifdef KUSH_TIMELINE
-// Timeline build only: copies the first `rows` rows (8 int64 each) of this unit's timeline records
-// to host memory `dst` (kush_decode.h, KUSH_TIMELINE). 0 on success, else the HIP error code.
+// Timeline build only: copies the first `rows` rows (TIMELINE_COLS int64 each) of this unit's
+// timeline records to host memory `dst` (kush_decode.h, KUSH_TIMELINE). 0 on success, else the HIP error code.
 extern "C" int kush_timeline_read(void* dst, int64_t rows) {
     if (rows < 0 || rows > kush::TIMELINE_ROWS) return (int)hipErrorInvalidValue;
-    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(kush::g_timeline), (size_t)rows * 8 * sizeof(long long), 0,
-                                    hipMemcpyDeviceToHost);
+    const size_t bytes = (size_t)rows * kush::TIMELINE_COLS * sizeof(long long);
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(kush::g_timeline), bytes, 0, hipMemcpyDeviceToHost);
 }
 #endif

@@ -1,6 +1,7 @@
 """The timeline build (kushkash_amd/libkushhip_timeline.so, read by bench.py --timeline) runs the same
 decode as the product library: bit-identical outputs on one input, and its records hold, per
-workgroup, phases in time order and an XCD id in 0..7 (needs an MI355X)."""
+workgroup, phases in time order, an XCD id in 0..7 and every wave's pages-done time between the
+workgroup's start and its output (needs an MI355X)."""
 import ctypes
 import importlib
 import math
@@ -40,7 +41,7 @@ def test_timeline_build_matches_the_product(waves):
         read = _lib.lib().kush_timeline_read
         read.argtypes, read.restype = [ctypes.c_void_p, ctypes.c_int64], ctypes.c_int32
         rows = B * Hkv
-        buf = np.zeros((rows, 8), dtype=np.int64)
+        buf = np.zeros((rows, 16), dtype=np.int64)
         assert read(buf.ctypes.data_as(ctypes.c_void_p), rows) == 0
     finally:
         _lib.LIB = saved
@@ -51,4 +52,6 @@ def test_timeline_build_matches_the_product(waves):
     assert (np.diff(wall, axis=1) >= 0).all(), "phases out of order"
     assert (buf[:, 6] >= buf[:, 5]).all()
     assert ((buf[:, 7] >= 0) & (buf[:, 7] < 8)).all()
+    waves_done = buf[:, 8:8 + waves]
+    assert (waves_done >= wall[:, :1]).all() and (waves_done <= wall[:, 4:5]).all()
     assert (wall[:, 4] - wall[:, 0] < 100 * 10_000).all()      # each workgroup within 10 ms (100 MHz clock)
