@@ -117,7 +117,7 @@ int kush_decode(int head_dim, int bits, int group, int dtype, const void* q, voi
  *   workgroup of each (sequence, kv head) merges the splits into out itself and resets its counter,
  *   so the buffer stays zero between calls and no kush_combine is needed; calls that share
  *   split_sync must not overlap.
- * waves: 2, 4 or 8 waves per workgroup (0 = 8; a configuration whose page ring does not fit in LDS
+ * waves: 2, 4 or 8 waves per workgroup (0 = 4; a configuration whose page ring does not fit in LDS
  *   runs fewer). Every choice is deterministic: the same call gives the same bits.
  * seq_order: NULL, or int32 [n_seqs] holding a permutation of the sequences: their workgroups start
  *   in that order (longest first balances a ragged batch); the results do not depend on it.

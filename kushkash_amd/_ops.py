@@ -29,7 +29,7 @@ import torch
 
 PAGE = 32
 DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
-DECODE_WAVES = 8                # default waves per decode workgroup (kush_decode: waves = 0)
+DECODE_WAVES = 4                # default waves per decode workgroup (kush_decode: waves = 0)
 SYNC_SLOTS = 1 << 16            # split-K merge counters per Ops: (sequence, kv head, 16-head chunk) slots
 
 
@@ -327,15 +327,13 @@ class Ops:
     def waves(self, num_seqs: int, num_kv_heads: int, n_splits: int, max_pages: int | None = None) -> int:
         """Waves per decode workgroup (measured on MI355X): 2 when the grid holds at least two
         workgroups per CU (smaller workgroups overlap one's start and merge with another's page
-        loop); else 8 when every workgroup streams >= 256 pages (the deepest ring per CU streams
-        fastest, 0.221 against 0.247 us per page step of 256 workgroups, for ~0.9 us more fixed
-        cost: 8 waves win from ~192 pages on); else 4. A configuration whose ring does not fit in LDS
-        runs fewer (the library picks)."""
+        loop); else 4, one wave per SIMD (C2 33.0 us against 33.5 with 8 waves, C4 217.8 against
+        221.0: the second wave of a SIMD adds issue slots but no bandwidth, and with a static page
+        assignment it finishes ~6 us after the first). max_pages is accepted for callers that pass
+        it. A configuration whose ring does not fit in LDS runs fewer (the library picks)."""
         if num_seqs * num_kv_heads * n_splits >= 2 * self.sms:
             return 2
-        if max_pages is not None and max_pages // max(1, n_splits) >= 256:
-            return 8
-        return 4
+        return DECODE_WAVES
 
     def decode(self, q: torch.Tensor, out: torch.Tensor, cache: torch.Tensor, block_table: torch.Tensor,
                seq_lens: torch.Tensor, tail_idx: torch.Tensor, tail_k: torch.Tensor,

@@ -29,7 +29,7 @@ int decode_impl(const char* what, int head_dim, int bits, int group, int dtype, 
     if (((uintptr_t)cache | (uint64_t)block_stride | (uint64_t)head_stride) & 15)
         return kush_fail(-2, "%s: cache records must be 16-byte aligned", what);
     if (((uintptr_t)q | (uintptr_t)tail_k) & 15) return kush_fail(-2, "%s: q and tail_k must be 16-byte aligned", what);
-    if (waves == 0) waves = 8;
+    if (waves == 0) waves = 4;
     if (waves != 2 && waves != 4 && waves != 8) return kush_fail(-2, "%s: waves must be 0, 2, 4 or 8", what);
     const int n_gc = (group + 15) / 16;
     if ((int64_t)n_splits * n_gc > 65535) return kush_fail(-2, "%s: n_splits %d too large", what, n_splits);
