@@ -117,14 +117,15 @@ def test_c4_full_size(c4, ns, merge, monkeypatch):
     assert int(ops._sync.abs().sum()) == 0
 
 
-@pytest.mark.parametrize("ns", [0, 64])
-def test_c4_repeated_steps_are_bit_identical(c4, ns):
-    """The same C4 decode step twice gives the same bits: every wave count sums a fixed set of pages in
-    a fixed order, and the split merge folds the splits in a fixed order (reference: gpu.mojo:566-807
-    assigns pages to warps statically)."""
+@pytest.mark.parametrize("ns,waves", [(0, 0), (0, 8), (64, 0), (64, 8)])
+def test_c4_repeated_steps_are_bit_identical(c4, ns, waves):
+    """The same C4 decode step three times gives the same bits, at the policy's launch shape and with 8
+    waves (two per SIMD, which the hardware runs at different rates): every wave count sums a fixed
+    set of pages in a fixed order, and the split merge folds the splits in a fixed order (reference:
+    gpu.mojo:566-807 assigns pages to warps statically)."""
     ops, B, Hkv, G, D, N = c4["ops"], c4["B"], c4["Hkv"], c4["G"], c4["D"], c4["N"]
     ns = ns or ops.splits(B, Hkv, N // PAGE)
-    waves = ops.waves(B, Hkv, ns, N // PAGE)
+    waves = waves or ops.waves(B, Hkv, ns, N // PAGE)
     work = torch.empty(B * Hkv * ns * G * (D + 2), dtype=torch.float32, device=DEV)
     outs = []
     for _ in range(3):
