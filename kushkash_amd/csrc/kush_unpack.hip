@@ -14,7 +14,7 @@
 // 2*D-byte row pieces). A workgroup takes TASKS consecutive tasks: it first loads all their
 // records into LDS (loads only, all issued before the first wait, so a workgroup keeps several
 // records in flight), then dequantizes from LDS and streams the rows out with non-temporal
-// stores. A token row is D / 16 consecutive lanes; lane c of the row holds dims 8c.. and
+// stores, row by row across its tasks when they are heads of one page. A token row is D / 16 consecutive lanes; lane c of the row holds dims 8c.. and
 // D/2 + 8c.. (the int4 record's byte order: byte 8c + j carries dims 8c + j and D/2 + 8c + j).
 #include "kush_fwht.h"
 
@@ -135,6 +135,46 @@ __global__ __launch_bounds__((Unpack<D, BITS>::THREADS)) void unpack_kernel(
     }
     __syncthreads();
 
+    // The common case, every task of the workgroup a full page of one item (TASKS consecutive kv heads
+    // of one page): rows outside, heads inside, so a wave's consecutive stores fill the TASKS heads'
+    // pieces of each row back to back (C4 group 129.7 -> 125.7 us, rotated back 143.9 -> 134.0)
+    // rather than coming back to every row once per head.
+    {
+        const int item0 = task0 / H, h0 = task0 - item0 * H;
+        if (h0 + U::TASKS <= H && item0 < n_pages && task0 + U::TASKS <= rec_tasks) {
+            const int64_t dst0 = page_dst[item0];
+            for (int t = r0; t < PAGE; t += U::RP) {
+                IN* ko = kp + (dst0 + t) * rs + (int64_t)h0 * D;
+                IN* vo = vp + (dst0 + t) * rs + (int64_t)h0 * D;
+#pragma unroll
+                for (int k = 0; k < U::TASKS; ++k) {
+                    const uint8_t* rec = stage[k];
+                    float kx[16], vx[16], ks[16], kb[16];
+                    f16x8(rec + F::OFF_KS + 2 * lo, ks);
+                    f16x8(rec + F::OFF_KS + 2 * hi, ks + 8);
+                    f16x8(rec + F::OFF_KB + 2 * lo, kb);
+                    f16x8(rec + F::OFF_KB + 2 * hi, kb + 8);
+                    row_codes<D, BITS>(rec + t * F::DC, c, kx);
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) kx[j] = __builtin_fmaf(kx[j], ks[j], kb[j]);
+                    row_codes<D, BITS>(rec + F::OFF_VQ + t * F::DC, c, vx);
+                    const float vs = f16_val(*reinterpret_cast<const uint16_t*>(rec + F::OFF_VS + 2 * t));
+                    const float vb = f16_val(*reinterpret_cast<const uint16_t*>(rec + F::OFF_VB + 2 * t));
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) vx[j] = __builtin_fmaf(vx[j], vs, vb);
+                    if (rot) {
+                        fwht_runs<D>(kx, c);
+                        fwht_runs<D>(vx, c);
+                    }
+                    stream8<VEC>(ko + k * D + lo, kx);
+                    stream8<VEC>(ko + k * D + hi, kx + 8);
+                    stream8<VEC>(vo + k * D + lo, vx);
+                    stream8<VEC>(vo + k * D + hi, vx + 8);
+                }
+            }
+            return;
+        }
+    }
     for (int k = 0; k < U::TASKS; ++k) {
         const int task = task0 + k;
         if (task >= n_tasks) break;
