@@ -103,6 +103,48 @@ def test_timeline_build_is_the_library_plus_its_reader(lib):
     assert not hasattr(ctypes.CDLL(str(_lib.LIB)), "kush_timeline_read")
 
 
+def test_missing_library_names_the_build(monkeypatch, tmp_path):
+    """No library -> a RuntimeError naming the build command on the first call, never a silent
+    fallback (the reference's loader surfaces its driver error the same way: tests/test_cpu.py:235-254)."""
+    monkeypatch.setattr(_lib, "LIB", tmp_path / "libkushhip.so")
+    _lib.lib.cache_clear()
+    try:
+        with pytest.raises(RuntimeError, match=r"libkushhip\.so is not built; run `python -m kushkash_amd\.build`"):
+            _lib.call("kush_abi_version")
+    finally:
+        monkeypatch.undo()
+        _lib.lib.cache_clear()
+
+
+def test_library_of_another_abi_is_refused(monkeypatch, tmp_path):
+    """A library built from other sources (another ABI revision) is refused when loaded, before any
+    entry point runs with a mismatched argument list."""
+    class Fn:
+        def __init__(self, ret):
+            self.ret = ret
+
+        def __call__(self, *args):
+            return self.ret
+
+    class OtherAbi:
+        def __getattr__(self, name):
+            fn = Fn(_lib.ABI_VERSION - 1 if name == "kush_abi_version" else 0)
+            setattr(self, name, fn)
+            return fn
+
+    fake = tmp_path / "libkushhip.so"
+    fake.write_bytes(b"")
+    monkeypatch.setattr(_lib, "LIB", fake)
+    monkeypatch.setattr(ctypes, "CDLL", lambda path: OtherAbi())
+    _lib.lib.cache_clear()
+    try:
+        with pytest.raises(RuntimeError, match=f"has ABI {_lib.ABI_VERSION - 1}, expected {_lib.ABI_VERSION}"):
+            _lib.lib()
+    finally:
+        monkeypatch.undo()
+        _lib.lib.cache_clear()
+
+
 def test_abi_version(lib):
     m = re.search(r"ABI revision of this header \((\d+)\)", HEADER.read_text())
     assert m and int(m.group(1)) == lib.kush_abi_version() == _lib.ABI_VERSION
