@@ -780,7 +780,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     using AL = AfterLoop<D>;
     static_assert(2 * NW * R::SLOT >= AL::ML_OFF + 2 * NW * 16 * 4 + 16, "the after-loop scratch must fit");
     static_assert(2 * R::DMA <= 63, "vmcnt holds at most 63 loads");
-    static_assert(2 * NW * R::SLOT >= 16 * D * 4, "ROT stages the chunk's q rows in the first array");
+    static_assert(2 * NW * R::SLOT >= 16 * D * 4, "ROT stages the chunk's q rows in the second array");
     static_assert(2 * NW * R::SLOT >= tile_bytes<D, IN>(), "the fused append's K tile lives in the first array");
 
     // one array per page pair (wave w at 2 w R::SLOT): the compiler tells the pairs apart and leaves
@@ -917,8 +917,16 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         // q (loaded above) is converted and the window's ids stored before the barrier: no vector
         // memory load of the compiler's is outstanding once the page DMAs start
         load_window();
+        int pa = w, pb = NW + w;                                         // the pairs in slots (0, 1), (2, 3)
         if constexpr (ROT) {                                             // rotate, round to IN, regather
-            float* const qst = reinterpret_cast<float*>(ringA);          // [16][D], idle before the DMAs
+            // The first pair goes out before q is rotated: every compiler load in (vmcnt 0, so no
+            // later wait of the compiler's counts the DMAs), the table's barrier, pair pa's DMAs into
+            // the first array; q is staged in the second, idle until pair pb's DMAs.
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+            __syncthreads();
+            KUSH_MARK(1);
+            KUSH_ISSUE_PAIR(sl0, sl1, pa)
+            float* const qst = reinterpret_cast<float*>(ringB);          // [16][D]
 #pragma unroll
             for (int pp = 0; pp < QPASS; ++pp) {
                 const int rr = (int)threadIdx.x / QCG + pp * QRP;
@@ -954,10 +962,11 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
                 qla[kk][j] = hin ? (_Float16)((float)lo * 0.0625f) : lo;
             }
         const float sa = rs * TWO24;                             // x = sa s + kx
-        int pa = w, pb = NW + w;                                         // the pairs in slots (0, 1), (2, 3)
         __syncthreads();
-        KUSH_MARK(1);
-        KUSH_ISSUE_PAIR(sl0, sl1, pa)
+        if constexpr (!ROT) {
+            KUSH_MARK(1);
+            KUSH_ISSUE_PAIR(sl0, sl1, pa)
+        }
         KUSH_ISSUE_PAIR(sl2, sl3, pb)
 
         // One pair step: the pair has landed once at most the other pair's loads are outstanding;
