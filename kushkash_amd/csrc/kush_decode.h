@@ -914,18 +914,18 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         issue_page<D, BITS>(SA, (P) < pairs, __builtin_amdgcn_readfirstlane(id2.x), head_base, bs, voff);  \
         issue_page<D, BITS>(SB, 2 * (P) + 1 < wn, __builtin_amdgcn_readfirstlane(id2.y), head_base, bs, voff); \
     }
-        // q (loaded above) is converted and the window's ids stored before the barrier: no vector
-        // memory load of the compiler's is outstanding once the page DMAs start
+        // the window's ids are stored and every load of the compiler's is in before the barrier: no
+        // vector memory load of the compiler's is outstanding once the page DMAs start
         load_window();
         int pa = w, pb = NW + w;                                         // the pairs in slots (0, 1), (2, 3)
+        // The first pair goes out before q is prepared: every compiler load in (vmcnt 0, so no later
+        // wait of the compiler's counts the DMAs), the table's barrier, pair pa's DMAs into the first
+        // array; a rotated q is staged in the second, idle until pair pb's DMAs.
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __syncthreads();
+        KUSH_MARK(1);
+        KUSH_ISSUE_PAIR(sl0, sl1, pa)
         if constexpr (ROT) {                                             // rotate, round to IN, regather
-            // The first pair goes out before q is rotated: every compiler load in (vmcnt 0, so no
-            // later wait of the compiler's counts the DMAs), the table's barrier, pair pa's DMAs into
-            // the first array; q is staged in the second, idle until pair pb's DMAs.
-            __builtin_amdgcn_s_waitcnt(0x0F70);
-            __syncthreads();
-            KUSH_MARK(1);
-            KUSH_ISSUE_PAIR(sl0, sl1, pa)
             float* const qst = reinterpret_cast<float*>(ringB);          // [16][D]
 #pragma unroll
             for (int pp = 0; pp < QPASS; ++pp) {
@@ -962,11 +962,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
                 qla[kk][j] = hin ? (_Float16)((float)lo * 0.0625f) : lo;
             }
         const float sa = rs * TWO24;                             // x = sa s + kx
-        __syncthreads();
-        if constexpr (!ROT) {
-            KUSH_MARK(1);
-            KUSH_ISSUE_PAIR(sl0, sl1, pa)
-        }
+        if constexpr (ROT) __syncthreads();                      // every wave done with the staged q
         KUSH_ISSUE_PAIR(sl2, sl3, pb)
 
         // One pair step: the pair has landed once at most the other pair's loads are outstanding;
