@@ -918,13 +918,15 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         // vector memory load of the compiler's is outstanding once the page DMAs start
         load_window();
         int pa = w, pb = NW + w;                                         // the pairs in slots (0, 1), (2, 3)
-        // The first pair goes out before q is prepared: every compiler load in (vmcnt 0, so no later
+        // The first pairs go out before q is prepared: every compiler load in (vmcnt 0, so no later
         // wait of the compiler's counts the DMAs), the table's barrier, pair pa's DMAs into the first
-        // array; a rotated q is staged in the second, idle until pair pb's DMAs.
+        // array and pair pb's into the second; a rotated q is staged in the second array instead,
+        // and pair pb waits until every wave has read it back.
         __builtin_amdgcn_s_waitcnt(0x0F70);
         __syncthreads();
         KUSH_MARK(1);
         KUSH_ISSUE_PAIR(sl0, sl1, pa)
+        if constexpr (!ROT) KUSH_ISSUE_PAIR(sl2, sl3, pb)
         if constexpr (ROT) {                                             // rotate, round to IN, regather
             float* const qst = reinterpret_cast<float*>(ringB);          // [16][D]
 #pragma unroll
@@ -962,8 +964,10 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
                 qla[kk][j] = hin ? (_Float16)((float)lo * 0.0625f) : lo;
             }
         const float sa = rs * TWO24;                             // x = sa s + kx
-        if constexpr (ROT) __syncthreads();                      // every wave done with the staged q
-        KUSH_ISSUE_PAIR(sl2, sl3, pb)
+        if constexpr (ROT) {
+            __syncthreads();                                     // every wave done with the staged q
+            KUSH_ISSUE_PAIR(sl2, sl3, pb)
+        }
 
         // One pair step: the pair has landed once at most the other pair's loads are outstanding;
         // scores of both pages (the next pair's table read hides behind them), one softmax update,
