@@ -70,12 +70,40 @@ def _includes(path: Path, seen: set) -> None:
                 break
 
 
+def _code(text: str) -> str:
+    """C / C++ source without its comments, blank lines and indentation (spaces inside a line
+    collapsed; line breaks kept, as they end preprocessor directives): what the compiler reads
+    (string and character literals are kept as they are)."""
+    out, i, n = [], 0, len(text)
+    while i < n:
+        ch = text[i]
+        if ch in "\"'":
+            j = i + 1
+            while j < n and text[j] != ch:
+                j += 2 if text[j] == "\\" else 1
+            out.append(text[i:j + 1])
+            i = j + 1
+        elif text.startswith("//", i):
+            while i < n and text[i] != "\n":
+                i += 1
+        elif text.startswith("/*", i):
+            j = text.find("*/", i + 2)
+            i = n if j < 0 else j + 2
+            out.append(" ")
+        else:
+            out.append(ch)
+            i += 1
+    lines = (" ".join(line.split()) for line in "".join(out).splitlines())
+    return "\n".join(line for line in lines if line)
+
+
 def source_digest(unit: str | None = None) -> str:
     """16 hex digits of sha256 over what decides the machine code of one translation unit (`unit`, a
     csrc/*.hip file: it and its local headers, transitively) or of the whole library (None: every
-    source and header), plus the compiler flags and instantiation units. The same sources give the
-    same digest on every machine and rebuild, so a measurement of a kernel taken on one build can be
-    matched to the build that runs later, and stays valid while only other kernels change."""
+    source and header) -- their code without comments or layout -- plus the compiler flags and
+    instantiation units. The same code gives the same digest on every machine and rebuild, so a
+    measurement of a kernel taken on one build can be matched to the build that runs later, and stays
+    valid while only other kernels or comments change."""
     h = hashlib.sha256()
     if unit is None:
         files = sorted((PKG / "csrc").glob("*.h")) + sorted((PKG / "csrc").glob("*.hip"))
@@ -85,7 +113,7 @@ def source_digest(unit: str | None = None) -> str:
         _includes(PKG / "csrc" / unit, seen)
         files = sorted(seen)
     for f in files:
-        h.update(f.name.encode() + b"\0" + f.read_bytes() + b"\0")
+        h.update(f.name.encode() + b"\0" + _code(f.read_text()).encode() + b"\0")
     h.update(repr((FLAGS, units())).encode())
     return h.hexdigest()[:16]
 

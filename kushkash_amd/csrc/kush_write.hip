@@ -3,10 +3,12 @@
 // kushkash/_ops.py:66-101 (launch), arithmetic kushkash/kush/quant.mojo:25-50. Pages are
 // bit-identical to the reference CPU path (kushkash/kush/cpu.mojo:173-304).
 //
-// Work split on CDNA4: one workgroup per (page, kv head), of 256 threads for the append and of
-// 128 (D <= 128) or 256 threads for the chunk write, small enough in threads and LDS that a CU
-// holds 16 of them: a chunk's pages then mostly run as one round, all their row loads in flight
-// together. The page quantizer itself (thread layout, K tile, rotation) is in kush_page.h.
+// Work split on CDNA4: a page task is one (page, kv head), of 256 threads for the append and of
+// 128 (D <= 128) or 256 threads for the chunk write, whose 256-thread workgroups take two
+// neighbouring kv heads of a page at D <= 128. A chunk's tasks start as fast as the dispatcher and
+// the CUs' registers allow (six such workgroups per CU at C4's 71 VGPRs), every task's row loads
+// issued before its first wait. The page quantizer itself (thread layout, K tile, rotation) is in
+// kush_page.h.
 #include "kush_page.h"
 
 namespace kush {
