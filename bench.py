@@ -14,9 +14,11 @@ The 155 MB of records of one pool fit in the 256 MB Infinity Cache, so steps rot
 --pools independent KV pools (default 4, 621 MB) and every step reads records that left the
 cache.
 
-Timing: both graphs (--warmup steps, then exactly --steps steps) are captured first; the warm-up
-graph is replayed, the host synchronizes, and one replay of the timed graph is bracketed by HIP
-events. The default warm-up of 1,000 steps (~35 ms for C2) brings the GPU to its steady clocks: the
+Timing: both graphs (--warmup steps, then exactly --steps steps) are captured first (for C2 over
+the allocated buffers, each launched once there before the records are written: a graph's first
+launch carries one-time work, and the data generation then keeps the GPU busy up to the warm-up
+instead of idling through the captures); the warm-up graph is replayed, the host synchronizes,
+and one replay of the timed graph is bracketed by HIP events. The default warm-up of 1,000 steps (~35 ms for C2) brings the GPU to its steady clocks: the
 first C2 line of a fresh process measured 35.0-38.2 us with 20 warm-up steps, 34.3-35.8 with 200 and
 33.1-33.2 with 1,000.
 
@@ -103,8 +105,10 @@ def parse_args(argv=None):
     return ap.parse_args(argv)
 
 
-def make_workload(a, dev):
-    """Pools of records written by the product's write kernel, per-pool block tables, q."""
+def make_workload(a, dev, defer: bool = False):
+    """Pools of records written by the product's write kernel, per-pool block tables, q. defer: the
+    buffers are allocated (and the block tables drawn) but the records and q are written only by
+    w["fill"](), with the same random draws in the same order, so graphs can be captured first."""
     import kushkash_amd as kk
     from kushkash_amd._ops import Ops, record_bytes
     B, N, Hkv, G, D, bits = a.batch, a.ctx, a.hkv, a.hq // a.hkv, a.dim, a.bits
@@ -122,28 +126,34 @@ def make_workload(a, dev):
     tail_k = torch.zeros(B, Hkv, PAGE, D, dtype=dtype, device=dev)
     tail_idx = torch.arange(B, dtype=torch.int32, device=dev)
     seq_lens = torch.full((B,), N, dtype=torch.int32, device=dev)
+    q = torch.zeros(B, a.hq, D, dtype=dtype, device=dev)
     n_bias = max(1, round(0.10 * D))
     chunk = max(1, (1 << 27) // (Hkv * N * D * 2))          # sequences per write call (~128 MB of K)
-    for i in range(a.pools):
-        bias = torch.zeros(Hkv, D, device=dev)
-        for h in range(Hkv):
-            ch = torch.randperm(D, generator=gen, device=dev)[:n_bias]
-            bias[h, ch] = 6.0 * torch.randn(n_bias, generator=gen, device=dev)
-        for s0 in range(0, B, chunk):
-            s1 = min(B, s0 + chunk)
-            n = s1 - s0
-            k = (torch.randn(n * N, Hkv, D, generator=gen, device=dev) + bias).to(dtype)
-            v = torch.randn(n * N, Hkv, D, generator=gen, device=dev).to(dtype)
-            qsl = torch.arange(n + 1, dtype=torch.int32, device=dev) * N
-            js = torch.arange(n, dtype=torch.int32, device=dev).repeat_interleave(pages)
-            jp = torch.arange(pages, dtype=torch.int32, device=dev).repeat(n)
-            ops.write(k, v, qsl, seq_lens[s0:s1], tail_idx[s0:s1], js, jp, cache, tables[i][s0:s1].contiguous(),
-                      tail_k, rot=a.rot)
-            del k, v
-    q = torch.randn(B, a.hq, D, generator=gen, device=dev).to(dtype)
-    torch.cuda.synchronize()
+
+    def fill():
+        for i in range(a.pools):
+            bias = torch.zeros(Hkv, D, device=dev)
+            for h in range(Hkv):
+                ch = torch.randperm(D, generator=gen, device=dev)[:n_bias]
+                bias[h, ch] = 6.0 * torch.randn(n_bias, generator=gen, device=dev)
+            for s0 in range(0, B, chunk):
+                s1 = min(B, s0 + chunk)
+                n = s1 - s0
+                k = (torch.randn(n * N, Hkv, D, generator=gen, device=dev) + bias).to(dtype)
+                v = torch.randn(n * N, Hkv, D, generator=gen, device=dev).to(dtype)
+                qsl = torch.arange(n + 1, dtype=torch.int32, device=dev) * N
+                js = torch.arange(n, dtype=torch.int32, device=dev).repeat_interleave(pages)
+                jp = torch.arange(pages, dtype=torch.int32, device=dev).repeat(n)
+                ops.write(k, v, qsl, seq_lens[s0:s1], tail_idx[s0:s1], js, jp, cache,
+                          tables[i][s0:s1].contiguous(), tail_k, rot=a.rot)
+                del k, v
+        q.copy_(torch.randn(B, a.hq, D, generator=gen, device=dev).to(dtype))
+        torch.cuda.synchronize()
+
+    if not defer:
+        fill()
     return dict(ops=ops, cache=cache, tables=tables, tail_k=tail_k, tail_idx=tail_idx, seq_lens=seq_lens, q=q,
-                B=B, N=N, Hkv=Hkv, G=G, D=D, bits=bits, RB=RB, pages=pages, kk=kk, rot=a.rot)
+                B=B, N=N, Hkv=Hkv, G=G, D=D, bits=bits, RB=RB, pages=pages, kk=kk, rot=a.rot, fill=fill)
 
 
 def algorithmic_bytes(w) -> int:
@@ -802,12 +812,21 @@ def main(argv=None):
         {"c1": bench_c1, "c3": bench_c3, "c4": bench_c4, "c4-write": bench_c4_write, "c4-unpack": bench_c4_unpack,
          "c4-fwht": bench_c4_fwht}[a.config](a)
         return
-    w = make_workload(a, dev)
+    # The graphs are captured over the allocated buffers before the records are written: the data
+    # generation (the write kernel over every pool) then keeps the GPU busy up to the warm-up steps,
+    # rather than the GPU idling through the host-side captures into a cold timed replay.
+    w = make_workload(a, dev, defer=True)
     ns = a.splits or w["ops"].splits(w["B"], w["Hkv"], w["N"] // PAGE)
     alg = algorithmic_bytes(w)
 
     wv = a.waves or w["ops"].waves(w["B"], w["Hkv"], ns, w["pages"])
-    ms = time_steps(w, ns, wv, a.steps, a.warmup)
+    g, _ = graph_of(w, ns, wv, a.steps)
+    gw = graph_of(w, ns, wv, a.warmup)[0] if a.warmup else None
+    for graph in (g, gw):                 # each graph's first launch (its one-time upload) during setup,
+        if graph is not None:             # on the not yet written buffers
+            graph.replay()
+    w["fill"]()
+    ms = _timed_replay(g, gw, a.steps)
     shape = (f"C2 Qwen2.5-7B decode layer: {a.hq} q / {a.hkv} kv heads, D {a.dim}, int{a.bits}, page 32, "
              f"batch {a.batch} x {a.ctx} tokens" + (", rotation folded into the kernels" if a.rot else "")
              + ("" if a.dtype == "bf16" else f", {a.dtype}"))
