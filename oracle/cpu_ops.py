@@ -35,9 +35,10 @@ _SIGS = {   # argument lists of the reference's CPU C ABI (kushkash/_cpu.py:10-2
 
 
 def build(force: bool = False) -> Path:
-    """Compile the oracle with its Makefile (gcc); returns the library path."""
+    """Compile the oracle with its Makefile (gcc); returns the library path. force: compile even when
+    the library is newer than its source (make -B)."""
     if force or not LIB.exists() or LIB.stat().st_mtime < (HERE / "kush_oracle.c").stat().st_mtime:
-        subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+        subprocess.run(["make", "-s", "-B"] if force else ["make", "-s"], check=True, cwd=str(HERE))
     return LIB
 
 
