@@ -73,6 +73,32 @@ def self_attention_blocks(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Ten
     return acc
 
 
+def ragged_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_start: list, k_start: list, scale: float,
+                     block_bytes: int = 1 << 28) -> torch.Tensor:
+    """Causal attention of ragged rows packed end to end: row i's queries q[q_start[i]:q_start[i+1]]
+    ([rows, Hq, D]) over its keys k, v[k_start[i]:k_start[i+1]] ([rows, Hk, D]), the queries being the
+    last T of the row's N keys (query t sees keys j <= N - T + t: the serving engines' prefill
+    convention). Keys go in blocks that keep each block's scores within block_bytes. Returns q's shape
+    and dtype."""
+    out = q.new_empty(q.shape)
+    Hk, D = k.shape[1], k.shape[2]
+    for i in range(len(q_start) - 1):
+        a, b, c, d = q_start[i], q_start[i + 1], k_start[i], k_start[i + 1]
+        if b <= a:
+            continue
+        T, N = b - a, d - c
+        qi = q[a:b].transpose(0, 1).unsqueeze(0)                               # [1, Hq, T, D]
+        ki = k[c:d].transpose(0, 1).unsqueeze(0)                               # [1, Hk, N, D]
+        vi = v[c:d].transpose(0, 1).unsqueeze(0)
+        n = keys_per_block(qi, Hk, 2 * Hk * D * 4, block_bytes, 1)
+        acc = None
+        for j0 in range(0, N, n):
+            j1 = min(N, j0 + n)
+            acc = merge(acc, attn_lse(qi, ki[:, :, j0:j1], vi[:, :, j0:j1], True, scale, key_offset=N - T - j0))
+        out[a:b] = acc[0][0].transpose(0, 1).to(q.dtype)
+    return out
+
+
 def history_attention(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, records: torch.Tensor,
                       block_ids: torch.Tensor, n_hist: int, tail_k: torch.Tensor, head_dim: int, bits: int,
                       scale: float, block_bytes: int = 1 << 28) -> torch.Tensor:
