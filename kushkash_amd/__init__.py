@@ -1,8 +1,9 @@
 """kushkash_amd: the compressed-KV hot path of kushkash (paged int4 / int8 KV cache with fused
 dequant decode attention) as hand-written HIP kernels for AMD Instinct MI355X (gfx950).
 
-Drop-in for the reference's kushkash.KushCache / kushkash._ops.Ops on one GPU, and for its Hugging
-Face entry points (KushHFCache, enable, generate; transformers is imported on first use)."""
+Drop-in for the reference's kushkash.KushCache / kushkash._ops.Ops on one GPU, for its Hugging Face
+entry points (KushHFCache, enable, generate; transformers is imported on first use) and for its
+SGLang plugin (kushkash_amd.sglang; SGLang is imported when the plugin registers)."""
 from ._ops import PAGE, Ops, record_bytes
 from .cache import KushCache, MemoryStats
 
