@@ -64,6 +64,39 @@ __device__ __forceinline__ void f16x8(const uint8_t* p, float* x) {
     for (int j = 0; j < 8; ++j) x[j] = (float)v[j];
 }
 
+// Token row t of a page record in LDS, dequantized for lane c (dims lo.. and hi..): V always from
+// the record; K from the record when k_src is null, else copied from the exact K row k_src + t * D.
+// fma(code, scale, bias) in fp32, then the rotation back when rot.
+#pragma clang fp contract(off)
+template <int D, int BITS, typename IN, bool VEC>
+__device__ __forceinline__ void dequant_row(const uint8_t* rec, int t, int c, int lo, int hi, const IN* k_src, int rot,
+                                            float (&kx)[16], float (&vx)[16]) {
+    using F = Fmt<D, BITS>;
+    if (k_src == nullptr) {
+        float ks[16], kb[16];
+        f16x8(rec + F::OFF_KS + 2 * lo, ks);
+        f16x8(rec + F::OFF_KS + 2 * hi, ks + 8);
+        f16x8(rec + F::OFF_KB + 2 * lo, kb);
+        f16x8(rec + F::OFF_KB + 2 * hi, kb + 8);
+        row_codes<D, BITS>(rec + t * F::DC, c, kx);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) kx[j] = __builtin_fmaf(kx[j], ks[j], kb[j]);
+    } else {
+        get8<VEC>(k_src + t * D + lo, reinterpret_cast<float(&)[8]>(kx[0]));
+        get8<VEC>(k_src + t * D + hi, reinterpret_cast<float(&)[8]>(kx[8]));
+    }
+    row_codes<D, BITS>(rec + F::OFF_VQ + t * F::DC, c, vx);
+    const float vs = f16_val(*reinterpret_cast<const uint16_t*>(rec + F::OFF_VS + 2 * t));
+    const float vb = f16_val(*reinterpret_cast<const uint16_t*>(rec + F::OFF_VB + 2 * t));
+#pragma unroll
+    for (int j = 0; j < 16; ++j) vx[j] = __builtin_fmaf(vx[j], vs, vb);
+    if (rot) {
+        fwht_runs<D>(kx, c);
+        fwht_runs<D>(vx, c);
+    }
+}
+#pragma clang fp contract(on)
+
 // 8 fp32 values rounded to IN at dst, 16-byte non-temporal stores when VEC (the rows are not
 // read again by this kernel, and a group's rows exceed the caches)
 template <bool VEC, typename IN>
@@ -148,24 +181,8 @@ __global__ __launch_bounds__((Unpack<D, BITS>::THREADS)) void unpack_kernel(
                 IN* vo = vp + (dst0 + t) * rs + (int64_t)h0 * D;
 #pragma unroll
                 for (int k = 0; k < U::TASKS; ++k) {
-                    const uint8_t* rec = stage[k];
-                    float kx[16], vx[16], ks[16], kb[16];
-                    f16x8(rec + F::OFF_KS + 2 * lo, ks);
-                    f16x8(rec + F::OFF_KS + 2 * hi, ks + 8);
-                    f16x8(rec + F::OFF_KB + 2 * lo, kb);
-                    f16x8(rec + F::OFF_KB + 2 * hi, kb + 8);
-                    row_codes<D, BITS>(rec + t * F::DC, c, kx);
-#pragma unroll
-                    for (int j = 0; j < 16; ++j) kx[j] = __builtin_fmaf(kx[j], ks[j], kb[j]);
-                    row_codes<D, BITS>(rec + F::OFF_VQ + t * F::DC, c, vx);
-                    const float vs = f16_val(*reinterpret_cast<const uint16_t*>(rec + F::OFF_VS + 2 * t));
-                    const float vb = f16_val(*reinterpret_cast<const uint16_t*>(rec + F::OFF_VB + 2 * t));
-#pragma unroll
-                    for (int j = 0; j < 16; ++j) vx[j] = __builtin_fmaf(vx[j], vs, vb);
-                    if (rot) {
-                        fwht_runs<D>(kx, c);
-                        fwht_runs<D>(vx, c);
-                    }
+                    float kx[16], vx[16];
+                    dequant_row<D, BITS, IN, VEC>(stage[k], t, c, lo, hi, nullptr, rot, kx, vx);
                     stream8<VEC>(ko + k * D + lo, kx);
                     stream8<VEC>(ko + k * D + hi, kx + 8);
                     stream8<VEC>(vo + k * D + lo, vx);
@@ -185,31 +202,10 @@ __global__ __launch_bounds__((Unpack<D, BITS>::THREADS)) void unpack_kernel(
             const int i = item - n_pages;
             const int64_t dst0 = page ? page_dst[item] : tail_info[3 * i];
             const int n = page ? PAGE : tail_info[3 * i + 1];
-            const IN* tk = page ? tail_k : tail_k + ((int64_t)tail_info[3 * i + 2] * H + h) * PAGE * D;
+            const IN* tk = page ? nullptr : tail_k + ((int64_t)tail_info[3 * i + 2] * H + h) * PAGE * D;
             for (int t = r0; t < n; t += U::RP) {
                 float kx[16], vx[16];
-                if (page) {
-                    float ks[16], kb[16];
-                    f16x8(rec + F::OFF_KS + 2 * lo, ks);
-                    f16x8(rec + F::OFF_KS + 2 * hi, ks + 8);
-                    f16x8(rec + F::OFF_KB + 2 * lo, kb);
-                    f16x8(rec + F::OFF_KB + 2 * hi, kb + 8);
-                    row_codes<D, BITS>(rec + t * F::DC, c, kx);
-#pragma unroll
-                    for (int j = 0; j < 16; ++j) kx[j] = __builtin_fmaf(kx[j], ks[j], kb[j]);
-                } else {
-                    get8<VEC>(tk + t * D + lo, reinterpret_cast<float(&)[8]>(kx[0]));
-                    get8<VEC>(tk + t * D + hi, reinterpret_cast<float(&)[8]>(kx[8]));
-                }
-                row_codes<D, BITS>(rec + F::OFF_VQ + t * F::DC, c, vx);
-                const float vs = f16_val(*reinterpret_cast<const uint16_t*>(rec + F::OFF_VS + 2 * t));
-                const float vb = f16_val(*reinterpret_cast<const uint16_t*>(rec + F::OFF_VB + 2 * t));
-#pragma unroll
-                for (int j = 0; j < 16; ++j) vx[j] = __builtin_fmaf(vx[j], vs, vb);
-                if (rot) {
-                    fwht_runs<D>(kx, c);
-                    fwht_runs<D>(vx, c);
-                }
+                dequant_row<D, BITS, IN, VEC>(rec, t, c, lo, hi, tk, rot, kx, vx);
                 IN* ko = kp + (dst0 + t) * rs + (int64_t)h * D;
                 IN* vo = vp + (dst0 + t) * rs + (int64_t)h * D;
                 stream8<VEC>(ko + lo, kx);
