@@ -168,33 +168,35 @@ def canonical_rotation(D: int, dtype: torch.dtype):
     return rotate
 
 
-def stored(K: torch.Tensor, V: torch.Tensor, bits: int, rotate=None, h: torch.Tensor | None = None):
-    """What the cache holds for exact K, V [n, Hk, D], in model space: K per channel over each full page
-    (the unfinished page exact), V per token. With a rotation, of rotate(K), rotate(V), rotated back by
-    the orthonormal Hadamard matrix h. The rotation is the format's own (the same rounding as the
-    kernels') and the quantizer's arithmetic is fp32 as the kernels', so every code matches: a
-    rotation or a quantizer that rounds differently moves a value across a rounding boundary now and
-    then, which changes its code by one level. K and V hold values of the model dtype."""
+def held_in_cache(K: torch.Tensor, V: torch.Tensor, bits: int, rotate=None, h: torch.Tensor | None = None):
+    """The K, V [n, Hk, D] a cache hands back for exact tokens K, V (values of the model dtype), in model
+    space: the K rows of every completed page quantized per channel across the page's 32 tokens, the
+    rows of the unfinished page as they are, every V row quantized per token. With a rotation the
+    cache holds rotate(K), rotate(V), handed back through the orthonormal Hadamard matrix h. The
+    rotation is the format's own and the quantizer works in fp32 like the kernels, so every code
+    matches theirs: a rotation or a quantizer that rounds differently moves a value across a rounding
+    boundary now and then, which changes its code by one level."""
     if rotate is not None:
         K, V = rotate(K), rotate(V)
-    n, Hk, D = K.shape
-    full = n // PAGE * PAGE
-    Kq = K.clone()
-    if full:
-        Kq[:full] = ref_dequant(K[:full].float().view(-1, PAGE, Hk, D), bits, 1).view(full, Hk, D).double()
-    Vq = ref_dequant(V.float(), bits, -1).double()
-    return (Kq, Vq) if rotate is None else (Kq @ h, Vq @ h)
+    done = K.shape[0] - K.shape[0] % PAGE
+    pages = K[:done].float().unflatten(0, (-1, PAGE))                    # [pages, 32, Hk, D]
+    k_held = torch.cat([ref_dequant(pages, bits, 1).flatten(0, 1).double(), K[done:]])
+    v_held = ref_dequant(V.float(), bits, -1).double()
+    if rotate is not None:
+        k_held, v_held = k_held @ h, v_held @ h
+    return k_held, v_held
 
 
-def attention(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, first: int, scale: float) -> torch.Tensor:
-    """q [T, Hq, D] over K, V [n, Hk, D]; query t sees keys < first + t + 1."""
-    T, Hq, _ = q.shape
-    G = Hq // K.shape[1]
-    Kx = K.transpose(0, 1).repeat_interleave(G, 0)
-    Vx = V.transpose(0, 1).repeat_interleave(G, 0)
-    s = (q.transpose(0, 1) @ Kx.transpose(1, 2)) * scale
-    visible = torch.ones(T, K.shape[0], dtype=torch.bool).tril(first)
-    return (torch.softmax(s.masked_fill(~visible, float("-inf")), -1) @ Vx).transpose(0, 1)
+def causal_gqa(q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, first: int, scale: float) -> torch.Tensor:
+    """Attention of T queries q [T, Hq, D] over keys K, V [n, Hk, D], float64 on the CPU: q head i reads
+    kv head i // (Hq / Hk); query t is at position first + t and sees the keys up to it."""
+    T, Hq, D = q.shape
+    Hk = K.shape[1]
+    qg = q.reshape(T, Hk, Hq // Hk, D)
+    logits = torch.einsum("tkgd,nkd->kgtn", qg, K) * scale
+    hidden = torch.arange(K.shape[0])[None, :] > (first + torch.arange(T))[:, None]      # [T, n]
+    weights = logits.masked_fill(hidden, float("-inf")).softmax(dim=-1)
+    return torch.einsum("kgtn,nkd->tkgd", weights, V).reshape(T, Hq, D)
 
 
 class Server:
@@ -221,13 +223,14 @@ class Server:
 
     # ---------------------------------------------------------------- SGLang's bookkeeping
     def grow(self, slot: int, n: int) -> None:
-        """Token slots for n more tokens of request `slot`, a new page at each page start."""
-        cur = self.length.get(slot, 0)
-        for pos in range(cur, cur + n):
-            if pos % PAGE == 0:
-                page = self.free.pop()
-                self.req_to_token[slot, pos:pos + PAGE] = page * PAGE + torch.arange(PAGE, dtype=torch.int32)
-        self.length[slot] = cur + n
+        """Token slots for n more tokens of request `slot`: whole pages from the free list, as many as
+        the new length needs beyond the pages the request holds."""
+        have = self.length.get(slot, 0)
+        held, needed = -(-have // PAGE), -(-(have + n) // PAGE)
+        for p in range(held, needed):
+            first = self.free.pop() * PAGE
+            self.req_to_token[slot, p * PAGE:(p + 1) * PAGE] = torch.arange(first, first + PAGE, dtype=torch.int32)
+        self.length[slot] = have + n
 
     def share(self, src: int, dst: int, n: int) -> None:
         """A radix-cache hit: request dst starts with the first n (whole pages) tokens of src."""
@@ -270,11 +273,11 @@ class Server:
             self.tokens[(layer, s)] = (Kall, Vall)
             qs = q[a:a + c].double().view(c, self.Hq, self.D)
             if decode:                                 # the whole cache, the new token included
-                Kq, Vq = stored(Kall, Vall, self.bits, self.rotate, self.h)
-            else:                                      # stored history, the chunk exact
-                Kh, Vh = stored(K0, V0, self.bits, self.rotate, self.h)
+                Kq, Vq = held_in_cache(Kall, Vall, self.bits, self.rotate, self.h)
+            else:                                      # the cached history, then the chunk exact
+                Kh, Vh = held_in_cache(K0, V0, self.bits, self.rotate, self.h)
                 Kq, Vq = torch.cat([Kh, kn]), torch.cat([Vh, vn])
-            outs.append(attention(qs, Kq, Vq, n0, self.D ** -0.5))
+            outs.append(causal_gqa(qs, Kq, Vq, n0, self.D ** -0.5))
             a += c
         return torch.cat(outs).reshape(-1, self.Hq * self.D)
 
