@@ -151,3 +151,33 @@ def test_packed_prefill_matches_attend_chunk():
     ref = c.attend_chunk(0, q.to(DEV), k.to(DEV), v.to(DEV)).float().cpu()
     err = (out - ref).abs().max().item()
     assert err < 2e-2, err
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_unpack_random_groups(seed):
+    """Seeded random groups, bit-identical to the oracle: head dim, bits, dtype, rot, 1-8 kv heads (the
+    row-by-row path when a workgroup's tasks are heads of one page, the per-task path otherwise),
+    0-40 full pages, 0-6 partial pages of 1-31 tokens, 0-4 runs of new rows, aligned or unaligned
+    new rows; rows no entry names stay untouched."""
+    import numpy as np
+    rng = np.random.default_rng(7000 + seed)
+    D, bits = int(rng.choice([64, 128, 256])), int(rng.choice([4, 8]))
+    dtype = (torch.float32, torch.bfloat16, torch.float16)[rng.integers(3)]
+    rot, H = bool(rng.random() < 0.5), int(rng.integers(1, 9))
+    tails = tuple(int(x) for x in rng.integers(1, 32, int(rng.integers(0, 7))))
+    runs = tuple(int(x) for x in rng.integers(1, 81, int(rng.integers(0, 5))))
+    c = make_group(D, bits, dtype, seed=seed, H=H, n_pages=int(rng.integers(0, 41)), tail_tokens=tails,
+                   new_runs=runs, slots=len(tails) + int(rng.integers(1, 4)))
+    print(f"seed {seed}: D {D} bits {bits} {dtype} rot {rot} H {H} pages {c['page_blk'].numel()} tails {tails} "
+          f"runs {runs}", flush=True)
+    k_new = v_new = None
+    if rng.random() < 0.3 and c["k_new"].shape[0]:                  # new rows one element off 16-byte alignment
+        n = c["k_new"].shape[0]
+
+        def odd_rows(x):
+            buf = torch.empty(n, H * D + 1, dtype=dtype, device=DEV)
+            buf[:, :H * D] = x.reshape(n, H * D).to(DEV)
+            return buf[:, :H * D].view(n, H, D)
+        k_new, v_new = odd_rows(c["k_new"]), odd_rows(c["v_new"])
+    got = gpu_unpack(c, D, bits, rot, dtype, k_new, v_new)
+    assert_same(c, got, oracle_unpack(c, D, bits, rot, dtype), dtype)
