@@ -53,7 +53,7 @@ def test_small_pack_budget_on_the_kernels(sg, monkeypatch):
     assert w.step([1, 2, 3], [52, 21, 80], False, gen) < BOUND[torch.bfloat16]
     monkeypatch.setenv("KUSHKASH_PACK_MB", "1")            # 1 MiB: 1024 keys of bf16 K + V at Hk 2, D 128
     assert w.step([1, 2, 3], [300, 800, 1100], False, gen) < BOUND[torch.bfloat16]     # 352, 821, 1180 keys
-    kinds = [(g.r0, g.r1, g.packed) for g in w.backend.forward_metadata.groups]
+    kinds = [(g.r0, g.r1, g.packed) for g in w.backend.forward_metadata.extend.groups]
     assert kinds == [(0, 1, True), (1, 2, True), (2, 3, False)], kinds
     assert w.step([1, 2, 3], [1, 1, 1], True, gen) < BOUND[torch.bfloat16]
 
