@@ -30,6 +30,14 @@ from ._attention import ragged_attention, unpacked_history_attention
 from ._ops import PAGE, pages_touched
 
 
+def record_bits() -> int:
+    """Record bits of a serving cache: KUSHKASH_BITS, 4 (default) or 8."""
+    value = os.environ.get("KUSHKASH_BITS", "4")
+    if value not in ("4", "8"):
+        raise ValueError(f"KUSHKASH_BITS must be 4 or 8, got {value}")
+    return int(value)
+
+
 def pack_budget() -> int:
     """Bytes of K + V one packed group may hold: KUSHKASH_PACK_MB MiB (auto or unset: 512)."""
     value = os.environ.get("KUSHKASH_PACK_MB", "auto").strip().lower()
