@@ -3,7 +3,7 @@
 Headline workload ("C2"): Qwen2.5-7B-shaped layer, 28 q heads / 4 kv
 heads (GQA 7), head_dim 128, int4 records, page 32, batch 64 x exactly 4096 cached tokens, bf16 q
 and output. One step = one decode-attention pass of that layer (one kernel: the split-K merge is
-fused), with the inputs resident in HBM; the timed steps run back to back from one HIP graph.
+fused), with the inputs resident in HBM; the timed steps are launched back to back.
 
 Synthetic data (seed 0, generated on the GPU in this order): per pool, K = N(0,1) with a per-channel
 bias ~ N(0, 6^2) (sigma 6) on a seeded 10% of the channels of each kv head (13 of 128), V = N(0,1),
@@ -14,16 +14,17 @@ The 155 MB of records of one pool fit in the 256 MB Infinity Cache, so steps rot
 --pools independent KV pools (default 4, 621 MB) and every step reads records that left the
 cache.
 
-Timing: both graphs (--warmup steps, then exactly --steps steps) are captured first (for C2 over
-the allocated buffers, each launched once there before the records are written: a graph's first
-launch carries one-time work, and the data generation then keeps the GPU busy up to the warm-up
-instead of idling through the captures); the warm-up graph is replayed, the host synchronizes,
-and one replay of the timed graph is bracketed by HIP events. The default warm-up of 1,000 steps (~35 ms for C2) brings the GPU to its steady clocks: the
-first C2 line of a fresh process measured 35.0-38.2 us with 20 warm-up steps, 34.3-35.8 with 200 and
-33.1-33.2 with 1,000.
+Timing: the library calls of a step are recorded once from the product's own Ops calls (for C2 over
+the allocated buffers before the records are written, so the data generation then keeps the GPU busy
+up to the warm-up); --warmup steps run untimed, the host synchronizes, and exactly --steps steps are
+launched back to back between HIP events, followed by a synchronization. At ~5 us of host time per
+launch the host stays ahead of the GPU from the first step, so the window holds the steps' kernels
+only; timing HIP graph replays instead (--graph-replay) adds the graph's launch latency, 27-50 us of
+idle GPU for a 20-node graph, to the window (C2, 20 steps: 32.1-32.8 us per step launched, 32.7-34.3
+replayed). The default warm-up of 1,000 steps (~33 ms for C2) brings the GPU to its steady clocks.
 
 Prints one JSON line (the driver's contract) with "roofline" (decode kernel: algorithmic bytes /
-its mean duration, from HIP events around the graph of decode kernels) and
+its mean duration, from HIP events around the timed decode launches) and
 "cpu_baseline" (the C restatement of the reference CPU path, oracle/, on the host cores).
 
 --config selects the other measured configurations of the path (each prints its own JSON line; the
@@ -66,7 +67,7 @@ PAGE = 32
 def parse_args(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200, help="timed steps (one graph of that many launches)")
+    ap.add_argument("--steps", type=int, default=200, help="timed steps")
     ap.add_argument("--warmup", type=int, default=1000,
                     help="untimed steps replayed right before the timed ones (the GPU reaches its steady clocks "
                          "after some tens of ms of sustained load)")
@@ -100,6 +101,8 @@ def parse_args(argv=None):
     ap.add_argument("--timeline", type=int, default=0, metavar="N",
                     help="c2: run on libkushhip_timeline.so and print N launches' per-workgroup phase times by XCD "
                          "(bf16, no rotation)")
+    ap.add_argument("--graph-replay", action="store_true",
+                    help="time the steps as HIP graph replays instead of recorded launches (for comparison)")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "decode_c2_traffic.md"),
                     help="rocprofv3 counter summary whose 'traffic_bytes_per_launch' fills roofline.traffic")
     return ap.parse_args(argv)
@@ -108,7 +111,8 @@ def parse_args(argv=None):
 def make_workload(a, dev, defer: bool = False):
     """Pools of records written by the product's write kernel, per-pool block tables, q. defer: the
     buffers are allocated (and the block tables drawn) but the records and q are written only by
-    w["fill"](), with the same random draws in the same order, so graphs can be captured first."""
+    w["fill"](), with the same random draws in the same order, so the timed launches can be recorded
+    first."""
     import kushkash_amd as kk
     from kushkash_amd._ops import Ops, record_bytes
     B, N, Hkv, G, D, bits = a.batch, a.ctx, a.hkv, a.hq // a.hkv, a.dim, a.bits
@@ -167,11 +171,8 @@ def algorithmic_bytes(w) -> int:
     return rec + tail_b + qo + B * w["pages"] * 4 + B * 4
 
 
-def graph_of(w, ns: int, waves: int, n_steps: int):
-    """One HIP graph holding n_steps decode steps back to back, step i on pool i % pools (as a model's
-    decode graph holds one attention launch per layer): graph launch cost is paid once per replay, not
-    once per step. Each step is a single kernel (split-K partials are merged inside it by the last
-    workgroup of each (sequence, kv head))."""
+def decode_step(w, ns: int, waves: int):
+    """(step, out): step(i) is one C2 decode step on pool i % pools, through the product's Ops."""
     ops, B, Hkv, G, D = w["ops"], w["B"], w["Hkv"], w["G"], w["D"]
     out = torch.empty_like(w["q"])
     work = torch.empty(max(1, B * Hkv * ns * G * (D + 2)), dtype=torch.float32, device=w["q"].device)
@@ -181,31 +182,82 @@ def graph_of(w, ns: int, waves: int, n_steps: int):
     def step(i):
         ops.decode(w["q"], out, w["cache"], w["tables"][i % P], w["seq_lens"], w["tail_idx"], w["tail_k"], sm, ns,
                    work, waves=waves, rot=w["rot"])
+    return step, out
 
-    for i in range(P):                     # eager first call per pool (lazy init outside the capture)
+
+class Launches:
+    """The library calls of a step, recorded once from the product's own Ops calls -- step(i) for
+    i < period, each entry point with exactly the arguments Ops computed for it -- and replayed
+    straight into libkushhip.so. A loop of K steps then issues its kernel launches back to back at
+    ~5 us of host time each, so from the first step on the host runs ahead of the GPU and the timed
+    window holds the K steps' kernels and nothing else (a HIP graph of K steps would add its launch
+    latency, 27-50 us of an idle GPU for a 20-node graph, to the window). Recording runs every step of
+    the period once; a step must not allocate device memory, or its recorded pointers would dangle."""
+
+    def __init__(self, step, period: int = 1):
+        from kushkash_amd import _lib
+        torch.cuda.synchronize()
+        allocations = torch.cuda.memory_stats().get("allocation.all.allocated", 0)
+        recorded, real = [], _lib.call
+
+        def record(name, *args):
+            recorded[-1].append((name, args))
+            real(name, *args)
+        _lib.call = record
+        try:
+            for i in range(period):
+                recorded.append([])
+                step(i)
+        finally:
+            _lib.call = real
+        torch.cuda.synchronize()
+        if torch.cuda.memory_stats().get("allocation.all.allocated", 0) != allocations:
+            raise RuntimeError("bench: a timed step allocates device memory; its recorded launches would dangle")
+        lib = _lib.lib()
+        self.calls = [[(getattr(lib, name), name, args) for name, args in step_calls] for step_calls in recorded]
+        self.period = period
+
+    def run(self, first: int, n: int) -> None:
+        """Steps first .. first + n - 1."""
+        calls, period = self.calls, self.period
+        for i in range(first, first + n):
+            for fn, name, args in calls[i % period]:
+                if fn(*args) != 0:
+                    raise RuntimeError(f"bench: {name} failed during the timed steps")
+
+
+def time_launches(launches: Launches, steps: int, warmup: int) -> float:
+    """Mean ms per step: `warmup` untimed steps, a host synchronization, then exactly `steps` steps
+    between HIP events on the launch stream, and a synchronization."""
+    launches.run(0, warmup)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    launches.run(warmup, steps)
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def time_graph(step, steps: int, warmup: int) -> float:
+    """--graph-replay: mean ms per step with the steps in HIP graphs instead (`warmup` steps in a graph
+    of their own, then exactly `steps` steps in one graph replayed once between HIP events; both
+    captured, and launched once, before either is timed)."""
+    def capture(n):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                step(i)
+        torch.cuda.synchronize()
+        return g
+    for i in range(2):                       # eager calls first (lazy init outside the capture)
         step(i)
     torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for i in range(n_steps):
-            step(i)
-    torch.cuda.synchronize()
-    return g, out
-
-
-def time_steps(w, ns: int, waves: int, steps: int, warmup: int) -> float:
-    """Mean ms per step: `warmup` untimed steps (a graph of their own), then exactly `steps` steps in
-    one graph replay bracketed by synchronizations and HIP events on the replay stream. Both graphs
-    are captured before either runs, so the timed replay follows the warm-up after one host
-    synchronization, not after the host-side capture (milliseconds of an idle GPU)."""
-    g, _ = graph_of(w, ns, waves, steps)
-    gw = graph_of(w, ns, waves, warmup)[0] if warmup else None
-    return _timed_replay(g, gw, steps)
-
-
-def _timed_replay(g, gw, steps: int) -> float:
-    """Replay the warm-up graph gw (if any), synchronize, then time one replay of g between HIP events
-    on the replay stream; returns ms per step."""
+    g = capture(steps)
+    gw = capture(warmup) if warmup else None
+    for graph in (g, gw):
+        if graph is not None:
+            graph.replay()
     if gw is not None:
         gw.replay()
     torch.cuda.synchronize()
@@ -215,6 +267,13 @@ def _timed_replay(g, gw, steps: int) -> float:
     b.record()
     torch.cuda.synchronize()
     return a.elapsed_time(b) / steps
+
+
+def time_steps(a, step, period: int) -> float:
+    """Mean ms per step of step(i) by the selected method (recorded launches, or --graph-replay)."""
+    if a.graph_replay:
+        return time_graph(step, a.steps, a.warmup)
+    return time_launches(Launches(step, period), a.steps, a.warmup)
 
 
 def cpu_baseline(w, budget_s: float):
@@ -341,25 +400,6 @@ def copy_calibration(a) -> None:
 
 
 # ---------------------------------------------------------------- other configurations (C3, C4)
-def time_graph(step, steps: int, warmup: int) -> float:
-    """Mean ms per call of step(i): `warmup` calls in a graph of their own, then exactly `steps`
-    calls captured in one graph, replayed once between HIP events on the replay stream (both graphs
-    captured first, as in time_steps)."""
-    def capture(n):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for i in range(n):
-                step(i)
-        torch.cuda.synchronize()
-        return g
-    for i in range(2):                       # eager calls first (lazy init outside the capture)
-        step(i)
-    torch.cuda.synchronize()
-    g = capture(steps)
-    gw = capture(warmup) if warmup else None
-    return _timed_replay(g, gw, steps)
-
-
 def ragged_cache(ops, lens, room: int, Hkv: int, bias_sigma: float, bias_frac: float, gen, dev):
     """One pool of records for sequences of lens[i] tokens (pages for lens[i] + room), written by the
     product's write kernel from seeded K = N(0,1) + per-channel bias (sigma bias_sigma on a seeded
@@ -531,7 +571,7 @@ def bench_c3(a) -> None:
             ops.append_decode(k_new, v_new, q, out, cache, table, sl, tail_idx, tail_k, sm, ns, work, waves=wv,
                               order=order)
 
-    ms = time_graph(step, a.steps, a.warmup)
+    ms = time_steps(a, step, 1)
     RB, DC = record_bytes(D, bits), (D if bits == 8 else D // 2)
     n1 = [n + 1 for n in lens]
     dec = sum((n // PAGE) * Hkv * RB + (n % PAGE) * Hkv * (2 * D + DC + 4) for n in n1)
@@ -570,8 +610,8 @@ def bench_c4(a) -> None:
     for i, ns in enumerate(nss):
         work = torch.empty(B * Hkv * ns * G * (D + 2), dtype=torch.float32, device=dev)
         wv = a.waves or ops.waves(B, Hkv, ns, N // PAGE)
-        ms = time_graph(lambda j: ops.decode(q, out, cache, table, sl, tail_idx, tail_k, sm, ns, work, waves=wv),
-                        a.steps, a.warmup)
+        ms = time_steps(a, lambda j: ops.decode(q, out, cache, table, sl, tail_idx, tail_k, sm, ns, work, waves=wv),
+                        1)
         _line("decode-attn us/step + achieved HBM GB/s (% peak), int4, bs8 x 131k ctx", ms * 1e3, alg,
               {"workload": f"C4 Qwen3-8B layer: {Hq} q / {Hkv} kv heads, D {D}, int{bits}, page 32, "
                            f"batch {B} x {N} tokens, splits {ns}, waves {wv}", "global_batch": B, "seq_len": N,
@@ -610,7 +650,7 @@ def bench_c4_write(a) -> None:
         k, v, cache, table = sets[i % P]
         ops.write(k, v, qsl, sl, tail_idx, js, jp, cache, table, tail_k, fused=not a.two_launch, rot=a.rot)
 
-    ms = time_graph(step, a.steps, a.warmup)
+    ms = time_steps(a, step, P)
     alg = 2 * B * T * Hkv * D * 2 + B * pages * Hkv * RB
     launches = ("two launches: mode 0, mode 1" if a.two_launch else "one launch: mode 2") + (", rot" if a.rot else "")
     _line("chunked-prefill write us/step + achieved HBM GB/s (% peak), int4, 8 x 2048 tokens", ms * 1e3, alg,
@@ -647,10 +687,10 @@ def bench_c4_unpack(a) -> None:
         cache, _, tail_k, _ = pools[i % P]
         ops.unpack(cache, blks[i % P], page_dst, none, none, tail_k, k_new, v_new, new_dst, kp, vp, a.rot)
 
-    ops.validate = True                        # indices checked once, outside the timed graph
+    ops.validate = True                        # indices checked once, outside the timed steps
     step(0)
     ops.validate = False
-    ms = time_graph(step, a.steps, a.warmup)
+    ms = time_steps(a, step, P)
     RB = record_bytes(D, bits)
     alg = pages * Hkv * RB + 2 * rows * Hkv * D * 2 + 2 * T * Hkv * D * 2
     extra = None
@@ -705,7 +745,7 @@ def bench_c4_fwht(a) -> None:
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
     xs = [torch.randn(rows * Hkv, D, generator=gen, device=dev).to(dtype) for _ in range(2)]
-    ms = time_graph(lambda i: ops.fwht(xs[i % 2], out=xs[i % 2]), a.steps, a.warmup)
+    ms = time_steps(a, lambda i: ops.fwht(xs[i % 2], out=xs[i % 2]), 2)
     alg = 2 * rows * Hkv * D * 2
     _line("fwht us/step + achieved HBM GB/s (% peak), 1,064,960 rows of D 128 bf16", ms * 1e3, alg,
           {"workload": f"C4 key rotation: {rows} tokens x {Hkv} kv heads, D {D}, bf16, in place", "rows": rows * Hkv},
@@ -812,21 +852,22 @@ def main(argv=None):
         {"c1": bench_c1, "c3": bench_c3, "c4": bench_c4, "c4-write": bench_c4_write, "c4-unpack": bench_c4_unpack,
          "c4-fwht": bench_c4_fwht}[a.config](a)
         return
-    # The graphs are captured over the allocated buffers before the records are written: the data
-    # generation (the write kernel over every pool) then keeps the GPU busy up to the warm-up steps,
-    # rather than the GPU idling through the host-side captures into a cold timed replay.
+    # The steps' launches are recorded over the allocated buffers before the records are written: the
+    # data generation (the write kernel over every pool) then keeps the GPU busy up to the warm-up.
     w = make_workload(a, dev, defer=True)
     ns = a.splits or w["ops"].splits(w["B"], w["Hkv"], w["N"] // PAGE)
     alg = algorithmic_bytes(w)
 
     wv = a.waves or w["ops"].waves(w["B"], w["Hkv"], ns, w["pages"])
-    g, _ = graph_of(w, ns, wv, a.steps)
-    gw = graph_of(w, ns, wv, a.warmup)[0] if a.warmup else None
-    for graph in (g, gw):                 # each graph's first launch (its one-time upload) during setup,
-        if graph is not None:             # on the not yet written buffers
-            graph.replay()
-    w["fill"]()
-    ms = _timed_replay(g, gw, a.steps)
+    step, _ = decode_step(w, ns, wv)
+    P = len(w["tables"])
+    if a.graph_replay:
+        w["fill"]()
+        ms = time_graph(step, a.steps, a.warmup)
+    else:
+        launches = Launches(step, P)
+        w["fill"]()
+        ms = time_launches(launches, a.steps, a.warmup)
     shape = (f"C2 Qwen2.5-7B decode layer: {a.hq} q / {a.hkv} kv heads, D {a.dim}, int{a.bits}, page 32, "
              f"batch {a.batch} x {a.ctx} tokens" + (", rotation folded into the kernels" if a.rot else "")
              + ("" if a.dtype == "bf16" else f", {a.dtype}"))
@@ -867,7 +908,7 @@ def main(argv=None):
 
     for item in [x for x in a.sweep.split(",") if x.strip()]:     # other launch shapes, a line each
         sns, swv = (int(v) for v in item.split(":"))
-        msx = time_steps(w, sns, swv, a.steps, a.warmup)
+        msx = time_steps(a, decode_step(w, sns, swv)[0], P)
         _line(res["metric"], msx * 1e3, alg, {"workload": f"{shape}, splits {sns}, waves {swv}",
                                               "global_batch": a.batch, "seq_len": a.ctx, "split_k": sns,
                                               "waves": swv, "sweep": True},
