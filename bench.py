@@ -19,9 +19,10 @@ the allocated buffers before the records are written, so the data generation the
 up to the warm-up); --warmup steps run untimed, the host synchronizes, and exactly --steps steps are
 launched back to back between HIP events, followed by a synchronization. At ~5 us of host time per
 launch the host stays ahead of the GPU from the first step, so the window holds the steps' kernels
-only; timing HIP graph replays instead (--graph-replay) adds the graph's launch latency, 27-50 us of
-idle GPU for a 20-node graph, to the window (C2, 20 steps: 32.1-32.8 us per step launched, 32.7-34.3
-replayed). The default warm-up of 1,000 steps (~33 ms for C2) brings the GPU to its steady clocks.
+only. --graph-replay times the reference's way instead (bench/bench_decode.py:28-51: a one-step HIP
+graph replayed back to back), which on ROCm adds ~5 us of device-side overhead per replay (C2: 37.8
+us per step against 32.5 launched). The default warm-up of 1,000 steps (~33 ms for C2) brings the GPU
+to its steady clocks.
 
 Prints one JSON line (the driver's contract) with "roofline" (decode kernel: algorithmic bytes /
 its mean duration, from HIP events around the timed decode launches) and
@@ -102,7 +103,8 @@ def parse_args(argv=None):
                     help="c2: run on libkushhip_timeline.so and print N launches' per-workgroup phase times by XCD "
                          "(bf16, no rotation)")
     ap.add_argument("--graph-replay", action="store_true",
-                    help="time the steps as HIP graph replays instead of recorded launches (for comparison)")
+                    help="time the steps as replays of one-step HIP graphs (the reference's method) instead of "
+                         "recorded launches")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "decode_c2_traffic.md"),
                     help="rocprofv3 counter summary whose 'traffic_bytes_per_launch' fills roofline.traffic")
     return ap.parse_args(argv)
@@ -239,31 +241,26 @@ def time_launches(launches: Launches, steps: int, warmup: int) -> float:
     return a.elapsed_time(b) / steps
 
 
-def time_graph(step, steps: int, warmup: int) -> float:
-    """--graph-replay: mean ms per step with the steps in HIP graphs instead (`warmup` steps in a graph
-    of their own, then exactly `steps` steps in one graph replayed once between HIP events; both
-    captured, and launched once, before either is timed)."""
-    def capture(n):
+def time_graph(step, steps: int, warmup: int, period: int = 1) -> float:
+    """--graph-replay, the reference's method (bench/bench_decode.py:28-51): each step of the period
+    captured as a HIP graph of its own, `warmup` untimed replays, a host synchronization, then exactly
+    `steps` replays issued back to back between HIP events, and a synchronization."""
+    graphs = []
+    for i in range(period):
+        step(i)                              # eager call first (lazy init outside the capture)
+        torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            for i in range(n):
-                step(i)
-        torch.cuda.synchronize()
-        return g
-    for i in range(2):                       # eager calls first (lazy init outside the capture)
-        step(i)
+            step(i)
+        graphs.append(g)
     torch.cuda.synchronize()
-    g = capture(steps)
-    gw = capture(warmup) if warmup else None
-    for graph in (g, gw):
-        if graph is not None:
-            graph.replay()
-    if gw is not None:
-        gw.replay()
+    for i in range(warmup):
+        graphs[i % period].replay()
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
-    g.replay()
+    for i in range(warmup, warmup + steps):
+        graphs[i % period].replay()
     b.record()
     torch.cuda.synchronize()
     return a.elapsed_time(b) / steps
@@ -272,7 +269,7 @@ def time_graph(step, steps: int, warmup: int) -> float:
 def time_steps(a, step, period: int) -> float:
     """Mean ms per step of step(i) by the selected method (recorded launches, or --graph-replay)."""
     if a.graph_replay:
-        return time_graph(step, a.steps, a.warmup)
+        return time_graph(step, a.steps, a.warmup, period)
     return time_launches(Launches(step, period), a.steps, a.warmup)
 
 
@@ -863,7 +860,7 @@ def main(argv=None):
     P = len(w["tables"])
     if a.graph_replay:
         w["fill"]()
-        ms = time_graph(step, a.steps, a.warmup)
+        ms = time_graph(step, a.steps, a.warmup, P)
     else:
         launches = Launches(step, P)
         w["fill"]()
