@@ -575,11 +575,13 @@ constexpr bool decode_fits() {
     return decode_lds_bytes<D, BITS, NW>() <= 160 * 1024;
 }
 
-// byte offsets in the second array of the after-loop scratch: q [16][D] fp32, tail scores [16][PAGE],
+// byte offsets in the second array of the after-loop scratch: q [16][QS] fp32 (rows padded by 4
+// floats, so the 16 rows of one MFMA operand read fall on different banks), tail scores [16][PAGE],
 // m and l per wave and head [NW][16] each, the split-K flag
 template <int D>
 struct AfterLoop {
-    static constexpr int Q_OFF = 0, SC_OFF = 16 * D * 4, ML_OFF = SC_OFF + 16 * PAGE * 4;
+    static constexpr int QS = D + 4;
+    static constexpr int Q_OFF = 0, SC_OFF = 16 * QS * 4, ML_OFF = SC_OFF + 16 * PAGE * 4;
 };
 
 // Rows r < n of an fp32 staging area [.][D] in LDS rotated back by the canonical Walsh-Hadamard
@@ -844,6 +846,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     }
 
     const int n = seq_lens[s];
+    const int tix = tail_idx != nullptr ? tail_idx[s] : 0;              // the tail slot, with the length
     const int full = n / PAGE, tail_n = n % PAGE;
     const int pps = (full + NS - 1) / NS;
     const int p0 = min(full, z * pps), p1 = min(full, p0 + pps);
@@ -860,7 +863,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
             const int owner = slot == PAGE - 1 ? pg / max(pps, 1) : NS - 1;
             if (z == owner) {
                 const IN* krow = app_k + (int64_t)s * app_ks + (int64_t)h * D;
-                IN* tail = tail_k + ((int64_t)tail_idx[s] * H + h) * PAGE * D;
+                IN* tail = tail_k + ((int64_t)tix * H + h) * PAGE * D;
                 uint8_t* rec = cache + (int64_t)bt[pg] * bs + (int64_t)h * hs;
                 stash_rows<D, IN, true, ROT, NW * WAVE>(tail + slot * D, krow, 0, 1, (int)threadIdx.x);
                 page_task<D, BITS, IN, true, NW * WAVE, ROT>(tail, krow, 0, PAGE - 1, slot == PAGE - 1,
@@ -871,6 +874,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         __syncthreads();
     }
     const bool has_tail = tail_n > 0 && z == NS - 1;
+    const int tail_blk = has_tail ? bt[full] : 0;                      // in before the page loop starts
     uint8_t* const sl0 = ringA + 2 * w * R::SLOT;
     uint8_t* const sl1 = sl0 + R::SLOT;
     uint8_t* const sl2 = ringB + 2 * w * R::SLOT;
@@ -904,8 +908,18 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
                     const int i = (int)threadIdx.x + k * NW * WAVE;
                     if (i < wn) tbl[i] = pre[k];
                 }
-            } else {
-                for (int i = threadIdx.x; i < wn; i += NW * WAVE) tbl[i] = bt[wb + i];
+            } else {                                                     // every id load in flight at once
+                int ids[PRE];
+#pragma unroll
+                for (int k = 0; k < PRE; ++k) {
+                    const int i = (int)threadIdx.x + k * NW * WAVE;
+                    ids[k] = i < wn ? bt[wb + i] : 0;
+                }
+#pragma unroll
+                for (int k = 0; k < PRE; ++k) {
+                    const int i = (int)threadIdx.x + k * NW * WAVE;
+                    if (i < wn) tbl[i] = ids[k];
+                }
             }
         };
 #define KUSH_ISSUE_PAIR(SA, SB, P)                                                                 \
@@ -1029,14 +1043,27 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     KUSH_MARK(3);
 
     // partial last page (last split only): V rows from its record, staged by one wave in its slot 0;
-    // exact fp32 K . q scores from the tail, spread over all waves (lane: token lane % 32, heads
-    // 2 w + lane / 32 + 2 NW i), with q (fp32, times sm log2 e) and the scores in the rings
+    // exact fp32 K . q scores from the tail by waves 0 and 1, with q (fp32, times sm log2 e) and the
+    // scores in the rings
     if (has_tail) {
-        float* const qs = reinterpret_cast<float*>(ringB + AL::Q_OFF);    // [16][D] q sm log2e
+        constexpr int QS = AL::QS;
+        float* const qs = reinterpret_cast<float*>(ringB + AL::Q_OFF);    // [16][QS] q sm log2e
         float* const sc = reinterpret_cast<float*>(ringB + AL::SC_OFF);   // [16][PAGE] tail scores
         const int ow = (p1 - p0) % NW;
         uint8_t* const tslot = ringA + 2 * ow * R::SLOT;
-        if (w == ow) issue_page<D, BITS>(tslot, true, bt[full], head_base, bs, voff);
+        if (w == ow) issue_page<D, BITS>(tslot, true, tail_blk, head_base, bs, voff);
+        // K . q as 16 x 16 x 4 fp32 MFMAs (fp32 products and sums): wave 0 takes tokens 0-15, wave 1
+        // tokens 16-31. Lane: head (A row) and token (B column) lane % 16, dims [q D/4, (q+1) D/4)
+        // (the 4 lane groups are the MFMA's contraction). Its K slice is loaded here, with the q
+        // rows below: one memory latency for both.
+        constexpr int DQ = D / 4, KP = DQ * (int)sizeof(IN) / 16;           // dims, 16-byte pieces per lane
+        const int tt = 16 * w + r16;                                     // this lane's token (waves 0, 1)
+        u4 kraw[KP];
+        if (w < 2) {
+            const IN* tk = tail_k + (((int64_t)tix * H + h) * PAGE + min(tt, tail_n - 1)) * D + q * DQ;
+#pragma unroll
+            for (int i = 0; i < KP; ++i) kraw[i] = reinterpret_cast<const u4*>(tk)[i];
+        }
         if constexpr (ROT) {                                             // rotated q rows, as in the prologue
             for (int rr = (int)threadIdx.x / QCG; rr < 16; rr += QRP) {  // a row's lanes iterate together
                 float x[16];
@@ -1045,35 +1072,43 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
                 fwht_runs<D>(x, qc);
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    qs[rr * D + 8 * qc + j] = rr < Gc ? to_f32(store_rounded<IN>(x[j])) * sm_log2 : 0.0f;
-                    qs[rr * D + D / 2 + 8 * qc + j] = rr < Gc ? to_f32(store_rounded<IN>(x[8 + j])) * sm_log2 : 0.0f;
+                    qs[rr * QS + 8 * qc + j] = rr < Gc ? to_f32(store_rounded<IN>(x[j])) * sm_log2 : 0.0f;
+                    qs[rr * QS + D / 2 + 8 * qc + j] = rr < Gc ? to_f32(store_rounded<IN>(x[8 + j])) * sm_log2 : 0.0f;
                 }
             }
-        } else {
-            for (int i = threadIdx.x; i < 16 * D; i += NW * WAVE)
-                qs[i] = i < Gc * D ? to_f32(qg[qbase + i]) * sm_log2 : 0.0f;
-        }
-        __syncthreads();
-        constexpr int HPL = 16 / (2 * NW);                       // heads per lane
-        const int t = lane & 31, hg = 2 * w + (lane >> 5);
-        const IN* tk = tail_k + (((int64_t)tail_idx[s] * H + h) * PAGE + min(t, tail_n - 1)) * D;
-        float acc[HPL];
+        } else {                                                 // 8-element pieces, all loads in flight
+            constexpr int QP = 16 * D / 8, QPT = (QP + NW * WAVE - 1) / (NW * WAVE);
+            float xq[QPT][8];
 #pragma unroll
-        for (int i = 0; i < HPL; ++i) acc[i] = 0.0f;
-#pragma unroll 4
-        for (int d = 0; d < D; d += 8) {
-            float kx[8];
-            load8(tk + d, kx);
+            for (int k = 0; k < QPT; ++k)                        // unconditional (a valid piece), no branch
+                load8(qg + qbase + (int64_t)min((int)threadIdx.x + k * NW * WAVE, Gc * (D / 8) - 1) * 8, xq[k]);
 #pragma unroll
-            for (int i = 0; i < HPL; ++i) {
-                const float4 qa = *reinterpret_cast<const float4*>(&qs[(hg + 2 * NW * i) * D + d]);
-                const float4 qb = *reinterpret_cast<const float4*>(&qs[(hg + 2 * NW * i) * D + d + 4]);
-                acc[i] += qa.x * kx[0] + qa.y * kx[1] + qa.z * kx[2] + qa.w * kx[3] +
-                          qb.x * kx[4] + qb.y * kx[5] + qb.z * kx[6] + qb.w * kx[7];
+            for (int k = 0; k < QPT; ++k) {
+                const int pc = (int)threadIdx.x + k * NW * WAVE;
+                if (pc < QP) {
+                    float* const dst = qs + (pc / (D / 8)) * QS + (pc % (D / 8)) * 8;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) dst[j] = pc < Gc * (D / 8) ? xq[k][j] * sm_log2 : 0.0f;
+                }
             }
         }
+        __syncthreads();
+        if (w < 2) {
+            f4 c = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int i = 0; i < HPL; ++i) sc[(hg + 2 * NW * i) * PAGE + t] = t < tail_n ? acc[i] : -__builtin_inff();
+            for (int j = 0; j < DQ; j += 8) {
+                float kx[8];
+                load8(reinterpret_cast<const IN*>(kraw) + j, kx);
+                const f4 qa = *reinterpret_cast<const f4*>(&qs[r16 * QS + q * DQ + j]);
+                const f4 qb = *reinterpret_cast<const f4*>(&qs[r16 * QS + q * DQ + j + 4]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) c = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[e], kx[e], c, 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) c = __builtin_amdgcn_mfma_f32_16x16x4f32(qb[e], kx[4 + e], c, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[(4 * q + i) * PAGE + tt] = tt < tail_n ? c[i] : -__builtin_inff();
+        }
         __syncthreads();
         if (w == ow) {
             float x[1][8];
