@@ -578,10 +578,49 @@ constexpr bool decode_fits() {
 // byte offsets in the second array of the after-loop scratch: q [16][QS] fp32 (rows padded by 4
 // floats, so the 16 rows of one MFMA operand read fall on different banks), tail scores [16][PAGE],
 // m and l per wave and head [NW][16] each, the split-K flag
-template <int D>
+template <int D, int NW>
 struct AfterLoop {
     static constexpr int QS = D + 4;
-    static constexpr int Q_OFF = 0, SC_OFF = 16 * QS * 4, ML_OFF = SC_OFF + 16 * PAGE * 4;
+    static constexpr int NKP = NW / 2;                   // tail-score parts (contraction split NW / 2 ways)
+    static constexpr int Q_OFF = 0, SC_OFF = 16 * QS * 4, ML_OFF = SC_OFF + NKP * 16 * PAGE * 4;
+};
+
+// N consecutive IN values kept packed in 32-bit words (a register-lean copy of a row slice)
+template <typename IN, int N>
+struct Packed {
+    static constexpr int BYTES = N * (int)sizeof(IN), WORDS = BYTES / 4;
+    static_assert(BYTES % 16 == 0 || BYTES == 8, "16-byte pieces, or one 8-byte piece");
+    uint32_t wd[WORDS];
+    __device__ __forceinline__ void load(const IN* p) {          // p aligned to min(16, BYTES)
+        if constexpr (BYTES % 16 == 0) {
+#pragma unroll
+            for (int i = 0; i < BYTES / 16; ++i) {
+                const u4 v = reinterpret_cast<const u4*>(p)[i];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) wd[4 * i + j] = v[j];
+            }
+        } else {
+            const u2 v = *reinterpret_cast<const u2*>(p);
+            wd[0] = v[0];
+            wd[1] = v[1];
+        }
+    }
+    __device__ __forceinline__ float get(int k) const {          // k a constant after unrolling
+        if constexpr (sizeof(IN) == 4) {
+            return __uint_as_float(wd[k]);
+        } else {
+            const uint16_t b = (uint16_t)((k & 1) ? wd[k / 2] >> 16 : wd[k / 2] & 0xFFFFu);
+            return to_f32(__builtin_bit_cast(IN, b));
+        }
+    }
+    __device__ __forceinline__ void set(int k, float x) {        // x exactly representable in IN
+        if constexpr (sizeof(IN) == 4) {
+            wd[k] = __float_as_uint(x);
+        } else {
+            const uint32_t b = __builtin_bit_cast(uint16_t, from_f32<IN>(x));
+            wd[k / 2] = (k & 1) ? ((wd[k / 2] & 0xFFFFu) | (b << 16)) : ((wd[k / 2] & 0xFFFF0000u) | b);
+        }
+    }
 };
 
 // Rows r < n of an fp32 staging area [.][D] in LDS rotated back by the canonical Walsh-Hadamard
@@ -779,7 +818,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     const float sm_log2 = p2 * rs;                            // exact: p2 is a power of two
     static_assert(NW == 2 || NW == 4 || NW == 8, "the tail splits 16 heads over 2 NW lane halves");
     static_assert(ST == 1 || ST == 2, "one or two page streams");
-    using AL = AfterLoop<D>;
+    using AL = AfterLoop<D, NW>;
     static_assert(2 * NW * R::SLOT >= AL::ML_OFF + 2 * NW * 16 * 4 + 16, "the after-loop scratch must fit");
     static_assert(2 * R::DMA <= 63, "vmcnt holds at most 63 loads");
     static_assert(2 * NW * R::SLOT >= 16 * D * 4, "ROT stages the chunk's q rows in the second array");
@@ -890,6 +929,21 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     for (int dt = 0; dt < DT; ++dt) o[dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     float m_run = -__builtin_inff(), l_run = 0.0f, vb_run = 0.0f;
 
+    // Partial page (last split): its exact-K scores are 16 x 16 x 4 fp32 MFMAs (fp32 products and
+    // sums) over all waves: wave w takes tokens 16 (w & 1) .. + 15 and part w >> 1 of the contraction
+    // (NKP = NW / 2 parts); lane: head (A row) and token (B column) lane % 16, dims [sdim, sdim + DS)
+    // (the 4 lane groups are the MFMA's contraction). The lane's K and q slices go out right after the
+    // first page DMAs and wait in registers until the loop ends (when they fit in 16 VGPRs, 32 at two
+    // waves); wave 0 issues the page's DMA into its slot 0 in place of its first empty issue of the
+    // last window, so both are in when the loop ends.
+    constexpr int NKP = AL::NKP, DS = D / (4 * NKP);
+    constexpr bool TPRE = 2 * Packed<IN, DS>::WORDS <= (NW == 2 ? 32 : 16);
+    const int tt = 16 * (w & 1) + r16, kp = w >> 1;
+    const int sdim = kp * (D / NKP) + q * DS;                          // first dim of the lane's slices
+    const IN* const ktail = tail_k + (((int64_t)tix * H + h) * PAGE + min(tt, tail_n - 1)) * D + sdim;
+    Packed<IN, DS> kpk, qpk;
+    bool tpre = false, tdma = false;                                   // slices loaded, page DMA issued
+
     // The split's pages go out in pairs (k: pages 2k, 2k + 1 of the window), over windows of WIN pages
     // whose block ids are first copied to an LDS table. Wave w takes pairs w, w + NW, ...: a fixed
     // assignment, so which wave sums which page, and in which order, never changes between calls
@@ -941,6 +995,11 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         KUSH_MARK(1);
         KUSH_ISSUE_PAIR(sl0, sl1, pa)
         if constexpr (!ROT) KUSH_ISSUE_PAIR(sl2, sl3, pb)
+        if (!ROT && TPRE && has_tail) {
+            kpk.load(ktail);
+            qpk.load(qg + qbase + (int64_t)min(r16, Gc - 1) * D + sdim);
+            tpre = true;
+        }
         if constexpr (ROT) {                                             // rotate, round to IN, regather
             float* const qst = reinterpret_cast<float*>(ringB);          // [16][D]
 #pragma unroll
@@ -960,6 +1019,12 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
             for (int kk = 0; kk < KSTEPS; ++kk)
 #pragma unroll
                 for (int j = 0; j < 8; ++j) qv[kk][j] = qst[min(hq, Gc - 1) * D + kdim<D, BITS>(kk, q, 0) + j];
+            if (TPRE && has_tail) {
+                kpk.load(ktail);
+#pragma unroll
+                for (int e = 0; e < DS; ++e) qpk.set(e, qst[min(r16, Gc - 1) * D + sdim + e]);
+                tpre = true;
+            }
         }
         // q' = q p2 as fp16 (+ its low part for fp32 q): qh, ql for the bias MFMAs; qa, qla the Q'
         // sources, divided by 16 in the int4 K-steps of high nibbles
@@ -988,7 +1053,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         // PV of both; then, every read of the
         // two slots complete (lgkmcnt 0), they take the next pair. The second page of a window's odd
         // last pair is masked.
-#define KUSH_STEP(SA, SB, P)                                                                       \
+#define KUSH_STEP(SA, SB, P, FIRST)                                                                \
     {                                                                                              \
         if ((P) >= pairs) break;                                                                   \
         KUSH_WAIT_VM(2 * R::DMA);                                                                  \
@@ -1014,14 +1079,17 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
             consume_pages<D, BITS, 2>(sp, o, vacc, sv, sa, kx, m_run, l_run, vb_run, lane);        \
         }                                                                                          \
         __builtin_amdgcn_s_waitcnt(0xC07F);                    /* lgkmcnt(0): slot reads done */    \
-        issue_page<D, BITS>(SA, nx < pairs, __builtin_amdgcn_readfirstlane(id2.x), head_base, bs, voff);  \
+        const bool tl = (FIRST) && w == 0 && has_tail && !tdma && nx >= pairs && wb + WIN >= p1;       \
+        issue_page<D, BITS>(SA, nx < pairs || tl, tl ? tail_blk : __builtin_amdgcn_readfirstlane(id2.x), \
+                            head_base, bs, voff);                                                  \
         issue_page<D, BITS>(SB, 2 * nx + 1 < wn, __builtin_amdgcn_readfirstlane(id2.y), head_base, bs, voff); \
+        tdma = tdma || tl;                                                                         \
         (P) = nx;                                                                                  \
     }
         for (;;) {
             for (;;) {
-                KUSH_STEP(sl0, sl1, pa)
-                KUSH_STEP(sl2, sl3, pb)
+                KUSH_STEP(sl0, sl1, pa, true)
+                KUSH_STEP(sl2, sl3, pb, false)
             }
             KUSH_MARK_WAVE();
             KUSH_WAIT_VM(0);                                     // drain the trailing (empty) issues
@@ -1042,79 +1110,51 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     }
     KUSH_MARK(3);
 
-    // partial last page (last split only): V rows from its record, staged by one wave in its slot 0;
-    // exact fp32 K . q scores from the tail by waves 0 and 1, with q (fp32, times sm log2 e) and the
-    // scores in the rings
+    // partial last page (last split only): V rows from its record in wave 0's slot 0 (issued in the
+    // loop, else now); the exact-K scores as set out before the loop, their NKP parts summed in order
     if (has_tail) {
         constexpr int QS = AL::QS;
-        float* const qs = reinterpret_cast<float*>(ringB + AL::Q_OFF);    // [16][QS] q sm log2e
-        float* const sc = reinterpret_cast<float*>(ringB + AL::SC_OFF);   // [16][PAGE] tail scores
-        const int ow = (p1 - p0) % NW;
-        uint8_t* const tslot = ringA + 2 * ow * R::SLOT;
-        if (w == ow) issue_page<D, BITS>(tslot, true, tail_blk, head_base, bs, voff);
-        // K . q as 16 x 16 x 4 fp32 MFMAs (fp32 products and sums): wave 0 takes tokens 0-15, wave 1
-        // tokens 16-31. Lane: head (A row) and token (B column) lane % 16, dims [q D/4, (q+1) D/4)
-        // (the 4 lane groups are the MFMA's contraction). Its K slice is loaded here, with the q
-        // rows below: one memory latency for both.
-        constexpr int DQ = D / 4, KP = DQ * (int)sizeof(IN) / 16;           // dims, 16-byte pieces per lane
-        const int tt = 16 * w + r16;                                     // this lane's token (waves 0, 1)
-        u4 kraw[KP];
-        if (w < 2) {
-            const IN* tk = tail_k + (((int64_t)tix * H + h) * PAGE + min(tt, tail_n - 1)) * D + q * DQ;
+        float* const qs = reinterpret_cast<float*>(ringB + AL::Q_OFF);    // [16][QS] rotated q (no prefetch)
+        float* const sc = reinterpret_cast<float*>(ringB + AL::SC_OFF);   // [NKP][16][PAGE] score parts
+        uint8_t* const tslot = ringA;                                      // wave 0's slot 0
+        if (w == 0 && !tdma) issue_page<D, BITS>(tslot, true, tail_blk, head_base, bs, voff);
+        if (!tpre) {                                                       // the slices now
+            kpk.load(ktail);
+            if constexpr (ROT) {                                           // rotated q rows, as in the prologue
+                for (int rr = (int)threadIdx.x / QCG; rr < 16; rr += QRP) {  // a row's lanes iterate together
+                    float x[16];
+                    load8(qg + qbase + (int64_t)min(rr, Gc - 1) * D + 8 * qc, reinterpret_cast<float(&)[8]>(x[0]));
+                    load8(qg + qbase + (int64_t)min(rr, Gc - 1) * D + D / 2 + 8 * qc,
+                          reinterpret_cast<float(&)[8]>(x[8]));
+                    fwht_runs<D>(x, qc);
 #pragma unroll
-            for (int i = 0; i < KP; ++i) kraw[i] = reinterpret_cast<const u4*>(tk)[i];
-        }
-        if constexpr (ROT) {                                             // rotated q rows, as in the prologue
-            for (int rr = (int)threadIdx.x / QCG; rr < 16; rr += QRP) {  // a row's lanes iterate together
-                float x[16];
-                load8(qg + qbase + (int64_t)min(rr, Gc - 1) * D + 8 * qc, reinterpret_cast<float(&)[8]>(x[0]));
-                load8(qg + qbase + (int64_t)min(rr, Gc - 1) * D + D / 2 + 8 * qc, reinterpret_cast<float(&)[8]>(x[8]));
-                fwht_runs<D>(x, qc);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    qs[rr * QS + 8 * qc + j] = rr < Gc ? to_f32(store_rounded<IN>(x[j])) * sm_log2 : 0.0f;
-                    qs[rr * QS + D / 2 + 8 * qc + j] = rr < Gc ? to_f32(store_rounded<IN>(x[8 + j])) * sm_log2 : 0.0f;
+                    for (int j = 0; j < 8; ++j) {
+                        qs[rr * QS + 8 * qc + j] = to_f32(store_rounded<IN>(x[j]));
+                        qs[rr * QS + D / 2 + 8 * qc + j] = to_f32(store_rounded<IN>(x[8 + j]));
+                    }
                 }
-            }
-        } else {                                                 // 8-element pieces, all loads in flight
-            constexpr int QP = 16 * D / 8, QPT = (QP + NW * WAVE - 1) / (NW * WAVE);
-            float xq[QPT][8];
+                __syncthreads();
 #pragma unroll
-            for (int k = 0; k < QPT; ++k)                        // unconditional (a valid piece), no branch
-                load8(qg + qbase + (int64_t)min((int)threadIdx.x + k * NW * WAVE, Gc * (D / 8) - 1) * 8, xq[k]);
-#pragma unroll
-            for (int k = 0; k < QPT; ++k) {
-                const int pc = (int)threadIdx.x + k * NW * WAVE;
-                if (pc < QP) {
-                    float* const dst = qs + (pc / (D / 8)) * QS + (pc % (D / 8)) * 8;
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) dst[j] = pc < Gc * (D / 8) ? xq[k][j] * sm_log2 : 0.0f;
-                }
+                for (int e = 0; e < DS; ++e) qpk.set(e, qs[min(r16, Gc - 1) * QS + sdim + e]);
+            } else {
+                qpk.load(qg + qbase + (int64_t)min(r16, Gc - 1) * D + sdim);
             }
         }
+        f4 c = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int e = 0; e < DS; ++e) c = __builtin_amdgcn_mfma_f32_16x16x4f32(qpk.get(e) * sm_log2, kpk.get(e), c, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[(kp * 16 + 4 * q + i) * PAGE + tt] = tt < tail_n ? c[i] : -__builtin_inff();
         __syncthreads();
-        if (w < 2) {
-            f4 c = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int j = 0; j < DQ; j += 8) {
-                float kx[8];
-                load8(reinterpret_cast<const IN*>(kraw) + j, kx);
-                const f4 qa = *reinterpret_cast<const f4*>(&qs[r16 * QS + q * DQ + j]);
-                const f4 qb = *reinterpret_cast<const f4*>(&qs[r16 * QS + q * DQ + j + 4]);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) c = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[e], kx[e], c, 0, 0, 0);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) c = __builtin_amdgcn_mfma_f32_16x16x4f32(qb[e], kx[4 + e], c, 0, 0, 0);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sc[(4 * q + i) * PAGE + tt] = tt < tail_n ? c[i] : -__builtin_inff();
-        }
-        __syncthreads();
-        if (w == ow) {
+        if (w == 0) {
             float x[1][8];
 #pragma unroll
-            for (int jj = 0; jj < 8; ++jj)
-                x[0][jj] = ST == 2 && r16 >= 8 ? -__builtin_inff() : sc[r16 * PAGE + tok(q, jj)];
+            for (int jj = 0; jj < 8; ++jj) {
+                float v = 0.0f;
+#pragma unroll
+                for (int k = 0; k < NKP; ++k) v += sc[(k * 16 + r16) * PAGE + tok(q, jj)];
+                x[0][jj] = ST == 2 && r16 >= 8 ? -__builtin_inff() : v;
+            }
             KUSH_WAIT_VM(0);
             if constexpr (ST == 2) {                             // stream 0 takes the page
                 consume2<D, BITS>(tslot, 0, o, vacc, x[0], 1.0f, 0.0f, m_run, l_run, vb_run, lane);
