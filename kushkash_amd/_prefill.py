@@ -201,7 +201,8 @@ class ExtendPlan:
         """Attention of the step's queries q3 [T, Hq, D] (rows in request order) over each request's
         cached history and its new rows k3, v3 [T, Hk, D], reading the cache as it was before this
         step's write. varlen(q, k, v, group, scale, out): an optional varlen attention kernel for packed
-        groups (causal, queries at the end of each request's keys); default: ragged_attention."""
+        groups (causal, queries at the end of each request's keys); default: ragged_attention (torch's
+        flash-attention kernel in its varlen form for bf16 / fp16 on the GPU)."""
         out = torch.empty(q3.shape, dtype=q3.dtype, device=q3.device) if out is None else out
         qs = self.q_start_host
         for g in self.groups:
@@ -220,7 +221,8 @@ class ExtendPlan:
                 if varlen is not None:
                     varlen(q3[a:b], kp, vp, g, scale, out[a:b])
                 else:
-                    out[a:b] = ragged_attention(q3[a:b], kp, vp, local, g.key_start, scale)
+                    out[a:b] = ragged_attention(q3[a:b], kp, vp, local, g.key_start, scale,
+                                                varlen=(g.cu_q, g.cu_k, g.max_q, g.max_k))
             else:
                 r = g.r0
 

@@ -118,6 +118,25 @@ def test_split_k_matches_oracle(ns, waves, fused, monkeypatch):
     assert int(c.ops._sync.abs().sum()) == 0
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("waves,ns", [(2, 1), (4, 1), (8, 1), (4, 2)])
+def test_windows_then_partial_page(bits, waves, ns):
+    """A split over more than two 1,024-page windows of block ids that ends in a 13-token partial
+    page: the page loop reloads its id table between windows, and the partial page's record goes out
+    from inside the last window. Against the oracle."""
+    torch.manual_seed(bits * 10 + waves + ns)
+    B, H, G, D, N = 1, 2, 4, 128, 32 * 2100 + 13
+    c = kk.KushCache(1, H, H * G, D, batch_size=B, bits=bits, device=DEV, dtype=torch.bfloat16, rotate=False)
+    K = torch.randn(B, H, N, D, device=DEV, dtype=torch.bfloat16)
+    c.write(0, K, K.flip(2))
+    work = torch.empty(B * H * ns * G * (D + 2), dtype=torch.float32, device=DEV)
+    q = torch.randn(B, H * G, D, device=DEV, dtype=torch.bfloat16)
+    out = torch.empty_like(q)
+    c.ops.decode(q, out, c.pool[0], c.block_table, c.seq_lens[0], c.tail_idx, c.tail_k[0], c.scale, ns, work,
+                 waves=waves)
+    assert_out_close(out, oracle_decode(c, 0, q), torch.bfloat16, what=f"{N} tokens")
+
+
 def test_empty_and_short_sequences():
     """Sequences of 0, 1, 31, 32 and 33 tokens in one batch (ragged lengths through the raw Ops):
     an empty sequence decodes to zeros, as the reference's l = 0 branch."""
