@@ -19,15 +19,31 @@ the same way). The fused kernel keeps no score matrix: only K / V bound its bloc
 from __future__ import annotations
 
 import os
+from functools import lru_cache
 
 import torch
 
 from ._records import PAGE, as_records, dequant_records
 
 
+@lru_cache(None)
+def _flash_takes(dtype: torch.dtype, head_dim: int, device: torch.device) -> bool:
+    """Whether torch's flash-attention kernel runs for this dtype and head size on this device: one call
+    on a single query and key, once per process and shape."""
+    x = torch.zeros(1, 1, 1, head_dim, dtype=dtype, device=device)
+    try:
+        torch.ops.aten._flash_attention_forward(x, x, x, None, None, 1, 1, 0.0, False, False, scale=1.0)
+        return True
+    except RuntimeError:
+        return False
+
+
 def fused_ok(q: torch.Tensor) -> bool:
-    """Whether torch's flash-attention kernel takes q: bf16 / fp16 on the GPU, unless KUSHKASH_ATTN=fp32."""
-    return q.is_cuda and q.dtype in (torch.bfloat16, torch.float16) and os.environ.get("KUSHKASH_ATTN") != "fp32"
+    """Whether torch's flash-attention kernel takes q: bf16 / fp16 on the GPU at a head size it runs,
+    unless KUSHKASH_ATTN=fp32. Block sizes follow this answer, so a refused shape never gets blocks
+    sized for the fused kernel."""
+    return (q.is_cuda and q.dtype in (torch.bfloat16, torch.float16) and os.environ.get("KUSHKASH_ATTN") != "fp32"
+            and _flash_takes(q.dtype, q.shape[-1], q.device))
 
 
 def _flash(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, scale: float):
@@ -66,6 +82,12 @@ def attn_lse(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool, sc
         r = _flash(q, k, v, causal, scale)
         if r is not None:
             return r
+        n = keys_per_block(q, Hk, 2 * B * Hk * D * 4, 1 << 28, 1)     # refused: products, scores bounded
+        if not causal and n < N:
+            acc = None
+            for j0 in range(0, N, n):
+                acc = merge(acc, attn_lse(q, k[:, :, j0:j0 + n], v[:, :, j0:j0 + n], False, scale))
+            return acc
     g = Hq // Hk
     qf = q.reshape(B, Hk, g * T, D).float()
     s = torch.matmul(qf, k.float().transpose(-1, -2).contiguous()).mul_(scale)      # [B, Hk, gT, N]
