@@ -79,6 +79,21 @@ def test_lse_merge_identity():
     assert torch.allclose(acc[0], full[0], atol=1e-5) and torch.allclose(acc[1], full[1], atol=1e-5)
 
 
+def test_fused_refusal_falls_back_to_bounded_products(monkeypatch):
+    """attn_lse(fused=True) when the flash kernel refuses a block it was told to take: the fp32 products
+    over key sub-blocks sized for their scores, merged by log-sum-exp, the same as one product."""
+    from kushkash_amd import _attention as A
+    monkeypatch.setattr(A, "fused_ok", lambda q: True)
+    monkeypatch.setattr(A, "_flash", lambda *a, **k: None)
+    monkeypatch.setattr(A, "keys_per_block", lambda *a, **k: 16)            # force several sub-blocks
+    torch.manual_seed(1)
+    q = torch.randn(2, 6, 3, 64)
+    k, v = torch.randn(2, 2, 100, 64), torch.randn(2, 2, 100, 64)
+    out, lse = A.attn_lse(q, k, v, False, 0.125, fused=True)
+    ref_out, ref_lse = A.attn_lse(q, k, v, False, 0.125)
+    assert torch.allclose(out, ref_out, atol=1e-5) and torch.allclose(lse, ref_lse, atol=1e-5)
+
+
 @pytest.mark.parametrize("bits", [4, 8])
 def test_dequant_token_major(bits):
     """token_major=True = the default layout with page and head axes swapped, contiguous."""
