@@ -16,10 +16,11 @@ cache.
 
 Timing: the library calls of a step are recorded once from the product's own Ops calls (for C2 over
 the allocated buffers before the records are written, so the data generation then keeps the GPU busy
-up to the warm-up); --warmup steps run untimed, the host synchronizes, and exactly --steps steps are
-launched back to back between HIP events, followed by a synchronization. At ~5 us of host time per
-launch the host stays ahead of the GPU from the first step, so the window holds the steps' kernels
-only. --graph-replay times the reference's way instead (bench/bench_decode.py:28-51: a one-step HIP
+up to the warm-up); --warmup steps run untimed, the last four of them launched after a host
+synchronization, and exactly --steps steps are launched back to back between HIP events, followed by
+a synchronization. The last warm-up step keeps the GPU busy while the start event and the first timed
+launches are issued, and at ~5 us of host time per launch the host then stays ahead of the GPU, so
+the window holds the steps' kernels only. --graph-replay times the reference's way instead (bench/bench_decode.py:28-51: a one-step HIP
 graph replayed back to back), which on ROCm adds ~5 us of device-side overhead per replay (C2: 37.8
 us per step against 32.5 launched). The default warm-up of 1,000 steps (~33 ms for C2) brings the GPU
 to its steady clocks.
@@ -229,11 +230,17 @@ class Launches:
 
 
 def time_launches(launches: Launches, steps: int, warmup: int) -> float:
-    """Mean ms per step: `warmup` untimed steps, a host synchronization, then exactly `steps` steps
-    between HIP events on the launch stream, and a synchronization."""
-    launches.run(0, warmup)
-    torch.cuda.synchronize()
+    """Mean ms per step: `warmup` untimed steps, the last four of them launched after a host
+    synchronization, then exactly `steps` steps between HIP events on the launch stream, and a
+    synchronization. On a GPU left idle by the synchronization the start event fires at once while
+    the first timed kernel is still being launched (~20 us later, per the kernel trace of a 20-step
+    run: ~1 us per step); with warm-up steps still running, the event fires as they end, with the
+    first timed launches already queued behind it."""
+    tail = min(4, warmup)                     # warm-up steps launched after the synchronization
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    launches.run(0, warmup - tail)
+    torch.cuda.synchronize()
+    launches.run(warmup - tail, tail)
     a.record()
     launches.run(warmup, steps)
     b.record()
@@ -243,8 +250,9 @@ def time_launches(launches: Launches, steps: int, warmup: int) -> float:
 
 def time_graph(step, steps: int, warmup: int, period: int = 1) -> float:
     """--graph-replay, the reference's method (bench/bench_decode.py:28-51): each step of the period
-    captured as a HIP graph of its own, `warmup` untimed replays, a host synchronization, then exactly
-    `steps` replays issued back to back between HIP events, and a synchronization."""
+    captured as a HIP graph of its own, `warmup` untimed replays (the last four after a host
+    synchronization, as in time_launches), then exactly `steps` replays issued back to back between
+    HIP events, and a synchronization."""
     graphs = []
     for i in range(period):
         step(i)                              # eager call first (lazy init outside the capture)
@@ -254,10 +262,13 @@ def time_graph(step, steps: int, warmup: int, period: int = 1) -> float:
             step(i)
         graphs.append(g)
     torch.cuda.synchronize()
-    for i in range(warmup):
+    tail = min(4, warmup)                     # as time_launches: the last warm-up replays after the sync
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for i in range(warmup - tail):
         graphs[i % period].replay()
     torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for i in range(warmup - tail, warmup):
+        graphs[i % period].replay()
     a.record()
     for i in range(warmup, warmup + steps):
         graphs[i % period].replay()
