@@ -346,15 +346,18 @@ def _b(x) -> str:
     return "true" if x else "false"
 
 
-def decode_kernel_name(D: int, bits: int, dtype, waves: int, G: int, rot: bool) -> str:
+def decode_kernel_name(D: int, bits: int, dtype, waves: int, G: int, rot: bool, ns: int = 1, chunks: int = 0) -> str:
     """The instantiation kush_decode launches, as rocprofv3 names it: the requested waves unless the
     configuration's page ring does not fit in LDS (4 KB of block ids + 4 slots per wave of one record
-    each, within 160 KiB), two page streams when G <= 8."""
+    each, within 160 KiB), two page streams when G <= 8, and wave splits as kush_decode.hip's
+    wave_splits picks them for ns splits over `chunks` (sequences x kv heads x head chunks)."""
     from kushkash_amd._ops import record_bytes
     nw = waves or 8
     while nw > 2 and 4 * nw * record_bytes(D, bits) + 4 * 1024 + 16 > 160 * 1024:
         nw //= 2
-    return f"kush::decode_kernel<{D}, {bits}, {_IN[dtype]}, {nw}, {2 if G <= 8 else 1}, {_b(rot)}>"
+    env = os.environ.get("KUSHKASH_AMD_WAVE_SPLITS", "")
+    ws = nw == 4 and ns % nw == 0 and ns >= 2 * nw and (env[:1] == "1" or (env[:1] != "0" and chunks * (ns // nw) >= 256))
+    return f"kush::decode_kernel<{D}, {bits}, {_IN[dtype]}, {nw}, {2 if G <= 8 else 1}, {_b(rot)}, {_b(ws)}>"
 
 
 # the translation unit of each kernel family (its digest covers the unit and its headers)
@@ -624,7 +627,7 @@ def bench_c4(a) -> None:
               {"workload": f"C4 Qwen3-8B layer: {Hq} q / {Hkv} kv heads, D {D}, int{bits}, page 32, "
                            f"batch {B} x {N} tokens, splits {ns}, waves {wv}", "global_batch": B, "seq_len": N,
                "split_k": ns, "waves": wv, "split_k_policy": ns == policy},
-              decode_kernel_name(D, bits, dtype, wv, G, False),
+              decode_kernel_name(D, bits, dtype, wv, G, False, ns, B * Hkv * -(-G // 16)),
               traffic_md="decode_c4_traffic.md", extra={"merge": "split-K partials merged inside the launch"})
 
 
@@ -784,7 +787,7 @@ def bench_timeline(a) -> None:
     ops, B, Hkv, G, D = w["ops"], w["B"], w["Hkv"], w["G"], w["D"]
     ns = a.splits or ops.splits(B, Hkv, w["N"] // PAGE)
     wv = a.waves or ops.waves(B, Hkv, ns, w["pages"])
-    kernel = decode_kernel_name(a.dim, a.bits, ops.dtype, wv, G, False)
+    kernel = decode_kernel_name(a.dim, a.bits, ops.dtype, wv, G, False, ns, B * Hkv * -(-G // 16))
     out = torch.empty_like(w["q"])
     work = torch.empty(max(1, B * Hkv * ns * G * (D + 2)), dtype=torch.float32, device="cuda:0")
     sm = 1.0 / math.sqrt(D)
@@ -880,7 +883,7 @@ def main(argv=None):
              f"batch {a.batch} x {a.ctx} tokens" + (", rotation folded into the kernels" if a.rot else "")
              + ("" if a.dtype == "bf16" else f", {a.dtype}"))
     workload = f"{shape}, splits {ns}, waves {wv}"
-    kernel = decode_kernel_name(a.dim, a.bits, w["ops"].dtype, wv, w["G"], a.rot)
+    kernel = decode_kernel_name(a.dim, a.bits, w["ops"].dtype, wv, w["G"], a.rot, ns, w["B"] * w["Hkv"] * -(-w["G"] // 16))
     ms_dec = ms                                   # one kernel per step: the decode kernel is the step
     gbs = alg / ms / 1e6
     gbs_dec = alg / ms_dec / 1e6
@@ -920,7 +923,8 @@ def main(argv=None):
         _line(res["metric"], msx * 1e3, alg, {"workload": f"{shape}, splits {sns}, waves {swv}",
                                               "global_batch": a.batch, "seq_len": a.ctx, "split_k": sns,
                                               "waves": swv, "sweep": True},
-              decode_kernel_name(a.dim, a.bits, w["ops"].dtype, swv, w["G"], a.rot))
+              decode_kernel_name(a.dim, a.bits, w["ops"].dtype, swv, w["G"], a.rot, sns,
+                                 w["B"] * w["Hkv"] * -(-w["G"] // 16)))
 
 
 if __name__ == "__main__":

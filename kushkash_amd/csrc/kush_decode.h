@@ -322,6 +322,24 @@ __device__ __forceinline__ void consume_pages(const uint8_t* const (&slot)[NP], 
     for (int p = 0; p < NP; ++p) vacc = mfma16(neg_half, pw[p], vacc);
 }
 
+// Wave splits: one wave stores the n (<= N * 64) block ids of its window, ids[0 .. n), into its own
+// table region tb, every id load in flight at once. Kept out of the workgroup's window lambda, whose
+// code the other kernels share unchanged.
+template <int N>
+__device__ __forceinline__ void load_wave_window(int* tb, const int32_t* ids, int n, int lane) {
+    int v[N];
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        const int i = lane + k * WAVE;
+        v[k] = i < n ? ids[i] : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        const int i = lane + k * WAVE;
+        if (i < n) tb[i] = v[k];
+    }
+}
+
 // Stage the record of block blk into LDS at dst: R::DMA buffer-to-LDS loads of 1 KB. An invalid page
 // (past the window's last) gets an empty buffer range: the loads then fill the slot with zeros and
 // touch no memory, and still count in vmcnt like a real page.
@@ -800,7 +818,7 @@ __device__ void merge_splits(const float* __restrict__ part_ml, const float* __r
 // NS > 1: each workgroup writes its split's partials; with `sync` (one zeroed int32 per
 // (sequence, kv head, head chunk)), the last workgroup of a (sequence, kv head, head chunk) to
 // finish merges all splits into `out` and resets its counter, so no second launch is needed.
-template <int D, int BITS, typename IN, int NW, int ST, bool ROT>
+template <int D, int BITS, typename IN, int NW, int ST, bool ROT, bool WS>
 __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) void decode_kernel(
     const IN* __restrict__ qg, IN* __restrict__ out, uint8_t* __restrict__ cache, int64_t bs, int64_t hs,
     IN* __restrict__ tail_k, const int32_t* __restrict__ tail_idx, const int32_t* __restrict__ block_table,
@@ -808,6 +826,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     float* __restrict__ part_ml, float* __restrict__ part_o, int32_t* __restrict__ sync,
     const int32_t* __restrict__ seq_order, const IN* __restrict__ app_k, const IN* __restrict__ app_v, int64_t app_ks,
     int64_t app_vs) {
+    constexpr bool ws = WS;
     using F = Fmt<D, BITS>;
     using R = Ring<D, BITS>;
     constexpr int KSTEPS = D / 32;
@@ -846,7 +865,13 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         s = seq_order[L / H];
         h = L % H;
     }
-    const int z = blockIdx.z % NS, gc = blockIdx.z / NS, g0 = gc * 16;
+    // ws (wave splits, NS a multiple of NW): each wave takes a whole split of its own -- splits zg NW + w
+    // of workgroup zg -- with its own block-id table and no merge with the other waves; else the
+    // waves of a workgroup share its split's pages
+    const int NSG = ws ? NS / NW : NS;                                    // workgroups per head chunk
+    const int zg = blockIdx.z % NSG, gc = blockIdx.z / NSG, g0 = gc * 16;
+    const int z = ws ? zg * NW + w : zg;                                  // this wave's split
+    const int tw = ws ? NW - 1 : 0;                                       // the wave taking the partial page
     const int Gc = min(16, G - g0);
 
     const int32_t* bt = block_table + (int64_t)s * bt_stride;
@@ -876,7 +901,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         for (int kk = 0; kk < KSTEPS; ++kk) load8(qg + qbase + (int64_t)min(hq, Gc - 1) * D + kdim<D, BITS>(kk, q, 0), qv[kk]);
     }
     constexpr int PRE = WIN / (NW * WAVE);                               // prefetched ids per thread
-    const int npre = z == 0 ? min(WIN, bt_cols) : 0;
+    const int npre = !ws && z == 0 ? min(WIN, bt_cols) : 0;
     int pre[PRE];
 #pragma unroll
     for (int k = 0; k < PRE; ++k) {
@@ -889,6 +914,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     const int full = n / PAGE, tail_n = n % PAGE;
     const int pps = (full + NS - 1) / NS;
     const int p0 = min(full, z * pps), p1 = min(full, p0 + pps);
+    const int wp1 = ws ? min(full, (zg + 1) * NW * pps) : p1, wp0 = ws ? min(full, zg * NW * pps) : p0;
     const uint8_t* head_base = cache + (int64_t)h * hs;
 
     // Fused append (app_k): the token at position n - 1 of sequence s, kv head h, is written by the one
@@ -900,7 +926,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         if (gc == 0 && n > 0) {
             const int pos = n - 1, slot = pos % PAGE, pg = pos / PAGE;
             const int owner = slot == PAGE - 1 ? pg / max(pps, 1) : NS - 1;
-            if (z == owner) {
+            if (zg == (ws ? owner / NW : owner)) {                  // the whole workgroup
                 const IN* krow = app_k + (int64_t)s * app_ks + (int64_t)h * D;
                 IN* tail = tail_k + ((int64_t)tix * H + h) * PAGE * D;
                 uint8_t* rec = cache + (int64_t)bt[pg] * bs + (int64_t)h * hs;
@@ -912,7 +938,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         }
         __syncthreads();
     }
-    const bool has_tail = tail_n > 0 && z == NS - 1;
+    const bool has_tail = tail_n > 0 && zg == NSG - 1;                 // the workgroup holds the last split
     const int tail_blk = has_tail ? bt[full] : 0;                      // in before the page loop starts
     uint8_t* const sl0 = ringA + 2 * w * R::SLOT;
     uint8_t* const sl1 = sl0 + R::SLOT;
@@ -953,8 +979,14 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     // grow, so once the pair it would consume is past the window's end, so is the one in flight. Each
     // pair issue is 2 R::DMA instructions, also for a pair past the end (an empty buffer range: no
     // memory access), so vmcnt counts stay exact.
-    if (p1 > p0) {
-        int wb = p0, wn = min(WIN, p1 - p0), pairs = (wn + 1) / 2;
+    if (wp1 > wp0) {                                                     // the workgroup has pages (uniform)
+        // windows of TW pages in the table region tb: the workgroup's (ws: the wave's own, a wave with
+        // no pages of its own runs empty pairs)
+        constexpr int TWS = WIN / NW;
+        const int TW = ws ? TWS : WIN;
+        int* const tb = tbl + (ws ? w * TWS : 0);
+        const int PS = ws ? 1 : NW;                                      // the wave's pair stride
+        int wb = p0, wn = min(TW, p1 - p0), pairs = (wn + 1) / 2;
         const auto load_window = [&]() {
             if (wb == 0 && wn <= npre) {                                 // split 0's first window, prefetched
 #pragma unroll
@@ -978,14 +1010,15 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         };
 #define KUSH_ISSUE_PAIR(SA, SB, P)                                                                 \
     {                                                                                              \
-        const int2 id2 = *reinterpret_cast<const int2*>(tbl + min(2 * (P), WIN - 2));              \
+        const int2 id2 = *reinterpret_cast<const int2*>(tb + min(2 * (P), TW - 2));                \
         issue_page<D, BITS>(SA, (P) < pairs, __builtin_amdgcn_readfirstlane(id2.x), head_base, bs, voff);  \
         issue_page<D, BITS>(SB, 2 * (P) + 1 < wn, __builtin_amdgcn_readfirstlane(id2.y), head_base, bs, voff); \
     }
         // the window's ids are stored and every load of the compiler's is in before the barrier: no
         // vector memory load of the compiler's is outstanding once the page DMAs start
-        load_window();
-        int pa = w, pb = NW + w;                                         // the pairs in slots (0, 1), (2, 3)
+        if constexpr (WS) load_wave_window<PRE>(tb, bt + wb, wn, lane);
+        else load_window();
+        int pa = ws ? 0 : w, pb = pa + PS;                               // the pairs in slots (0, 1), (2, 3)
         // The first pairs go out before q is prepared: every compiler load in (vmcnt 0, so no later
         // wait of the compiler's counts the DMAs), the table's barrier, pair pa's DMAs into the first
         // array and pair pb's into the second; a rotated q is staged in the second array instead,
@@ -1058,7 +1091,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         if ((P) >= pairs) break;                                                                   \
         KUSH_WAIT_VM(2 * R::DMA);                                                                  \
         if ((P) == 0) KUSH_MARK(2);                                                                \
-        const int nx = (P) + 2 * NW;                     /* this wave's pair after next */          \
+        const int nx = (P) + 2 * PS;                     /* this wave's pair after next */          \
         int2 id2;                                                                                  \
         if constexpr (ST == 2) {                                                                   \
             float sv[8], kx;                                                                       \
@@ -1066,7 +1099,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
             if (2 * (P) + 1 >= wn && r16 >= 8) {                                                   \
                 _Pragma("unroll") for (int jj = 0; jj < 8; ++jj) sv[jj] = -__builtin_inff();       \
             }                                                                                      \
-            id2 = *reinterpret_cast<const int2*>(tbl + min(2 * nx, WIN - 2));                      \
+            id2 = *reinterpret_cast<const int2*>(tb + min(2 * nx, TW - 2));                        \
             consume2<D, BITS>(SA, R::SLOT, o, vacc, sv, sa, kx, m_run, l_run, vb_run, lane);       \
         } else {                                                                                   \
             const uint8_t* const sp[2] = {SA, SB};                                                 \
@@ -1075,11 +1108,11 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
             if (2 * (P) + 1 >= wn) {                                                               \
                 _Pragma("unroll") for (int jj = 0; jj < 8; ++jj) sv[1][jj] = -__builtin_inff();    \
             }                                                                                      \
-            id2 = *reinterpret_cast<const int2*>(tbl + min(2 * nx, WIN - 2));                      \
+            id2 = *reinterpret_cast<const int2*>(tb + min(2 * nx, TW - 2));                        \
             consume_pages<D, BITS, 2>(sp, o, vacc, sv, sa, kx, m_run, l_run, vb_run, lane);        \
         }                                                                                          \
         __builtin_amdgcn_s_waitcnt(0xC07F);                    /* lgkmcnt(0): slot reads done */    \
-        const bool tl = (FIRST) && w == 0 && has_tail && !tdma && nx >= pairs && wb + WIN >= p1;       \
+        const bool tl = (FIRST) && w == tw && has_tail && !tdma && nx >= pairs && wb + TW >= p1;       \
         issue_page<D, BITS>(SA, nx < pairs || tl, tl ? tail_blk : __builtin_amdgcn_readfirstlane(id2.x), \
                             head_base, bs, voff);                                                  \
         issue_page<D, BITS>(SB, 2 * nx + 1 < wn, __builtin_amdgcn_readfirstlane(id2.y), head_base, bs, voff); \
@@ -1093,31 +1126,33 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
             }
             KUSH_MARK_WAVE();
             KUSH_WAIT_VM(0);                                     // drain the trailing (empty) issues
-            __syncthreads();                                     // table and rings idle
-            wb += WIN;
+            if (!ws) __syncthreads();                            // table and rings idle (ws: the wave's own)
+            wb += TW;
             if (wb >= p1) break;
-            wn = min(WIN, p1 - wb);
+            wn = min(TW, p1 - wb);
             pairs = (wn + 1) / 2;
-            pa = w;
-            pb = NW + w;
-            load_window();
-            __syncthreads();
+            pa = ws ? 0 : w;
+            pb = pa + PS;
+            if constexpr (WS) load_wave_window<PRE>(tb, bt + wb, wn, lane);   // a wave's DS operations stay in order
+            else load_window();
+            if (!ws) __syncthreads();
             KUSH_ISSUE_PAIR(sl0, sl1, pa)
             KUSH_ISSUE_PAIR(sl2, sl3, pb)
         }
+        if (ws) __syncthreads();                                 // every wave's pages done: rings idle
 #undef KUSH_STEP
 #undef KUSH_ISSUE_PAIR
     }
     KUSH_MARK(3);
 
-    // partial last page (last split only): V rows from its record in wave 0's slot 0 (issued in the
+    // partial last page (last split only): V rows from its record in wave tw's slot 0 (issued in the
     // loop, else now); the exact-K scores as set out before the loop, their NKP parts summed in order
     if (has_tail) {
         constexpr int QS = AL::QS;
         float* const qs = reinterpret_cast<float*>(ringB + AL::Q_OFF);    // [16][QS] rotated q (no prefetch)
         float* const sc = reinterpret_cast<float*>(ringB + AL::SC_OFF);   // [NKP][16][PAGE] score parts
-        uint8_t* const tslot = ringA;                                      // wave 0's slot 0
-        if (w == 0 && !tdma) issue_page<D, BITS>(tslot, true, tail_blk, head_base, bs, voff);
+        uint8_t* const tslot = ringA + 2 * tw * R::SLOT;                   // wave tw's slot 0
+        if (w == tw && !tdma) issue_page<D, BITS>(tslot, true, tail_blk, head_base, bs, voff);
         if (!tpre) {                                                       // the slices now
             kpk.load(ktail);
             if constexpr (ROT) {                                           // rotated q rows, as in the prologue
@@ -1146,7 +1181,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
 #pragma unroll
         for (int i = 0; i < 4; ++i) sc[(kp * 16 + 4 * q + i) * PAGE + tt] = tt < tail_n ? c[i] : -__builtin_inff();
         __syncthreads();
-        if (w == 0) {
+        if (w == tw) {
             float x[1][8];
 #pragma unroll
             for (int jj = 0; jj < 8; ++jj) {
@@ -1172,7 +1207,8 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     // columns in the idle rings (region of wave ww: 16 D floats, dims d as [d / 4][column][d % 4],
     // one 16-byte store per lane and tile). After a second barrier wave w sums tiles w, w + NW, ...
     // over the waves (and a head's two stream columns) and writes them out. No lane shuffles or
-    // masked stores: on one wave per SIMD this tail is latency-bound.
+    // masked stores: on one wave per SIMD this tail is latency-bound. ws: every wave its own split,
+    // so the same steps over its own columns only, all its tiles.
     constexpr int OBYTES = 16 * D * 4;
     static_assert(NW * OBYTES <= 2 * NW * R::SLOT, "the merge needs 16 D floats per wave in the first array");
     l_run = rows_sum(l_run);
@@ -1198,13 +1234,15 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
 #pragma unroll
     for (int ww = 0; ww < NW; ++ww)
 #pragma unroll
-        for (int c2 = 0; c2 < ST; ++c2) M = __builtin_fmaxf(M, mv[ww][c2]);
+        for (int c2 = 0; c2 < ST; ++c2)
+            if (!ws || ww == w) M = __builtin_fmaxf(M, mv[ww][c2]);
     float L = 0.0f;
     if (M > -__builtin_inff()) {
 #pragma unroll
         for (int ww = 0; ww < NW; ++ww)
 #pragma unroll
-            for (int c2 = 0; c2 < ST; ++c2) L += lv[ww][c2] * __builtin_amdgcn_exp2f(mv[ww][c2] - M);
+            for (int c2 = 0; c2 < ST; ++c2)
+                if (!ws || ww == w) L += lv[ww][c2] * __builtin_amdgcn_exp2f(mv[ww][c2] - M);
     }
     const float inv_l = L > 0.0f ? 1.0f / L : 0.0f;
     {
@@ -1224,19 +1262,28 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     const bool out_vec = (((uintptr_t)out) & 15) == 0;
     const int hcol = ST == 2 ? (r16 & 7) : r16;                  // the (first) column of head r16
     float* const ostage = reinterpret_cast<float*>(ringB + AL::Q_OFF);   // ROT: [16][D] output rows
-    for (int dt = w; dt < DT; dt += NW) {
-        f4 part[NW][ST];                                         // every wave's pieces, read together
-#pragma unroll
-        for (int ww = 0; ww < NW; ++ww)
+    for (int dt = ws ? 0 : w; dt < DT; dt += ws ? 1 : NW) {
+        f4 acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (WS) {                                      // this wave's own pieces
+            f4 part[ST];
 #pragma unroll
             for (int c2 = 0; c2 < ST; ++c2)
-                part[ww][c2] = *reinterpret_cast<const f4*>(ringA + ww * OBYTES +
-                                                            (((4 * dt + q) * 16 + hcol + 8 * c2) * 4) * 4);
-        f4 acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
+                part[c2] = *reinterpret_cast<const f4*>(ringA + w * OBYTES + (((4 * dt + q) * 16 + hcol + 8 * c2) * 4) * 4);
 #pragma unroll
-        for (int ww = 0; ww < NW; ++ww)
+            for (int c2 = 0; c2 < ST; ++c2) acc += part[c2];
+        } else {
+            f4 part[NW][ST];                                     // every wave's pieces, read together
 #pragma unroll
-            for (int c2 = 0; c2 < ST; ++c2) acc += part[ww][c2];
+            for (int ww = 0; ww < NW; ++ww)
+#pragma unroll
+                for (int c2 = 0; c2 < ST; ++c2)
+                    part[ww][c2] = *reinterpret_cast<const f4*>(ringA + ww * OBYTES +
+                                                                (((4 * dt + q) * 16 + hcol + 8 * c2) * 4) * 4);
+#pragma unroll
+            for (int ww = 0; ww < NW; ++ww)
+#pragma unroll
+                for (int c2 = 0; c2 < ST; ++c2) acc += part[ww][c2];
+        }
         if (r16 < Gc) {
             const int d0 = 16 * dt + 4 * q;
             if (ROT && NS == 1) {                                // fp32 rows, rotated below
@@ -1267,7 +1314,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         store_rotated<D, IN, NW * WAVE>(out + qbase, ostage, Gc, out_vec);
     }
     KUSH_MARK(4);
-    if (NS > 1 && w == 0 && q == 0 && r16 < Gc) {
+    if (NS > 1 && (ws || w == 0) && q == 0 && r16 < Gc) {
         publish(part_ml + 2 * pb, M);
         publish(part_ml + 2 * pb + 1, L);
     }
@@ -1281,11 +1328,11 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     KUSH_WAIT_VM(0);
     __syncthreads();
     if (threadIdx.x == 0) {
-        const int n_gc = gridDim.z / NS;
+        const int n_gc = gridDim.z / NSG;
         int32_t* ctr = sync + ((int64_t)s * H + h) * n_gc + gc;
         const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *last_flag = prev == NS - 1;
-        if (prev == NS - 1) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *last_flag = prev == NSG - 1;                            // one count per workgroup (ws: NW splits)
+        if (prev == NSG - 1) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!*last_flag) return;
@@ -1404,7 +1451,7 @@ int launch_decode(dim3 grid, hipStream_t stream, const void* q, void* out, const
                          int64_t hs, const void* tail_k, const int32_t* tail_idx, const int32_t* block_table,
                          const int32_t* seq_lens, int64_t bt_stride, int bt_cols, int hkv, int group, float p2, float rs,
                          int n_splits, float* part_ml, float* part_o, int32_t* sync, const int32_t* seq_order,
-                         const void* app_k, const void* app_v, int64_t app_ks, int64_t app_vs);
+                         const void* app_k, const void* app_v, int64_t app_ks, int64_t app_vs, int ws);
 
 #ifdef KUSH_DECODE_INSTANTIATE
 template <int D, int BITS, typename IN, int NW, bool ROT>
@@ -1412,9 +1459,13 @@ int launch_decode(dim3 grid, hipStream_t stream, const void* q, void* out, const
                          int64_t hs, const void* tail_k, const int32_t* tail_idx, const int32_t* block_table,
                          const int32_t* seq_lens, int64_t bt_stride, int bt_cols, int hkv, int group, float p2, float rs,
                          int n_splits, float* part_ml, float* part_o, int32_t* sync, const int32_t* seq_order,
-                         const void* app_k, const void* app_v, int64_t app_ks, int64_t app_vs) {
-    // two page streams whenever the heads of a kv head fit in half the MFMA columns
-    auto kern = group <= 8 ? decode_kernel<D, BITS, IN, NW, 2, ROT> : decode_kernel<D, BITS, IN, NW, 1, ROT>;
+                         const void* app_k, const void* app_v, int64_t app_ks, int64_t app_vs, int ws) {
+    // two page streams whenever the heads of a kv head fit in half the MFMA columns; wave splits are
+    // built for 4 waves only (the policy's choice for the split counts that take them)
+    auto kern = group <= 8 ? decode_kernel<D, BITS, IN, NW, 2, ROT, false> : decode_kernel<D, BITS, IN, NW, 1, ROT, false>;
+    if constexpr (NW == 4) {
+        if (ws) kern = group <= 8 ? decode_kernel<D, BITS, IN, NW, 2, ROT, true> : decode_kernel<D, BITS, IN, NW, 1, ROT, true>;
+    }
     kern<<<grid, dim3(NW * WAVE), 0, stream>>>(
         (const IN*)q, (IN*)out, (uint8_t*)cache, bs, hs, (IN*)tail_k, tail_idx, block_table, seq_lens, bt_stride,
         bt_cols, hkv, group, p2, rs, n_splits, part_ml, part_o, sync, seq_order, (const IN*)app_k, (const IN*)app_v,

@@ -1,6 +1,7 @@
 // C entry points of the fused dequant decode attention (kush_decode), the same launch with the
 // step's token appended first (kush_append_decode) and the split-K combine (kush_combine); the
 // kernels and their launch are in kush_decode.h (contract and design notes there).
+#include <cstdlib>
 #include <mutex>
 
 #include "kush_decode.h"
@@ -15,6 +16,19 @@ struct Append {
     const void* v = nullptr;
     int64_t k_stride = 0, v_stride = 0;
 };
+
+// Wave splits (decode_kernel WS: every wave a whole split of its own, no merge between the waves, the
+// workgroup's q and launch cost shared by its 4 splits): at 4 waves, whenever 4 divides NS, NS >= 8
+// and the workgroups still fill MI355X's 256 CUs. C4 (8 x 131,072 tokens) at 4 waves: NS 32 / 64 /
+// 128 / 256 232 / 243 / 280 / 373 us -> 232 / 240 / 257 / 292 us. KUSHKASH_AMD_WAVE_SPLITS=0 / 1
+// turns it off / on wherever NS allows it.
+int wave_splits(int ns, int nw, int64_t chunks) {
+    if (nw != 4 || ns % nw != 0 || ns < 2 * nw) return 0;             // built for 4 waves
+    const char* env = std::getenv("KUSHKASH_AMD_WAVE_SPLITS");
+    if (env != nullptr && env[0] == '0') return 0;
+    if (env != nullptr && env[0] == '1') return 1;
+    return chunks * (ns / nw) >= 256 ? 1 : 0;
+}
 
 int decode_impl(const char* what, int head_dim, int bits, int group, int dtype, const void* q, void* out,
                 const void* cache, int64_t block_stride, int64_t head_stride, const void* tail_k, const int32_t* tail_idx,
@@ -46,20 +60,21 @@ int decode_impl(const char* what, int head_dim, int bits, int group, int dtype, 
         p2 = std::copysign(std::ldexp(1.0f, e2), sm_log2);
         rs = sm_log2 / p2;
     }
-    const dim3 grid(n_seqs, hkv, n_splits * n_gc);
     hipStream_t st = (hipStream_t)stream;
     return dispatch_shape(head_dim, bits, dtype, what, [&](auto dd, auto bb, auto in) -> int {
         constexpr int D = decltype(dd)::value, BITS = decltype(bb)::value;
         using IN = decltype(in);
         if (n_seqs == 0) return 0;
-#define KUSH_DECODE_ARGS grid, st, q, out, cache, block_stride, head_stride, tail_k, tail_idx, block_table, seq_lens, \
+#define KUSH_DECODE_ARGS st, q, out, cache, block_stride, head_stride, tail_k, tail_idx, block_table, seq_lens, \
                          bt_stride, bt_cols, hkv, group, p2, rs, n_splits, part_ml, part_o, split_sync, seq_order, app.k, \
                          app.v, app.k_stride, app.v_stride
         // the largest of the requested, 4 and 2 waves whose rings fit in LDS
         const auto launch = [&](auto nw) -> int {
             constexpr int NW = decltype(nw)::value;
-            return rot ? launch_decode<D, BITS, IN, NW, true>(KUSH_DECODE_ARGS)
-                       : launch_decode<D, BITS, IN, NW, false>(KUSH_DECODE_ARGS);
+            const int ws = wave_splits(n_splits, NW, (int64_t)n_seqs * hkv * n_gc);
+            const dim3 g(n_seqs, hkv, (ws ? n_splits / NW : n_splits) * n_gc);
+            return rot ? launch_decode<D, BITS, IN, NW, true>(g, KUSH_DECODE_ARGS, ws)
+                       : launch_decode<D, BITS, IN, NW, false>(g, KUSH_DECODE_ARGS, ws);
         };
         if (waves >= 8) {
             if constexpr (decode_fits<D, BITS, 8>()) return launch(std::integral_constant<int, 8>{});
