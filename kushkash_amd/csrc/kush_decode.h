@@ -51,7 +51,7 @@ namespace kush {
 // register XCC_ID) in slot 7; every wave w records the wall clock at which it consumed its last page
 // pair (before the workgroup's barrier; the last window's, with several) in slot 8 + w. Rows
 // beyond TIMELINE_ROWS are not recorded. The stores are ordinary vector stores (every lane of the
-// wave the same value).
+// wave the same value), made once the output is stored.
 #ifdef KUSH_TIMELINE
 constexpr int TIMELINE_ROWS = 1 << 16, TIMELINE_COLS = 16;
 static __device__ long long g_timeline[TIMELINE_ROWS * TIMELINE_COLS];
@@ -59,24 +59,36 @@ __device__ __forceinline__ long long* timeline_row() {
     const long long row = ((long long)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
     return row < TIMELINE_ROWS ? g_timeline + row * TIMELINE_COLS : nullptr;
 }
-__device__ __forceinline__ void timeline_mark(int k) {
-    long long* const r = timeline_row();
-    if (__builtin_amdgcn_readfirstlane(threadIdx.x) < WAVE && r != nullptr) {   // wave 0: wave-uniform
-        r[k] = wall_clock64();
-        if (k == 0) r[7] = __builtin_amdgcn_s_getreg((3 << 11) | 20);         // XCC_ID bits [3:0]
-        if (k == 2) r[5] = clock64();
-        if (k == 3) r[6] = clock64();
+// The marks are held in registers and stored once, after the output (KUSH_MARK_FLUSH): a store
+// inside the page loop would count in the vmcnt the loop waits on and hold the marking wave back.
+struct TimelineMarks {
+    long long v[8] = {};
+    long long wave_done = 0;
+    __device__ __forceinline__ void mark(int k) {
+        v[k] = wall_clock64();
+        if (k == 0) v[7] = __builtin_amdgcn_s_getreg((3 << 11) | 20);         // XCC_ID bits [3:0]
+        if (k == 2) v[5] = clock64();
+        if (k == 3) v[6] = clock64();
     }
-}
-__device__ __forceinline__ void timeline_wave_done() {
-    long long* const r = timeline_row();
-    if (r != nullptr) r[8 + __builtin_amdgcn_readfirstlane(threadIdx.x) / WAVE] = wall_clock64();
-}
-#define KUSH_MARK(k) timeline_mark(k)
-#define KUSH_MARK_WAVE() timeline_wave_done()
+    __device__ __forceinline__ void flush(int w) {
+        long long* const r = timeline_row();
+        if (r == nullptr) return;
+        if (w == 0) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) r[k] = v[k];
+        }
+        r[8 + w] = wave_done;
+    }
+};
+#define KUSH_TIMELINE_DECL TimelineMarks tl_marks
+#define KUSH_MARK(k) tl_marks.mark(k)
+#define KUSH_MARK_WAVE() (tl_marks.wave_done = wall_clock64())
+#define KUSH_MARK_FLUSH() tl_marks.flush(w)
 #else
+#define KUSH_TIMELINE_DECL
 #define KUSH_MARK(k) ((void)0)
 #define KUSH_MARK_WAVE() ((void)0)
+#define KUSH_MARK_FLUSH() ((void)0)
 #endif
 
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
@@ -853,6 +865,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     float* const l_l = m_l + NW * 16;
     int* const last_flag = reinterpret_cast<int*>(l_l + NW * 16);
 
+    KUSH_TIMELINE_DECL;
     KUSH_MARK(0);
     const int lane = threadIdx.x & (WAVE - 1);
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);   // wave-uniform: scalar page loop
@@ -1314,6 +1327,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         store_rotated<D, IN, NW * WAVE>(out + qbase, ostage, Gc, out_vec);
     }
     KUSH_MARK(4);
+    KUSH_MARK_FLUSH();
     if (NS > 1 && (ws || w == 0) && q == 0 && r16 < Gc) {
         publish(part_ml + 2 * pb, M);
         publish(part_ml + 2 * pb + 1, L);
