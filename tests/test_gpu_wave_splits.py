@@ -10,6 +10,7 @@ import kushkash_amd as kk
 from _harness import assert_out_close
 from kushkash_amd._ops import PAGE
 from oracle.cpu_ops import OracleOps
+from test_gpu_append_decode import test_fused_equals_append_then_decode as fused_append_case
 from test_gpu_parity import oracle_decode
 
 pytestmark = pytest.mark.gpu
@@ -87,6 +88,18 @@ def test_two_windows_per_wave_then_partial_page(bits, monkeypatch):
     q = torch.randn(B, H * G, D, device=DEV, dtype=torch.bfloat16)
     out = _decode(c, q, ns, work, "1", monkeypatch)
     assert_out_close(out, oracle_decode(c, 0, q), torch.bfloat16, what=f"{N} tokens")
+
+
+@pytest.mark.parametrize("rot", [False, True])
+@pytest.mark.parametrize("ns", [8, 16])
+@pytest.mark.parametrize("D,bits,G,dtype", [(128, 4, 7, torch.bfloat16), (128, 8, 4, torch.float16),
+                                            (256, 4, 2, torch.float32)])
+def test_fused_append_then_decode(D, bits, G, dtype, ns, rot, monkeypatch):
+    """The fused append + decode with wave splits (the workgroup holding the split of the page a
+    token completes writes it), rotation folded in or not: the same records, K tails and outputs as
+    the append followed by the decode."""
+    monkeypatch.setenv("KUSHKASH_AMD_WAVE_SPLITS", "1")
+    fused_append_case(D, bits, G, dtype, ns, 4, True, rot, monkeypatch)
 
 
 def test_policy_takes_wave_splits_where_the_library_does():
