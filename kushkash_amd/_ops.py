@@ -325,20 +325,19 @@ class Ops:
         return ns
 
     def waves(self, num_seqs: int, num_kv_heads: int, n_splits: int, max_pages: int | None = None) -> int:
-        """Waves per decode workgroup (measured on MI355X): 4 where the library gives every wave a
-        split of its own -- split counts of 8 and more that 4 divides, with the workgroups (a quarter
-        of the splits per sequence, kv head and 16-head chunk) still filling the CUs (C4 at NS 8: 223
-        us against 255 at 2 waves; NS 64 / 128 / 256: 240 / 258 / 289 us against 252 / 271 / 332 at
-        the best of 2 and 4 waves without); else 2 when the grid holds at least two workgroups per CU
-        (smaller workgroups overlap one's start and merge with another's page loop; C3 213.7 against
-        220.1 at 4); else 4, one wave per SIMD (C2 33.0 us against 33.5 with 8 waves, C4 217.8 against
-        221.0: the second wave of a SIMD adds issue slots but no bandwidth, and with a static page
-        assignment it finishes ~6 us after the first). max_pages is accepted for callers that pass
-        it. A configuration whose ring does not fit in LDS runs fewer (the library picks)."""
-        chunks = num_seqs * num_kv_heads * -(-self.cfg.group // 16)
-        if n_splits >= 2 * DECODE_WAVES and n_splits % DECODE_WAVES == 0 and \
-                chunks * (n_splits // DECODE_WAVES) >= self.sms:
-            return DECODE_WAVES                # wave splits (the library's own test, kush_decode.hip)
+        """Waves per decode workgroup (measured on MI355X): 4 for split counts of 8 and more that 4
+        divides -- where the workgroups (a quarter of the splits per sequence, kv head and 16-head
+        chunk) still fill the CUs the library then gives every wave a split of its own (C4 at NS 64 /
+        128 / 256: 226 / 234 / 242 us against 243 / 271 / 332 at the best of 2 and 4 waves without),
+        and below that the waves share each split (C4 at NS 8: 224.6 us against 254.8 at 2 waves);
+        else 2 when the grid holds at least two workgroups per CU (smaller workgroups overlap one's
+        start and merge with another's page loop; C3 213.7 against 220.1 at 4); else 4, one wave per
+        SIMD (C2 33.0 us against 33.5 with 8 waves, C4 217.8 against 221.0: the second wave of a SIMD
+        adds issue slots but no bandwidth, and with a static page assignment it finishes ~6 us after
+        the first). max_pages is accepted for callers that pass it. A configuration whose ring does
+        not fit in LDS runs fewer (the library picks)."""
+        if n_splits >= 2 * DECODE_WAVES and n_splits % DECODE_WAVES == 0:
+            return DECODE_WAVES                # wave splits where the grid allows (kush_decode.hip)
         if num_seqs * num_kv_heads * n_splits >= 2 * self.sms:
             return 2
         return DECODE_WAVES

@@ -885,6 +885,11 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     const int zg = blockIdx.z % NSG, gc = blockIdx.z / NSG, g0 = gc * 16;
     const int z = ws ? zg * NW + w : zg;                                  // this wave's split
     const int tw = ws ? NW - 1 : 0;                                       // the wave taking the partial page
+    // ws with the in-launch merge (sync): the workgroup first merges its NW splits in LDS and writes one
+    // partial (index zg of NSG), so the last workgroup merges NSG partials; without sync every wave
+    // writes its own (index z of NS) for the caller's combine over NS
+    const bool wmerge = ws && sync != nullptr, own = ws && !wmerge;
+    const int NSP = wmerge ? NSG : NS, zp = wmerge ? zg : z;                   // partials per head chunk, this one's
     const int Gc = min(16, G - g0);
 
     const int32_t* bt = block_table + (int64_t)s * bt_stride;
@@ -1248,14 +1253,14 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     for (int ww = 0; ww < NW; ++ww)
 #pragma unroll
         for (int c2 = 0; c2 < ST; ++c2)
-            if (!ws || ww == w) M = __builtin_fmaxf(M, mv[ww][c2]);
+            if (!ws || wmerge || ww == w) M = __builtin_fmaxf(M, mv[ww][c2]);
     float L = 0.0f;
     if (M > -__builtin_inff()) {
 #pragma unroll
         for (int ww = 0; ww < NW; ++ww)
 #pragma unroll
             for (int c2 = 0; c2 < ST; ++c2)
-                if (!ws || ww == w) L += lv[ww][c2] * __builtin_amdgcn_exp2f(mv[ww][c2] - M);
+                if (!ws || wmerge || ww == w) L += lv[ww][c2] * __builtin_amdgcn_exp2f(mv[ww][c2] - M);
     }
     const float inv_l = L > 0.0f ? 1.0f / L : 0.0f;
     {
@@ -1271,19 +1276,33 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         }
     }
     __syncthreads();
-    const int64_t pb = (((int64_t)s * H + h) * NS + z) * G + g0 + r16;   // partials row of head r16
+    const int64_t pb = (((int64_t)s * H + h) * NSP + zp) * G + g0 + r16; // partials row of head r16
     const bool out_vec = (((uintptr_t)out) & 15) == 0;
     const int hcol = ST == 2 ? (r16 & 7) : r16;                  // the (first) column of head r16
     float* const ostage = reinterpret_cast<float*>(ringB + AL::Q_OFF);   // ROT: [16][D] output rows
-    for (int dt = ws ? 0 : w; dt < DT; dt += ws ? 1 : NW) {
+    for (int dt = own ? 0 : w; dt < DT; dt += own ? 1 : NW) {
         f4 acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
-        if constexpr (WS) {                                      // this wave's own pieces
-            f4 part[ST];
+        if constexpr (WS) {
+            if (own) {                                           // this wave's own pieces
+                f4 part[ST];
 #pragma unroll
-            for (int c2 = 0; c2 < ST; ++c2)
-                part[c2] = *reinterpret_cast<const f4*>(ringA + w * OBYTES + (((4 * dt + q) * 16 + hcol + 8 * c2) * 4) * 4);
+                for (int c2 = 0; c2 < ST; ++c2)
+                    part[c2] = *reinterpret_cast<const f4*>(ringA + w * OBYTES + (((4 * dt + q) * 16 + hcol + 8 * c2) * 4) * 4);
 #pragma unroll
-            for (int c2 = 0; c2 < ST; ++c2) acc += part[c2];
+                for (int c2 = 0; c2 < ST; ++c2) acc += part[c2];
+            } else {                                             // the workgroup's NW splits, merged here
+                f4 part[NW][ST];
+#pragma unroll
+                for (int ww = 0; ww < NW; ++ww)
+#pragma unroll
+                    for (int c2 = 0; c2 < ST; ++c2)
+                        part[ww][c2] = *reinterpret_cast<const f4*>(ringA + ww * OBYTES +
+                                                                    (((4 * dt + q) * 16 + hcol + 8 * c2) * 4) * 4);
+#pragma unroll
+                for (int ww = 0; ww < NW; ++ww)
+#pragma unroll
+                    for (int c2 = 0; c2 < ST; ++c2) acc += part[ww][c2];
+            }
         } else {
             f4 part[NW][ST];                                     // every wave's pieces, read together
 #pragma unroll
@@ -1328,7 +1347,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     }
     KUSH_MARK(4);
     KUSH_MARK_FLUSH();
-    if (NS > 1 && (ws || w == 0) && q == 0 && r16 < Gc) {
+    if (NS > 1 && (own || w == 0) && q == 0 && r16 < Gc) {
         publish(part_ml + 2 * pb, M);
         publish(part_ml + 2 * pb + 1, L);
     }
@@ -1350,9 +1369,9 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     }
     __syncthreads();
     if (!*last_flag) return;
-    const int64_t base = ((int64_t)s * H + h) * NS;
-    if (merge_smem_floats(NS, Gc, NW) * 4 <= 2 * NW * R::SLOT) {      // the idle first ring holds the scratch
-        merge_splits<D, NW>(part_ml, part_o, base, NS, G, g0, Gc, reinterpret_cast<float*>(ringA),
+    const int64_t base = ((int64_t)s * H + h) * NSP;
+    if (merge_smem_floats(NSP, Gc, NW) * 4 <= 2 * NW * R::SLOT) {      // the idle first ring holds the scratch
+        merge_splits<D, NW>(part_ml, part_o, base, NSP, G, g0, Gc, reinterpret_cast<float*>(ringA),
                             [&](int g, int d, f4 v) {
                                 if constexpr (ROT) {
                                     *reinterpret_cast<f4*>(ostage + g * D + d) = v;
@@ -1367,10 +1386,10 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     for (int i = threadIdx.x; i < Gc * D; i += NW * WAVE) {      // one dependent chain per split (large NS)
         const int g = g0 + i / D, d = i % D;
         float Mg = -__builtin_inff();
-        for (int zz = 0; zz < NS; ++zz) Mg = __builtin_fmaxf(Mg, fetch(part_ml + 2 * ((base + zz) * G + g)));
+        for (int zz = 0; zz < NSP; ++zz) Mg = __builtin_fmaxf(Mg, fetch(part_ml + 2 * ((base + zz) * G + g)));
         float L = 0.0f, acc = 0.0f;
         if (Mg > -__builtin_inff()) {
-            for (int zz = 0; zz < NS; ++zz) {
+            for (int zz = 0; zz < NSP; ++zz) {
                 const int64_t pb = (base + zz) * G + g;
                 const float mz = fetch(part_ml + 2 * pb);
                 if (mz > -__builtin_inff()) {

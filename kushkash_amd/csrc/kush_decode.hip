@@ -17,11 +17,12 @@ struct Append {
     int64_t k_stride = 0, v_stride = 0;
 };
 
-// Wave splits (decode_kernel WS: every wave a whole split of its own, no merge between the waves, the
-// workgroup's q and launch cost shared by its 4 splits): at 4 waves, whenever 4 divides NS, NS >= 8
-// and the workgroups still fill MI355X's 256 CUs. C4 (8 x 131,072 tokens) at 4 waves: NS 32 / 64 /
-// 128 / 256 232 / 243 / 280 / 373 us -> 232 / 240 / 257 / 292 us. KUSHKASH_AMD_WAVE_SPLITS=0 / 1
-// turns it off / on wherever NS allows it.
+// Wave splits (decode_kernel WS: every wave a whole split of its own, the workgroup's q and launch
+// cost shared by its 4 splits; with the in-launch merge the workgroup merges its 4 splits in LDS and
+// writes one partial, so the last workgroup merges NS / 4): at 4 waves, whenever 4 divides NS,
+// NS >= 8 and the workgroups still fill MI355X's 256 CUs. C4 (8 x 131,072 tokens) at 4 waves:
+// NS 32 / 64 / 128 / 256 232 / 243 / 280 / 373 us -> 222 / 226 / 234 / 242 us.
+// KUSHKASH_AMD_WAVE_SPLITS=0 / 1 turns it off / on wherever NS allows it.
 int wave_splits(int ns, int nw, int64_t chunks) {
     if (nw != 4 || ns % nw != 0 || ns < 2 * nw) return 0;             // built for 4 waves
     const char* env = std::getenv("KUSHKASH_AMD_WAVE_SPLITS");

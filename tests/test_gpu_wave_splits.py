@@ -102,12 +102,13 @@ def test_fused_append_then_decode(D, bits, G, dtype, ns, rot, monkeypatch):
     fused_append_case(D, bits, G, dtype, ns, 4, True, rot, monkeypatch)
 
 
-def test_policy_takes_wave_splits_where_the_library_does():
-    """Ops.waves picks 4 waves exactly where the library's own test (kush_decode.hip wave_splits)
-    gives every wave a split: NS >= 8, 4 | NS and S * Hkv * ceil(G / 16) * NS / 4 >= 256."""
+def test_policy_takes_four_waves_for_split_counts_that_four_divides():
+    """Ops.waves picks 4 waves for NS >= 8 that 4 divides (the library gives every wave a split of its
+    own where S * Hkv * ceil(G / 16) * NS / 4 >= 256, kush_decode.hip wave_splits, else the waves
+    share each split), and its other rules below that."""
     ops = kk.Ops(torch.device(DEV), 128, 4, 7, torch.bfloat16)
     assert ops.sms == 256
-    assert ops.waves(64, 4, 8) == 4 and ops.waves(16, 8, 8) == 4       # 128 / 64 workgroups: 2 waves else
-    assert ops.waves(8, 8, 16) == 4                                      # 256 workgroups
-    assert ops.waves(8, 8, 8) == 2                                       # 128 workgroups: no wave splits
+    assert ops.waves(64, 4, 8) == 4 and ops.waves(8, 8, 16) == 4         # wave splits
+    assert ops.waves(8, 8, 8) == 4                                       # 128 workgroups: shared splits
     assert ops.waves(64, 8, 10) == 2                                     # 4 does not divide 10
+    assert ops.waves(64, 4, 1) == 4 and ops.waves(128, 8, 1) == 2        # C2, C3
