@@ -106,6 +106,13 @@ def parse_args(argv=None):
     ap.add_argument("--graph-replay", action="store_true",
                     help="time the steps as replays of one-step HIP graphs (the reference's method) instead of "
                          "recorded launches")
+    ap.add_argument("--floor", default="", metavar="MODE:WAVES:DEPTH[:Z],...",
+                    help="c2: after the decode line, time the decode's streaming floor (libkushfloor.so: the same "
+                         "records and block tables, no attention math) in each listed launch shape -- mode 0 the "
+                         "decode's grid (sequence, kv head), mode 1 a grid (sequence, Z) over every kv head of a "
+                         "page range; WAVES per workgroup; DEPTH page pairs in flight per wave (2: the decode's ring)")
+    ap.add_argument("--floor-timeline", type=int, default=0, metavar="N",
+                    help="with --floor: also print N launches of each floor shape by XCD (per-workgroup wall clocks)")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "decode_c2_traffic.md"),
                     help="rocprofv3 counter summary whose 'traffic_bytes_per_launch' fills roofline.traffic")
     return ap.parse_args(argv)
@@ -349,15 +356,20 @@ def _b(x) -> str:
 def decode_kernel_name(D: int, bits: int, dtype, waves: int, G: int, rot: bool, ns: int = 1, chunks: int = 0) -> str:
     """The instantiation kush_decode launches, as rocprofv3 names it: the requested waves unless the
     configuration's page ring does not fit in LDS (4 KB of block ids + 4 slots per wave of one record
-    each, within 160 KiB), two page streams when G <= 8, and wave splits as kush_decode.hip's
-    wave_splits picks them for ns splits over `chunks` (sequences x kv heads x head chunks)."""
+    each, within 160 KiB), two page streams when G <= 8, wave splits as kush_decode.hip's
+    wave_splits picks them for ns splits over `chunks` (sequences x kv heads x head chunks), and the
+    ring depth launch_decode picks (three page pairs per wave with KUSHKASH_AMD_RING=3 where a third
+    ring array fits, else two)."""
     from kushkash_amd._ops import record_bytes
     nw = waves or 8
     while nw > 2 and 4 * nw * record_bytes(D, bits) + 4 * 1024 + 16 > 160 * 1024:
         nw //= 2
     env = os.environ.get("KUSHKASH_AMD_WAVE_SPLITS", "")
     ws = nw == 4 and ns % nw == 0 and ns >= 2 * nw and (env[:1] == "1" or (env[:1] != "0" and chunks * (ns // nw) >= 256))
-    return f"kush::decode_kernel<{D}, {bits}, {_IN[dtype]}, {nw}, {2 if G <= 8 else 1}, {_b(rot)}, {_b(ws)}>"
+    rec = record_bytes(D, bits)
+    fits3 = 6 * nw * rec + 4 * 1024 + 16 <= 160 * 1024 and 4 * -(-rec // 1024) <= 63
+    dep = 3 if nw == 4 and not rot and not ws and fits3 and os.environ.get("KUSHKASH_AMD_RING", "")[:1] == "3" else 2
+    return f"kush::decode_kernel<{D}, {bits}, {_IN[dtype]}, {nw}, {2 if G <= 8 else 1}, {_b(rot)}, {_b(ws)}, {dep}>"
 
 
 # the translation unit of each kernel family (its digest covers the unit and its headers)
@@ -842,6 +854,83 @@ def bench_timeline(a) -> None:
                       f"{pct(us[m, 3], 50):.2f} / {us[m, 3].max():.2f} | {pct(mhz[m], 50):.0f} |", flush=True)
 
 
+def _floor_fn():
+    """kush_floor_stream of the measurement library (kushkash_amd/csrc/kush_floor.hip)."""
+    import ctypes
+    import importlib
+    kbuild = importlib.import_module("kushkash_amd.build")
+    if not kbuild.FLOOR_LIB.exists():
+        raise SystemExit(f"--floor: {kbuild.FLOOR_LIB.name} is not built; run `python -m kushkash_amd.build`")
+    fn = ctypes.CDLL(str(kbuild.FLOOR_LIB)).kush_floor_stream
+    P, I32, I64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    fn.argtypes = [I32, I32, P, I64, I64, P, P, I64, I32, I32, I32, I32, I32, I32, I32, P, P, P]
+    fn.restype = I32
+    return fn
+
+
+class FloorLaunches:
+    """The decode's streaming floor over the workload's pools, step i on pool i % pools, in one launch
+    shape (mode, waves, depth, z); run() has the interface of Launches.run, so time_launches times it
+    the way it times the decode."""
+
+    def __init__(self, w, mode: int, waves: int, depth: int, z: int, marks: bool = False):
+        self.fn = _floor_fn()
+        cache, B, Hkv, pages = w["cache"], w["B"], w["Hkv"], w["pages"]
+        self.wgs = B * (z if mode == 1 else Hkv)
+        self.sums = torch.empty(self.wgs * waves * 64, dtype=torch.int32, device=cache.device)
+        self.marks = torch.zeros(self.wgs, 8, dtype=torch.int64, device=cache.device) if marks else None
+        stream = torch.cuda.current_stream().cuda_stream
+        self.args = [(w["D"], w["bits"], cache.data_ptr(), cache.stride(0), cache.stride(1), t.data_ptr(),
+                      w["seq_lens"].data_ptr(), t.stride(0), Hkv, B, pages, mode, z, waves, depth,
+                      self.sums.data_ptr(), None if self.marks is None else self.marks.data_ptr(), stream)
+                     for t in w["tables"]]
+        if self.fn(*self.args[0]) != 0:
+            raise SystemExit(f"--floor: no floor kernel for mode {mode}, {waves} waves, depth {depth}, z {z}")
+
+    def run(self, first: int, n: int) -> None:
+        for i in range(first, first + n):
+            if self.fn(*self.args[i % len(self.args)]) != 0:
+                raise RuntimeError("bench: kush_floor_stream failed")
+
+
+def floor_shapes(spec: str):
+    for item in [x for x in spec.split(",") if x.strip()]:
+        v = [int(x) for x in item.split(":")]
+        if len(v) not in (3, 4):
+            raise SystemExit(f"--floor: '{item}' is not MODE:WAVES:DEPTH[:Z]")
+        yield v[0], v[1], v[2], (v[3] if len(v) == 4 else 1)
+
+
+def floor_timeline(w, shape, reps: int, warmup: int) -> None:
+    """Per-workgroup wall clocks of one floor launch (after `warmup` untimed ones), by XCD, as markdown."""
+    import numpy as np
+    mode, wv, depth, z = shape
+    fl = FloorLaunches(w, mode, wv, depth, z, marks=True)
+    for rep in range(reps):
+        fl.run(0, warmup)
+        torch.cuda.synchronize()
+        fl.run(1, 1)
+        torch.cuda.synchronize()
+        t = fl.marks.cpu().numpy().astype(np.float64)
+        t0 = t[:, 0].min()
+        us = (t[:, [0, 1, 2]] - t0) / 100.0
+        xcd = t[:, 3].astype(int)
+        loop = us[:, 2] - us[:, 1]
+        pct = lambda x, p: float(np.percentile(x, p))
+        print(f"\nfloor mode {mode}, {wv} waves, depth {depth}" + (f", z {z}" if mode == 1 else "")
+              + f": launch {rep + 1} of {reps}, first workgroup start -> last pages done {us[:, 2].max():.2f} us\n\n"
+              "| phase (us from the first start) | min | p10 | p50 | p90 | max |\n|---|---|---|---|---|---|")
+        for name, k in (("start", 0), ("first page pair landed", 1), ("pages done", 2)):
+            x = us[:, k]
+            print(f"| {name} | {x.min():.2f} | {pct(x, 10):.2f} | {pct(x, 50):.2f} | {pct(x, 90):.2f} | {x.max():.2f} |")
+        print("\n| XCD | workgroups | page loop p10 / p50 / max (us) | pages done p50 / max (us) |\n|---|---|---|---|")
+        for x in range(8):
+            m = xcd == x
+            if m.any():
+                print(f"| {x} | {int(m.sum())} | {pct(loop[m], 10):.2f} / {pct(loop[m], 50):.2f} / {loop[m].max():.2f} | "
+                      f"{pct(us[m, 2], 50):.2f} / {us[m, 2].max():.2f} |", flush=True)
+
+
 def main(argv=None):
     a = parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -916,6 +1005,17 @@ def main(argv=None):
     if not a.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(w, a.cpu_seconds)
     print(json.dumps(res), flush=True)
+
+    for mode, fwv, depth, z in floor_shapes(a.floor):              # the streaming floor, a line each
+        fms = time_launches(FloorLaunches(w, mode, fwv, depth, z), a.steps, a.warmup)
+        rec = w["B"] * w["Hkv"] * (w["N"] // PAGE) * w["RB"]
+        print(json.dumps({"floor": {"mode": mode, "waves": fwv, "depth": depth, "z": z if mode == 1 else None},
+                          "kernel": f"kush_floor_stream (floor_kernel<{a.dim}, {a.bits}, {fwv}, {depth}>)",
+                          "us_per_step": round(fms * 1e3, 2), "records_GBps": round(rec / fms / 1e6, 1),
+                          "pct_peak_hbm": round(100 * alg / fms / 1e6 / PEAK_HBM_GBS, 1),
+                          "decode_us_per_step": round(ms * 1e3, 2)}), flush=True)
+        if a.floor_timeline:
+            floor_timeline(w, (mode, fwv, depth, z), a.floor_timeline, min(a.warmup, 200))
 
     for item in [x for x in a.sweep.split(",") if x.strip()]:     # other launch shapes, a line each
         sns, swv = (int(v) for v in item.split(":"))

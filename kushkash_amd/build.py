@@ -23,6 +23,10 @@ DIGEST = PKG / "libkushhip.so.digest"          # source digest of the library la
 # recompiled with -DKUSH_TIMELINE (per-workgroup phase timestamps and XCD ids, kush_decode.h), read by
 # `python bench.py --timeline`. The product never loads it.
 TIMELINE_LIB = PKG / "libkushhip_timeline.so"
+# A measurement instrument beside the product: the decode's streaming floor (csrc/kush_floor.hip, the
+# same records, launch shape and DMA ring as the decode without its math), loaded only by bench.py.
+FLOOR_LIB = PKG / "libkushfloor.so"
+FLOOR_SOURCE = "kush_floor.hip"
 SOURCES = ("kush_capi.hip", "kush_write.hip", "kush_decode.hip", "kush_rotate.hip",
            "kush_unpack.hip", "kush_decode_inst.hip")
 # the decode kernel instantiations: one object per (input dtype, rot)
@@ -148,9 +152,10 @@ def _run(cmd: list[str], verbose: bool) -> None:
 
 
 def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compile every HIP source for gfx950 into LIB, and TIMELINE_LIB from the same objects with the
-    timeline unit instrumented (always recompiles; objects in parallel, then the links); returns LIB."""
-    todo = units() + [(TIMELINE_UNIT[0], dict(TIMELINE_UNIT[1], KUSH_TIMELINE=1))]
+    """Compile every HIP source for gfx950 into LIB, TIMELINE_LIB from the same objects with the
+    timeline unit instrumented, and the measurement library FLOOR_LIB (always recompiles; objects in
+    parallel, then the links); returns LIB."""
+    todo = units() + [(FLOOR_SOURCE, {}), (TIMELINE_UNIT[0], dict(TIMELINE_UNIT[1], KUSH_TIMELINE=1))]
     jobs = jobs or max(1, min(len(todo), int(os.environ.get("MAX_JOBS", 0)) or os.cpu_count() or 1))
     compile_flags = [f for f in FLAGS if f != "-shared"]
     with tempfile.TemporaryDirectory(prefix="kushkash_amd_build_") as tmpdir:
@@ -162,15 +167,16 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
                          "-c", str(PKG / "csrc" / src), "-o", obj])
         with ThreadPoolExecutor(jobs) as ex:
             list(ex.map(lambda c: _run(c, verbose), cmds))
-        product = objs[:-1]
+        product = objs[:len(units())]
         swap = units().index(TIMELINE_UNIT)
         timeline = product[:swap] + objs[-1:] + product[swap + 1:]
-        for dst, parts in ((LIB, product), (TIMELINE_LIB, timeline)):
+        for dst, parts in ((LIB, product), (TIMELINE_LIB, timeline), (FLOOR_LIB, objs[-2:-1])):
             tmp = dst.with_suffix(".so.tmp")
             _run([hipcc(), *FLAGS, "-o", str(tmp), *parts], verbose)
             os.replace(tmp, dst)
     import json
-    DIGEST.write_text(json.dumps({"all": source_digest(), **{u: source_digest(u) for u in SOURCES}}, indent=1) + "\n")
+    DIGEST.write_text(json.dumps({"all": source_digest(), **{u: source_digest(u) for u in SOURCES + (FLOOR_SOURCE,)}},
+                                 indent=1) + "\n")
     return LIB
 
 

@@ -11,9 +11,9 @@
 //      per instruction, issued one pair ahead and waited on with explicit vmcnt counts);
 //   2. reads K code rows from the ring and turns them into exact subnormal fp16 operands (one
 //      v_perm and one v_bitop3 per pair of codes), and computes the scores S^T = K . Q'^T on MFMA
-//      16x16x32 f16 with Q' = q' * k_scale as an fp16 pair (q' = q times a power of two; the rest
-//      of scale * log2 e multiplies the fp32 scores); the K-bias and -HALF * k_scale terms come
-//      from two more MFMAs per K-step;
+//      16x16x32 f16 with Q' = fp16(q' * k_scale) (q' = q times a power of two; the rest of
+//      scale * log2 e multiplies the fp32 scores); the K-bias and -HALF * k_scale terms of both pages
+//      come from one more MFMA per K-step;
 //   3. runs a page-granular online softmax in base 2 per MFMA column (with G <= 8 two page
 //      streams share the 16 columns: page A in 0-7, page B in 8-15), moving the running max only
 //      when a page exceeds it by more than 2^3;
@@ -38,6 +38,7 @@
 #pragma once
 
 #include <cmath>
+#include <cstdlib>
 
 #include "kush_page.h"
 
@@ -383,10 +384,11 @@ __device__ __forceinline__ void issue_page(uint8_t* dst, bool valid, int blk, co
 // a = rs 2^24.
 // sacc = K . Q'^T on codes n = c + HALF as subnormal fp16 (units of 2^-24) and Q' = q' ks as an fp16
 // pair qp + qr, q' = q p2 (p2 a power of two: q' is exact in fp16 for bf16 / fp16 q; fp32 q adds
-// its low fp16 part ql). int4 high nibbles enter as 16 n against Q' / 16 (qa holds q' / 16 there).
-// kx = rs (sum_d kb[d] q'[d] - HALF sum_d ks[d] q'[d]): two MFMAs per K-step for both pages, their
-// A rows alternating between the pages' biases and scales (row r: page r % 2, so C register i holds
-// page i % 2).
+// its low fp16 part ql): fp32-grade scores for more than 8 q heads per kv head, the reference's
+// CUDA-core domain (its tensor-core path takes G <= 8, gpu.mojo:576). int4 high nibbles enter as
+// 16 n against Q' / 16 (qa holds q' / 16 there). kx = rs (sum_d kb[d] q'[d] - HALF sum_d ks[d] q'[d]): one
+// MFMA per K-step for both pages, A row r holding page r % 2's biases (r % 4 < 2) or scales, so C
+// register i holds page i % 2's bias dot (i < 2) or scale dot (i >= 2).
 template <int D, int BITS, bool QLO>
 __device__ __forceinline__ void pair_scores(const uint8_t* s0, const h8 (&qa)[D / 32],
                                             const h8 (&qla)[D / 32], const h8 (&qh)[D / 32], const h8 (&ql)[D / 32],
@@ -396,11 +398,12 @@ __device__ __forceinline__ void pair_scores(const uint8_t* s0, const h8 (&qa)[D 
     constexpr int KBYTES = F::DC / 4;                // K code bytes per lane per 16-token tile
     const int r16 = lane & 15, q = lane >> 4;
     const uint8_t* const sl[2] = {s0, s0 + Ring<D, BITS>::SLOT};
-    const uint8_t* const own = s0 + (r16 & 1) * Ring<D, BITS>::SLOT;
+    // A row r16 of the bias MFMA: page r16 & 1, k bias (r16 & 2 == 0) or k scale
+    const uint8_t* const brow = s0 + (r16 & 1) * Ring<D, BITS>::SLOT + ((r16 & 2) ? F::OFF_KS : F::OFF_KB);
     f4 sacc[2][2];
 #pragma unroll
     for (int p = 0; p < 2; ++p) sacc[p][0] = sacc[p][1] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    f4 kb_acc = f4{0.0f, 0.0f, 0.0f, 0.0f}, ks_acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    f4 bacc = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk) {
         const int d0 = kdim<D, BITS>(kk, q, 0);
@@ -432,20 +435,16 @@ __device__ __forceinline__ void pair_scores(const uint8_t* s0, const h8 (&qa)[D 
             sacc[p][0] = mfma16(a[0], qr, sacc[p][0]);
             sacc[p][1] = mfma16(a[1], qr, sacc[p][1]);
         }
-        const h8 kbo = *reinterpret_cast<const h8*>(own + F::OFF_KB + 2 * d0);
-        const h8 kso = *reinterpret_cast<const h8*>(own + F::OFF_KS + 2 * d0);
-        kb_acc = mfma16(kbo, qh[kk], kb_acc);
-        ks_acc = mfma16(kso, qh[kk], ks_acc);
-        if constexpr (QLO) {
-            kb_acc = mfma16(kbo, ql[kk], kb_acc);
-            ks_acc = mfma16(kso, ql[kk], ks_acc);
-        }
+        const h8 b8 = *reinterpret_cast<const h8*>(brow + 2 * d0);
+        bacc = mfma16(b8, qh[kk], bacc);
+        if constexpr (QLO) bacc = mfma16(b8, ql[kk], bacc);
     }
+    // C register i is row 4 q + i: page i & 1, the k bias dot (i < 2) or the k scale dot
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) sv[p][j] = sacc[p][j >> 2][j & 3];
-        kx[p] = rs * __builtin_fmaf(-(float)F::HALF, ks_acc[p], kb_acc[p]);
+        kx[p] = rs * __builtin_fmaf(-(float)F::HALF, bacc[2 + p], bacc[p]);
     }
 }
 
@@ -458,7 +457,9 @@ __device__ __forceinline__ void pair_scores(const uint8_t* s0, const h8 (&qa)[D 
 // Scores of a staged pair (page A at s0, page B in the next slot) for this lane's column: sv[j] for
 // token tok(q, j) of its page, x = a sv[j] + kx. The Q' operand is built once for both pages (each
 // column from its own page's scales); K of page A and of page B each meet it in their own MFMAs,
-// and a column keeps the product with its page.
+// and a column keeps the product with its page. Q' = fp16(q' ks), one rounding of the product, as
+// the reference's tensor-core path (G <= 8) forms its operand (gpu.mojo:660-675); fp32 q adds the
+// residual of that product (plus its low part ql times ks) as a second operand.
 template <int D, int BITS, bool QLO>
 __device__ __forceinline__ void pair_scores2(const uint8_t* s0, const h8 (&qa)[D / 32], const h8 (&qla)[D / 32],
                                              const h8 (&qh)[D / 32], const h8 (&ql)[D / 32], float (&sv)[8],
@@ -470,18 +471,20 @@ __device__ __forceinline__ void pair_scores2(const uint8_t* s0, const h8 (&qa)[D
     const int r16 = lane & 15, q = lane >> 4, st = r16 >> 3;
     const uint8_t* const sl[2] = {s0, s0 + SLOT};
     const uint8_t* const mine = s0 + st * SLOT;                 // the page of this lane's column
-    const uint8_t* const own = s0 + (r16 & 1) * SLOT;           // A row r16 of the bias MFMAs
+    // A row r16 of the bias MFMA: page r16 & 1, k bias (r16 & 2 == 0) or k scale
+    const uint8_t* const brow = s0 + (r16 & 1) * SLOT + ((r16 & 2) ? F::OFF_KS : F::OFF_KB);
     f4 sacc[2][2];
 #pragma unroll
     for (int p = 0; p < 2; ++p) sacc[p][0] = sacc[p][1] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    f4 kb_acc = f4{0.0f, 0.0f, 0.0f, 0.0f}, ks_acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    f4 bacc = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk) {
         const int d0 = kdim<D, BITS>(kk, q, 0);
         const h8 ks8 = *reinterpret_cast<const h8*>(mine + F::OFF_KS + 2 * d0);
+        // Q' = fp16(q' ks), rounded once (the reference's tensor-core form); fp32 q adds a residual operand
         const h8 qp = qa[kk] * ks8;
-        h8 qr = __builtin_elementwise_fma(qa[kk], ks8, -qp);
-        if constexpr (QLO) qr = __builtin_elementwise_fma(qla[kk], ks8, qr);
+        h8 qr{};
+        if constexpr (QLO) qr = __builtin_elementwise_fma(qla[kk], ks8, __builtin_elementwise_fma(qa[kk], ks8, -qp));
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
             h8 a[2];
@@ -500,21 +503,19 @@ __device__ __forceinline__ void pair_scores2(const uint8_t* s0, const h8 (&qa)[D
             }
             sacc[p][0] = mfma16(a[0], qp, sacc[p][0]);
             sacc[p][1] = mfma16(a[1], qp, sacc[p][1]);
-            sacc[p][0] = mfma16(a[0], qr, sacc[p][0]);
-            sacc[p][1] = mfma16(a[1], qr, sacc[p][1]);
+            if constexpr (QLO) {
+                sacc[p][0] = mfma16(a[0], qr, sacc[p][0]);
+                sacc[p][1] = mfma16(a[1], qr, sacc[p][1]);
+            }
         }
-        const h8 kbo = *reinterpret_cast<const h8*>(own + F::OFF_KB + 2 * d0);
-        const h8 kso = *reinterpret_cast<const h8*>(own + F::OFF_KS + 2 * d0);
-        kb_acc = mfma16(kbo, qh[kk], kb_acc);
-        ks_acc = mfma16(kso, qh[kk], ks_acc);
-        if constexpr (QLO) {
-            kb_acc = mfma16(kbo, ql[kk], kb_acc);
-            ks_acc = mfma16(kso, ql[kk], ks_acc);
-        }
+        const h8 b8 = *reinterpret_cast<const h8*>(brow + 2 * d0);
+        bacc = mfma16(b8, qh[kk], bacc);
+        if constexpr (QLO) bacc = mfma16(b8, ql[kk], bacc);
     }
+    // C register i is row 4 q + i: page i & 1, the k bias dot (i < 2) or the k scale dot
 #pragma unroll
     for (int j = 0; j < 8; ++j) sv[j] = st ? sacc[1][j >> 2][j & 3] : sacc[0][j >> 2][j & 3];
-    kx = rs * __builtin_fmaf(-(float)F::HALF, st ? ks_acc[1] : ks_acc[0], st ? kb_acc[1] : kb_acc[0]);
+    kx = rs * __builtin_fmaf(-(float)F::HALF, st ? bacc[3] : bacc[2], st ? bacc[1] : bacc[0]);
 }
 
 // Softmax update of this lane's column over its page (scores x = a sv[j] + kx; masked tokens
@@ -603,6 +604,13 @@ constexpr int decode_lds_bytes() {
 template <int D, int BITS, int NW>
 constexpr bool decode_fits() {
     return decode_lds_bytes<D, BITS, NW>() <= 160 * 1024;
+}
+
+// A third ring array (DEP = 3: each wave holds three page pairs, one consumed while two are in flight)
+// where it fits in LDS and in vmcnt's 63 outstanding loads.
+template <int D, int BITS, int NW>
+constexpr bool decode_fits3() {
+    return decode_lds_bytes<D, BITS, NW>() + 2 * NW * Ring<D, BITS>::SLOT <= 160 * 1024 && 4 * Ring<D, BITS>::DMA <= 63;
 }
 
 // byte offsets in the second array of the after-loop scratch: q [16][QS] fp32 (rows padded by 4
@@ -830,7 +838,7 @@ __device__ void merge_splits(const float* __restrict__ part_ml, const float* __r
 // NS > 1: each workgroup writes its split's partials; with `sync` (one zeroed int32 per
 // (sequence, kv head, head chunk)), the last workgroup of a (sequence, kv head, head chunk) to
 // finish merges all splits into `out` and resets its counter, so no second launch is needed.
-template <int D, int BITS, typename IN, int NW, int ST, bool ROT, bool WS>
+template <int D, int BITS, typename IN, int NW, int ST, bool ROT, bool WS, int DEP>
 __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) void decode_kernel(
     const IN* __restrict__ qg, IN* __restrict__ out, uint8_t* __restrict__ cache, int64_t bs, int64_t hs,
     IN* __restrict__ tail_k, const int32_t* __restrict__ tail_idx, const int32_t* __restrict__ block_table,
@@ -852,6 +860,8 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     using AL = AfterLoop<D, NW>;
     static_assert(2 * NW * R::SLOT >= AL::ML_OFF + 2 * NW * 16 * 4 + 16, "the after-loop scratch must fit");
     static_assert(2 * R::DMA <= 63, "vmcnt holds at most 63 loads");
+    static_assert(DEP == 2 || (DEP == 3 && !ROT && !WS && decode_fits3<D, BITS, NW>()),
+                  "three pairs per wave: unrotated, shared splits, where the third array fits");
     static_assert(2 * NW * R::SLOT >= 16 * D * 4, "ROT stages the chunk's q rows in the second array");
     static_assert(2 * NW * R::SLOT >= tile_bytes<D, IN>(), "the fused append's K tile lives in the first array");
 
@@ -860,6 +870,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     // pair is only read once both have landed)
     __shared__ __align__(16) uint8_t ringA[2 * NW * R::SLOT];
     __shared__ __align__(16) uint8_t ringB[2 * NW * R::SLOT];
+    __shared__ __align__(16) uint8_t ringC[DEP == 3 ? 2 * NW * R::SLOT : 16];   // DEP = 3 only
     __shared__ __align__(16) int tbl[WIN];                               // block ids of the window
     float* const m_l = reinterpret_cast<float*>(ringB + AL::ML_OFF);      // after the loop only
     float* const l_l = m_l + NW * 16;
@@ -962,6 +973,8 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     uint8_t* const sl1 = sl0 + R::SLOT;
     uint8_t* const sl2 = ringB + 2 * w * R::SLOT;
     uint8_t* const sl3 = sl2 + R::SLOT;
+    uint8_t* const sl4 = ringC + 2 * w * R::SLOT;                      // DEP = 3 only
+    uint8_t* const sl5 = sl4 + R::SLOT;
 
     // per-lane DMA source offsets (swizzled code rows), fixed for every page
     uint32_t voff[R::DMA];
@@ -1036,7 +1049,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         // vector memory load of the compiler's is outstanding once the page DMAs start
         if constexpr (WS) load_wave_window<PRE>(tb, bt + wb, wn, lane);
         else load_window();
-        int pa = ws ? 0 : w, pb = pa + PS;                               // the pairs in slots (0, 1), (2, 3)
+        int pa = ws ? 0 : w, pb = pa + PS, pc = pb + PS;                 // the pairs in slots (0, 1), (2, 3), (4, 5)
         // The first pairs go out before q is prepared: every compiler load in (vmcnt 0, so no later
         // wait of the compiler's counts the DMAs), the table's barrier, pair pa's DMAs into the first
         // array and pair pb's into the second; a rotated q is staged in the second array instead,
@@ -1046,6 +1059,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         KUSH_MARK(1);
         KUSH_ISSUE_PAIR(sl0, sl1, pa)
         if constexpr (!ROT) KUSH_ISSUE_PAIR(sl2, sl3, pb)
+        if constexpr (DEP == 3) KUSH_ISSUE_PAIR(sl4, sl5, pc)
         if (!ROT && TPRE && has_tail) {
             kpk.load(ktail);
             qpk.load(qg + qbase + (int64_t)min(r16, Gc - 1) * D + sdim);
@@ -1107,9 +1121,9 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
 #define KUSH_STEP(SA, SB, P, FIRST)                                                                \
     {                                                                                              \
         if ((P) >= pairs) break;                                                                   \
-        KUSH_WAIT_VM(2 * R::DMA);                                                                  \
+        KUSH_WAIT_VM((DEP - 1) * 2 * R::DMA);                                                      \
         if ((P) == 0) KUSH_MARK(2);                                                                \
-        const int nx = (P) + 2 * PS;                     /* this wave's pair after next */          \
+        const int nx = (P) + DEP * PS;                   /* this wave's next pair in these slots */ \
         int2 id2;                                                                                  \
         if constexpr (ST == 2) {                                                                   \
             float sv[8], kx;                                                                       \
@@ -1141,6 +1155,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
             for (;;) {
                 KUSH_STEP(sl0, sl1, pa, true)
                 KUSH_STEP(sl2, sl3, pb, false)
+                if constexpr (DEP == 3) KUSH_STEP(sl4, sl5, pc, false)
             }
             KUSH_MARK_WAVE();
             KUSH_WAIT_VM(0);                                     // drain the trailing (empty) issues
@@ -1151,11 +1166,13 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
             pairs = (wn + 1) / 2;
             pa = ws ? 0 : w;
             pb = pa + PS;
+            pc = pb + PS;
             if constexpr (WS) load_wave_window<PRE>(tb, bt + wb, wn, lane);   // a wave's DS operations stay in order
             else load_window();
             if (!ws) __syncthreads();
             KUSH_ISSUE_PAIR(sl0, sl1, pa)
             KUSH_ISSUE_PAIR(sl2, sl3, pb)
+            if constexpr (DEP == 3) KUSH_ISSUE_PAIR(sl4, sl5, pc)
         }
         if (ws) __syncthreads();                                 // every wave's pages done: rings idle
 #undef KUSH_STEP
@@ -1487,6 +1504,12 @@ int launch_decode(dim3 grid, hipStream_t stream, const void* q, void* out, const
                          const void* app_k, const void* app_v, int64_t app_ks, int64_t app_vs, int ws);
 
 #ifdef KUSH_DECODE_INSTANTIATE
+// Page pairs each wave holds in its ring where a third array fits (KUSHKASH_AMD_RING=2 | 3)
+inline int ring_depth() {
+    const char* env = std::getenv("KUSHKASH_AMD_RING");
+    return env != nullptr && env[0] == '3' ? 3 : 2;
+}
+
 template <int D, int BITS, typename IN, int NW, bool ROT>
 int launch_decode(dim3 grid, hipStream_t stream, const void* q, void* out, const void* cache, int64_t bs,
                          int64_t hs, const void* tail_k, const int32_t* tail_idx, const int32_t* block_table,
@@ -1495,9 +1518,13 @@ int launch_decode(dim3 grid, hipStream_t stream, const void* q, void* out, const
                          const void* app_k, const void* app_v, int64_t app_ks, int64_t app_vs, int ws) {
     // two page streams whenever the heads of a kv head fit in half the MFMA columns; wave splits are
     // built for 4 waves only (the policy's choice for the split counts that take them)
-    auto kern = group <= 8 ? decode_kernel<D, BITS, IN, NW, 2, ROT, false> : decode_kernel<D, BITS, IN, NW, 1, ROT, false>;
+    auto kern = group <= 8 ? decode_kernel<D, BITS, IN, NW, 2, ROT, false, 2> : decode_kernel<D, BITS, IN, NW, 1, ROT, false, 2>;
     if constexpr (NW == 4) {
-        if (ws) kern = group <= 8 ? decode_kernel<D, BITS, IN, NW, 2, ROT, true> : decode_kernel<D, BITS, IN, NW, 1, ROT, true>;
+        if (ws) kern = group <= 8 ? decode_kernel<D, BITS, IN, NW, 2, ROT, true, 2> : decode_kernel<D, BITS, IN, NW, 1, ROT, true, 2>;
+    }
+    if constexpr (NW == 4 && !ROT && decode_fits3<D, BITS, NW>()) {
+        if (!ws && ring_depth() == 3)
+            kern = group <= 8 ? decode_kernel<D, BITS, IN, NW, 2, ROT, false, 3> : decode_kernel<D, BITS, IN, NW, 1, ROT, false, 3>;
     }
     kern<<<grid, dim3(NW * WAVE), 0, stream>>>(
         (const IN*)q, (IN*)out, (uint8_t*)cache, bs, hs, (IN*)tail_k, tail_idx, block_table, seq_lens, bt_stride,
