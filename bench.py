@@ -913,14 +913,14 @@ def floor_timeline(w, shape, reps: int, warmup: int) -> None:
         torch.cuda.synchronize()
         t = fl.marks.cpu().numpy().astype(np.float64)
         t0 = t[:, 0].min()
-        us = (t[:, [0, 1, 2]] - t0) / 100.0
-        xcd = t[:, 3].astype(int)
-        loop = us[:, 2] - us[:, 1]
+        us = (t[:, [0, 1, 2, 3]] - t0) / 100.0
+        xcd = t[:, 4].astype(int)
+        loop = us[:, 3] - us[:, 2]
         pct = lambda x, p: float(np.percentile(x, p))
         print(f"\nfloor mode {mode}, {wv} waves, depth {depth}" + (f", z {z}" if mode == 1 else "")
-              + f": launch {rep + 1} of {reps}, first workgroup start -> last pages done {us[:, 2].max():.2f} us\n\n"
+              + f": launch {rep + 1} of {reps}, first workgroup start -> last pages done {us[:, 3].max():.2f} us\n\n"
               "| phase (us from the first start) | min | p10 | p50 | p90 | max |\n|---|---|---|---|---|---|")
-        for name, k in (("start", 0), ("first page pair landed", 1), ("pages done", 2)):
+        for name, k in (("start", 0), ("first page DMAs issued", 1), ("first page pair landed", 2), ("pages done", 3)):
             x = us[:, k]
             print(f"| {name} | {x.min():.2f} | {pct(x, 10):.2f} | {pct(x, 50):.2f} | {pct(x, 90):.2f} | {x.max():.2f} |")
         print("\n| XCD | workgroups | page loop p10 / p50 / max (us) | pages done p50 / max (us) |\n|---|---|---|---|")
@@ -928,7 +928,7 @@ def floor_timeline(w, shape, reps: int, warmup: int) -> None:
             m = xcd == x
             if m.any():
                 print(f"| {x} | {int(m.sum())} | {pct(loop[m], 10):.2f} / {pct(loop[m], 50):.2f} / {loop[m].max():.2f} | "
-                      f"{pct(us[m, 2], 50):.2f} / {us[m, 2].max():.2f} |", flush=True)
+                      f"{pct(us[m, 3], 50):.2f} / {us[m, 3].max():.2f} |", flush=True)
 
 
 def main(argv=None):

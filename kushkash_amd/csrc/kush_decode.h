@@ -533,9 +533,12 @@ __device__ __forceinline__ void consume2(const uint8_t* s0, int ds, f4 (&o)[D / 
     for (int j = 1; j < 8; ++j) pm = __builtin_fmaxf(pm, sv[j]);
     pm = rows_max(__builtin_fmaf(pm, a, kx));
     const float m_new = pm > m_run + 3.0f ? pm : m_run;
+    // A masked page (every token's sv = -inf, or the whole column's kx = -inf with finite sv from a
+    // zero-filled slot) moves nothing: its x = -inf, so its weights are exp2(-inf) = 0, also in a
+    // column that has seen nothing yet (m_new = -inf, where the reference point is -inf as well)
     const bool none = m_new == -__builtin_inff();                 // nothing seen yet in this column
     const float corr = none ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-    const float bp = none ? 0.0f : kx - m_new;
+    const float bp = none ? -__builtin_inff() : kx - m_new;
 
     const h4v vs0 = *reinterpret_cast<const h4v*>(mine + F::OFF_VS + 8 * q);
     const h4v vs1 = *reinterpret_cast<const h4v*>(mine + F::OFF_VS + 32 + 8 * q);
@@ -1128,9 +1131,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         if constexpr (ST == 2) {                                                                   \
             float sv[8], kx;                                                                       \
             pair_scores2<D, BITS, QLO>(SA, qa, qla, qh, ql, sv, kx, rs, lane);                     \
-            if (2 * (P) + 1 >= wn && r16 >= 8) {                                                   \
-                _Pragma("unroll") for (int jj = 0; jj < 8; ++jj) sv[jj] = -__builtin_inff();       \
-            }                                                                                      \
+            if (2 * (P) + 1 >= wn && r16 >= 8) kx = -__builtin_inff();   /* page B masked */        \
             id2 = *reinterpret_cast<const int2*>(tb + min(2 * nx, TW - 2));                        \
             consume2<D, BITS>(SA, R::SLOT, o, vacc, sv, sa, kx, m_run, l_run, vb_run, lane);       \
         } else {                                                                                   \

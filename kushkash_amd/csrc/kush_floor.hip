@@ -14,9 +14,9 @@
 //           every kv head, heads fastest, so a page pair is two neighbouring records of one block
 //   waves   4 or 8 per workgroup; depth: page pairs each wave holds in its ring (2 = the decode's:
 //           one consumed while one is in flight; 3 or 4: more bytes in flight per wave)
-// marks (optional, int64 [workgroups][8]): the 100 MHz wall clock at the workgroup's start, when wave 0's
-// first pair landed, when every wave's pages were done (after the workgroup barrier), the XCD the
-// workgroup ran on, and the wall clock at which waves 0-3 finished their pages.
+// marks (optional, int64 [workgroups][8]): the 100 MHz wall clock at the workgroup's start, when wave 0
+// issued its first page DMAs, when wave 0's first pair landed, when every wave's pages were done (after
+// the workgroup barrier), and the XCD the workgroup ran on.
 #include "kush_decode.h"
 
 using namespace kush;
@@ -66,6 +66,7 @@ __global__ __launch_bounds__(NW * WAVE) void floor_kernel(const uint8_t* __restr
     };
     uint8_t* const mine = ring + 2 * w * R::SLOT;                // slot d of this wave: mine + d * 2 NW SLOT
     constexpr int DSTRIDE = 2 * NW * R::SLOT;
+    const long long t_issue = wall_clock64();
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
         const int p = w + d * NW;
@@ -87,20 +88,17 @@ __global__ __launch_bounds__(NW * WAVE) void floor_kernel(const uint8_t* __restr
         issue_unit(sl + R::SLOT, 2 * nx + 1);
     }
     KUSH_WAIT_VM(0);                                             // the trailing (empty) issues
-    const long long t_wave = wall_clock64();
     const int wg = blockIdx.y * gridDim.x + blockIdx.x;
     sums[(int64_t)wg * NW * WAVE + threadIdx.x] = acc;
     if (marks == nullptr) return;
-    __shared__ long long wave_done[NW];
-    if (lane == 0) wave_done[w] = t_wave;
     __syncthreads();
     if (threadIdx.x == 0) {
         long long* const r = marks + (int64_t)wg * 8;
         r[0] = t_start;
-        r[1] = t_first;
-        r[2] = wall_clock64();
-        r[3] = __builtin_amdgcn_s_getreg((3 << 11) | 20);        // XCC_ID bits [3:0]
-        for (int k = 0; k < 4 && k < NW; ++k) r[4 + k] = wave_done[k];
+        r[1] = t_issue;
+        r[2] = t_first;
+        r[3] = wall_clock64();
+        r[4] = __builtin_amdgcn_s_getreg((3 << 11) | 20);        // XCC_ID bits [3:0]
     }
 }
 
