@@ -159,7 +159,7 @@ def make_workload(a, dev, defer: bool = False):
                 js = torch.arange(n, dtype=torch.int32, device=dev).repeat_interleave(pages)
                 jp = torch.arange(pages, dtype=torch.int32, device=dev).repeat(n)
                 ops.write(k, v, qsl, seq_lens[s0:s1], tail_idx[s0:s1], js, jp, cache,
-                          tables[i][s0:s1].contiguous(), tail_k, rot=a.rot)
+                          tables[i][s0:s1].contiguous(), tail_k, fused=True, rot=a.rot)
                 del k, v
         q.copy_(torch.randn(B, a.hq, D, generator=gen, device=dev).to(dtype))
         torch.cuda.synchronize()
@@ -459,7 +459,8 @@ def ragged_cache(ops, lens, room: int, Hkv: int, bias_sigma: float, bias_frac: f
         qsl = torch.tensor([0] + list(torch.tensor(ln).cumsum(0)), dtype=torch.int32, device=dev)
         js = torch.cat([torch.full((-(-n // PAGE),), i, dtype=torch.int32) for i, n in enumerate(ln)]).to(dev)
         jp = torch.cat([torch.arange(-(-n // PAGE), dtype=torch.int32) for n in ln]).to(dev)
-        ops.write(k, v, qsl, seq_lens[s0:s1], tail_idx[s0:s1], js, jp, cache, table[s0:s1].contiguous(), tail_k)
+        ops.write(k, v, qsl, seq_lens[s0:s1], tail_idx[s0:s1], js, jp, cache, table[s0:s1].contiguous(), tail_k,
+                  fused=True)
         del k, v
         s0 = s1
     torch.cuda.synchronize()

@@ -213,13 +213,15 @@ class Ops:
 
     def write(self, k: torch.Tensor, v: torch.Tensor, query_start_loc: torch.Tensor, seq_lens: torch.Tensor,
               tail_idx: torch.Tensor, job_seq: torch.Tensor, job_page: torch.Tensor, cache: torch.Tensor,
-              block_table: torch.Tensor, tail_k: torch.Tensor, *, fused: bool = True, rot: bool = False) -> None:
+              block_table: torch.Tensor, tail_k: torch.Tensor, *, fused: bool = False, rot: bool = False) -> None:
         """Ragged multi-token write: sequence s owns rows [qsl[s], qsl[s+1]) at positions ending at
         seq_lens[s] (already counting them); one job per (sequence, logical page) touched
-        (_ops.py:82-101). The reference's two ordered launches (V rows + completed K pages, then K
-        tails) run as one (mode 2) when `fused`, which needs a job for every page each chunk touches
-        (pages_touched, as every caller builds the list); fused=False launches modes 0 and 1 and
-        accepts any subset of those jobs. rot: as in append (rows from the chunk are rotated)."""
+        (_ops.py:82-101). By default the reference's two ordered launches (mode 0: V rows + completed
+        K pages, then mode 1: K tails), which accept any subset of those jobs. fused=True declares that
+        the list holds a job for every page each chunk touches (pages_touched, as this package's callers
+        build it) and runs both modes as one launch (mode 2), whose tail handling relies on that; under
+        KUSHKASH_AMD_VALIDATE the declaration is checked and a list that misses a touched page raises.
+        rot: as in append (rows from the chunk are rotated)."""
         n_jobs, H = job_seq.numel(), k.shape[1]
         if n_jobs == 0:
             return
@@ -242,6 +244,8 @@ class Ops:
             pages = (seq_lens.long()[js] + PAGE - 1) // PAGE
             if bool((job_page.long() < 0).any()) or bool((job_page.long() >= pages).any()):
                 raise ValueError("job_page outside the sequence's pages")
+            if fused:
+                _check_covers(query_start_loc, seq_lens, job_seq, job_page)
             self._check_values(cache, block_table, seq_lens, tail_idx, tail_k, S)
         bs, hs = _byte_strides(cache)
         for mode in ((2,) if fused else (0, 1)):
@@ -443,6 +447,25 @@ def pages_touched(ctx: int, total: int) -> range:
     if total <= ctx:
         return range(0)
     return range(ctx // PAGE, (total - 1) // PAGE + 1)
+
+
+def _check_covers(query_start_loc: torch.Tensor, seq_lens: torch.Tensor, job_seq: torch.Tensor,
+                  job_page: torch.Tensor) -> None:
+    """A one-launch write (mode 2) needs a job for every page each sequence's new rows touch
+    (pages_touched(seq_lens[s] - rows, seq_lens[s])): the first touched page's job reads a partly
+    filled tail and the last one's writes the new tail. Raises ValueError naming the first sequence
+    whose list misses a touched page."""
+    qsl = query_start_loc.long().cpu().tolist()
+    sl = seq_lens.long().cpu().tolist()
+    have: dict[int, set] = {}
+    for s_, p_ in zip(job_seq.long().cpu().tolist(), job_page.long().cpu().tolist()):
+        have.setdefault(s_, set()).add(p_)
+    for s_ in range(len(sl)):
+        rows = qsl[s_ + 1] - qsl[s_]
+        missing = [p_ for p_ in pages_touched(sl[s_] - rows, sl[s_]) if p_ not in have.get(s_, ())]
+        if missing:
+            raise ValueError(f"write(fused=True): the jobs of sequence {s_} miss touched page(s) {missing[:4]}; "
+                             "list every page pages_touched gives, or write with fused=False (two launches)")
 
 
 def default_scale(head_dim: int) -> float:

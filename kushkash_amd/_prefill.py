@@ -28,6 +28,7 @@ import torch
 
 from ._attention import ragged_attention, unpacked_history_attention
 from ._ops import PAGE, pages_touched
+from ._serving import torch_unpack, unpack_mode
 
 
 def record_bits() -> int:
@@ -214,8 +215,12 @@ class ExtendPlan:
                 if g.has_history:
                     kp = torch.empty((g.n_keys,) + tuple(k3.shape[1:]), dtype=k3.dtype, device=k3.device)
                     vp = torch.empty_like(kp)
-                    ops.unpack(cache, g.page_blk, g.page_dst, g.tail_blk, g.tail_info, tail, k3[a:b], v3[a:b],
-                               g.new_dst, kp, vp, rot)
+                    if unpack_mode() == "torch":           # KUSHKASH_UNPACK=torch: the same bits, built by torch
+                        torch_unpack(cache, g.page_blk, g.page_dst, g.tail_blk, g.tail_info, tail, k3[a:b], v3[a:b],
+                                     g.new_dst, kp, vp, ops.D, ops.bits, rot)
+                    else:
+                        ops.unpack(cache, g.page_blk, g.page_dst, g.tail_blk, g.tail_info, tail, k3[a:b], v3[a:b],
+                                   g.new_dst, kp, vp, rot)
                 else:                                  # no history: the new rows are the keys
                     kp, vp = k3[a:b], v3[a:b]
                 if varlen is not None:
@@ -237,4 +242,4 @@ class ExtendPlan:
               cache: torch.Tensor, block_table: torch.Tensor, tail: torch.Tensor, rot: bool) -> None:
         """Quantize the step's new rows into the cache (one write launch); seq_lens count them."""
         ops.write(k3, v3, self.q_start, seq_lens, slots, self.job_seq, self.job_page, cache, block_table, tail,
-                  rot=rot)
+                  fused=True, rot=rot)

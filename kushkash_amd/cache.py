@@ -190,7 +190,7 @@ class KushCache:
             starts = seqs * T
             qsl = torch.cat([starts, starts[-1:] + T])
             self.ops.write(kr, vr, qsl, self.seq_lens[layer], self.tail_idx,
-                           seqs.repeat_interleave(len(touched)), pages.repeat(B), **dst, **kw)
+                           seqs.repeat_interleave(len(touched)), pages.repeat(B), **dst, fused=True, **kw)
         self._tokens[layer] = n + T
 
     def attend(self, layer: int, q: torch.Tensor) -> torch.Tensor:

@@ -134,16 +134,18 @@ def prompt_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: f
                      block_bytes: int = 1 << 28) -> torch.Tensor:
     """Causal attention of a prompt over itself when nothing is cached yet: q [B, Hq, T, D], k, v
     [B, Hkv, T, D] -> [B, Hq, T, D] in q's dtype (hf.py:122-129). Half-precision inputs go to torch's
-    fused attention, limited to its flash and memory-efficient kernels (K / V expanded to the q heads);
-    everything else, and any input those kernels refuse, to fp32 products over blocks of keys whose
-    memory stays within block_bytes. torch's half-precision math path (batched products over
-    transposed views) is never taken."""
+    fused attention, limited to its flash kernel (K / V expanded to the q heads); everything else, and
+    any input the flash kernel refuses, to fp32 products over blocks of keys whose memory stays within
+    block_bytes. torch's memory-efficient kernel is not allowed: on ROCm its dense and varlen forms are
+    the same kernel family, and its varlen form with a bottom-right causal mask has taken an
+    illegal-address fault on this device. torch's half-precision math path (batched products over
+    transposed views) is never taken either."""
     if q.dtype in (torch.float16, torch.bfloat16):
         g = q.shape[1] // k.shape[1]
         ke = k.repeat_interleave(g, 1) if g > 1 else k
         ve = v.repeat_interleave(g, 1) if g > 1 else v
         try:
-            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
                 return F.scaled_dot_product_attention(q, ke, ve, is_causal=True, scale=scale)
         except RuntimeError:
             pass

@@ -94,7 +94,10 @@ class OracleOps:
              seq_lens.data_ptr(), pos_offset, int(advance), cache.data_ptr(), bs, hs, tail_k.data_ptr(),
              tail_idx.data_ptr(), block_table.data_ptr(), block_table.stride(0), H, S)
 
-    def write(self, k, v, query_start_loc, seq_lens, tail_idx, job_seq, job_page, cache, block_table, tail_k) -> None:
+    def write(self, k, v, query_start_loc, seq_lens, tail_idx, job_seq, job_page, cache, block_table, tail_k, *,
+              fused: bool = False) -> None:
+        """The reference's two ordered modes (0, then 1); `fused` (Ops.write's one-launch declaration) is
+        accepted and changes nothing here: for a complete job list both give the same bytes."""
         n_jobs, H = job_seq.numel(), k.shape[1]
         if n_jobs == 0:
             return

@@ -106,10 +106,11 @@ class RotatingOracleOps(OracleOps):
         super().append(k, v, seq_lens, tail_idx, cache, block_table, tail_k, pos_offset, advance)
 
     def write(self, k, v, query_start_loc, seq_lens, tail_idx, job_seq, job_page, cache, block_table, tail_k, *,
-              fused=True, rot=False):
+              fused=False, rot=False):
         if rot:
             k, v = self._rotated(k), self._rotated(v)
-        super().write(k, v, query_start_loc, seq_lens, tail_idx, job_seq, job_page, cache, block_table, tail_k)
+        super().write(k, v, query_start_loc, seq_lens, tail_idx, job_seq, job_page, cache, block_table, tail_k,
+                      fused=fused)
 
     def decode(self, q, out, cache, block_table, seq_lens, tail_idx, tail_k, scale, n_splits=1, work=None, *,
                waves=None, order=None, rot=False):

@@ -122,3 +122,44 @@ def test_c3_append_full_size(lens_kind, fused):
     changed = (cache != before).flatten(1).any(1).nonzero().flatten()
     assert set(changed.tolist()) <= set(blocks.tolist()), "the append wrote outside the touched pages"
     assert torch.equal(sl.cpu(), torch.tensor(lens, dtype=torch.int32) + 1)   # advance = 0: lengths untouched
+
+
+def test_partial_job_list_takes_the_reference_two_launches():
+    """Ops.write with its default (the reference's two launches) accepts any subset of the
+    pages_touched jobs, as the reference's write does: with the last touched page's job left out of
+    every sequence's list, the records and K tails equal the oracle's write of the same list byte for
+    byte (that page's V rows and the new K tail are simply not written); under KUSHKASH_AMD_VALIDATE a
+    one-launch write of the same list raises."""
+    import os
+    B, Hkv, D, bits, T = 4, 2, 128, 4, 70
+    dtype = torch.bfloat16
+    n0 = [5, 32, 61, 100]
+    total = [n + T for n in n0]
+    touched = [pages_touched(a, b) for a, b in zip(n0, total)]
+    jobs = [(i, p) for i, t in enumerate(touched) for p in list(t)[:-1]]
+    RB = record_bytes(D, bits)
+    g = torch.Generator().manual_seed(11)
+    nblk = max(total) // PAGE + 1
+    cache0 = torch.randint(0, 256, (B * nblk, Hkv, RB), dtype=torch.uint8, generator=g)
+    table = torch.arange(B * nblk, dtype=torch.int32).view(B, nblk)
+    tail0 = torch.randn(B, Hkv, PAGE, D, generator=g).to(dtype)
+    k = torch.randn(B * T, Hkv, D, generator=g).to(dtype)
+    v = torch.randn(B * T, Hkv, D, generator=g).to(dtype)
+    qsl = torch.arange(B + 1, dtype=torch.int32) * T
+    sl = torch.tensor(total, dtype=torch.int32)
+    tail_idx = torch.arange(B, dtype=torch.int32)
+    js = torch.tensor([j[0] for j in jobs], dtype=torch.int32)
+    jp = torch.tensor([j[1] for j in jobs], dtype=torch.int32)
+    ops = Ops(torch.device(DEV), D, bits, 4, dtype)
+    cache, tail = cache0.to(DEV), tail0.to(DEV)
+    args = (k.to(DEV), v.to(DEV), qsl.to(DEV), sl.to(DEV), tail_idx.to(DEV), js.to(DEV), jp.to(DEV), cache,
+            table.to(DEV), tail)
+    ops.write(*args)
+    torch.cuda.synchronize()
+    want_cache, want_tail = cache0.clone(), tail0.float()
+    OracleOps("cpu", D, bits, 4).write(k.float(), v.float(), qsl, sl, tail_idx, js, jp, want_cache, table, want_tail)
+    assert torch.equal(cache.cpu(), want_cache), "records differ from the oracle's write of the same jobs"
+    assert torch.equal(tail.float().cpu(), want_tail), "K tails differ from the oracle's write of the same jobs"
+    if os.environ.get("KUSHKASH_AMD_VALIDATE", "") not in ("", "0"):
+        with pytest.raises(ValueError, match="miss touched page"):
+            ops.write(*args, fused=True)

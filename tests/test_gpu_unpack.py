@@ -181,3 +181,19 @@ def test_unpack_random_groups(seed):
         k_new, v_new = odd_rows(c["k_new"]), odd_rows(c["v_new"])
     got = gpu_unpack(c, D, bits, rot, dtype, k_new, v_new)
     assert_same(c, got, oracle_unpack(c, D, bits, rot, dtype), dtype)
+
+
+@pytest.mark.parametrize("D,bits", [(128, 4), (64, 8)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("rot", [False, True])
+def test_torch_unpack_equals_the_kernel(D, bits, dtype, rot):
+    """KUSHKASH_UNPACK=torch (kushkash_amd._serving.torch_unpack, the serving switch's torch path) gives
+    the unpack kernel's bits on the GPU, and leaves the same gap rows untouched."""
+    from kushkash_amd._serving import torch_unpack
+    c = make_group(D, bits, dtype, seed=3 * D + bits)
+    shape = (c["rows"], c["H"], D)
+    kp = torch.full(shape, float("nan"), dtype=dtype, device=DEV)
+    vp = torch.full(shape, float("nan"), dtype=dtype, device=DEV)
+    args = [c[n].to(DEV) for n in INDEX_NAMES]
+    torch_unpack(c["records"].to(DEV), *args, kp, vp, D, bits, rot)
+    assert_same(c, (kp.cpu(), vp.cpu()), gpu_unpack(c, D, bits, rot, dtype), dtype)

@@ -128,3 +128,23 @@ def test_rotation_switch(monkeypatch):
     monkeypatch.setenv("KUSHKASH_ROTATE", "maybe")
     with pytest.raises(ValueError):
         rotation_enabled(4)
+
+
+def test_fused_write_coverage_check():
+    """A one-launch write (Ops.write(fused=True)) needs a job for every page the new rows touch;
+    the validation check names the sequence whose list misses one (the last page here, the first
+    there) and accepts the complete pages_touched list."""
+    from kushkash_amd._ops import _check_covers
+    qsl = torch.tensor([0, 40, 40, 100], dtype=torch.int32)     # sequence 1 has no new rows
+    sl = torch.tensor([50, 7, 130], dtype=torch.int32)          # 40 rows end at 50; 60 rows end at 130
+    full = [(0, p) for p in pages_touched(10, 50)] + [(2, p) for p in pages_touched(70, 130)]
+
+    def check(jobs):
+        _check_covers(qsl, sl, torch.tensor([j[0] for j in jobs], dtype=torch.int32),
+                      torch.tensor([j[1] for j in jobs], dtype=torch.int32))
+    check(full)
+    check(full + [(1, 0)])                                       # extra jobs are allowed
+    with pytest.raises(ValueError, match="sequence 0 miss touched page"):
+        check([j for j in full if j != (0, 1)])                  # the last page of sequence 0
+    with pytest.raises(ValueError, match="sequence 2 miss touched page"):
+        check([j for j in full if j != (2, 2)])                  # the first page of sequence 2
