@@ -713,6 +713,51 @@ __device__ __forceinline__ f4 fetch4(const float* p) {
     return f4{a, b, c, d};
 }
 
+// The splits a wave has finished (wave splits with several splits per wave), folded in split order:
+// a finished split's own softmax state (m, l, vb and its O and -HALF sum P' accumulators, per MFMA
+// column) is merged into the folded one by log-sum-exp -- both rescaled to the larger max, a side over
+// no keys adding nothing -- and the split's state starts afresh for the next split. Every accumulator
+// is in the same units in every split, so the fold is the same weighted sum the merge of split
+// partials forms, in a fixed order.
+template <int DT>
+struct SplitFold {
+    f4 o[DT];
+    f4 vacc = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -__builtin_inff(), l = 0.0f, vb = 0.0f;
+    __device__ __forceinline__ SplitFold() {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    __device__ __forceinline__ void fold(f4 (&so)[DT], f4& svacc, float& sm, float& sl, float& svb, bool reset) {
+        const float M = __builtin_fmaxf(m, sm);
+        const float a = m == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m - M);
+        const float b = sm == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(sm - M);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt] = o[dt] * a + so[dt] * b;
+        vacc = vacc * a + svacc * b;
+        l = l * a + sl * b;
+        vb = vb * a + svb * b;
+        m = M;
+        if (reset) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) so[dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            svacc = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            sm = -__builtin_inff();
+            sl = 0.0f;
+            svb = 0.0f;
+        }
+    }
+    // the folded state back into the wave's running state (after its last split)
+    __device__ __forceinline__ void restore(f4 (&so)[DT], f4& svacc, float& sm, float& sl, float& svb) const {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) so[dt] = o[dt];
+        svacc = vacc;
+        sm = m;
+        sl = l;
+        svb = vb;
+    }
+};
+
 // (m, l) of two disjoint key sets in log2 units folded into one: the sums rescaled to the larger
 // max; a side over no keys (m = -inf) adds nothing.
 __device__ __forceinline__ void fold_ml(float& m, float& l, float m2, float l2) {
@@ -848,7 +893,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     const int32_t* __restrict__ seq_lens, int64_t bt_stride, int bt_cols, int H, int G, float p2, float rs, int NS,
     float* __restrict__ part_ml, float* __restrict__ part_o, int32_t* __restrict__ sync,
     const int32_t* __restrict__ seq_order, const IN* __restrict__ app_k, const IN* __restrict__ app_v, int64_t app_ks,
-    int64_t app_vs) {
+    int64_t app_vs, int KW) {
     constexpr bool ws = WS;
     using F = Fmt<D, BITS>;
     using R = Ring<D, BITS>;
@@ -892,12 +937,14 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         s = seq_order[L / H];
         h = L % H;
     }
-    // ws (wave splits, NS a multiple of NW): each wave takes a whole split of its own -- splits zg NW + w
-    // of workgroup zg -- with its own block-id table and no merge with the other waves; else the
-    // waves of a workgroup share its split's pages
-    const int NSG = ws ? NS / NW : NS;                                    // workgroups per head chunk
+    // ws (wave splits, NS a multiple of NW KW): each wave takes KW whole consecutive splits of its own --
+    // splits (zg NW + w) KW .. + KW - 1 of workgroup zg, one contiguous run of pages -- with its own
+    // block-id table and no merge with the other waves until the end; else the waves of a workgroup
+    // share its split's pages. With KW > 1 a wave starts a fresh softmax state at each of its splits
+    // and folds the finished split into its running state in split order (a log-sum-exp merge).
+    const int NSG = ws ? NS / (NW * KW) : NS;                             // workgroups per head chunk
     const int zg = blockIdx.z % NSG, gc = blockIdx.z / NSG, g0 = gc * 16;
-    const int z = ws ? zg * NW + w : zg;                                  // this wave's split
+    const int z = ws ? (zg * NW + w) * KW : zg;                           // this wave's (first) split
     const int tw = ws ? NW - 1 : 0;                                       // the wave taking the partial page
     // ws with the in-launch merge (sync): the workgroup first merges its NW splits in LDS and writes one
     // partial (index zg of NSG), so the last workgroup merges NSG partials; without sync every wave
@@ -945,8 +992,8 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     const int tix = tail_idx != nullptr ? tail_idx[s] : 0;              // the tail slot, with the length
     const int full = n / PAGE, tail_n = n % PAGE;
     const int pps = (full + NS - 1) / NS;
-    const int p0 = min(full, z * pps), p1 = min(full, p0 + pps);
-    const int wp1 = ws ? min(full, (zg + 1) * NW * pps) : p1, wp0 = ws ? min(full, zg * NW * pps) : p0;
+    const int p0 = min(full, z * pps), p1 = min(full, p0 + (ws ? KW : 1) * pps);
+    const int wp1 = ws ? min(full, (zg + 1) * NW * KW * pps) : p1, wp0 = ws ? min(full, zg * NW * KW * pps) : p0;
     const uint8_t* head_base = cache + (int64_t)h * hs;
 
     // Fused append (app_k): the token at position n - 1 of sequence s, kv head h, is written by the one
@@ -958,7 +1005,7 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         if (gc == 0 && n > 0) {
             const int pos = n - 1, slot = pos % PAGE, pg = pos / PAGE;
             const int owner = slot == PAGE - 1 ? pg / max(pps, 1) : NS - 1;
-            if (zg == (ws ? owner / NW : owner)) {                  // the whole workgroup
+            if (zg == (ws ? owner / (NW * KW) : owner)) {           // the whole workgroup
                 const IN* krow = app_k + (int64_t)s * app_ks + (int64_t)h * D;
                 IN* tail = tail_k + ((int64_t)tix * H + h) * PAGE * D;
                 uint8_t* rec = cache + (int64_t)bt[pg] * bs + (int64_t)h * hs;
@@ -988,6 +1035,10 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[dt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     float m_run = -__builtin_inff(), l_run = 0.0f, vb_run = 0.0f;
+    // ws, KW > 1: the splits this wave finished, folded in split order (fold_split), and the pages left
+    // in the split being streamed
+    SplitFold<DT> folded;
+    int split_left = pps;
 
     // Partial page (last split): its exact-K scores are 16 x 16 x 4 fp32 MFMAs (fp32 products and
     // sums) over all waves: wave w takes tokens 16 (w & 1) .. + 15 and part w >> 1 of the contraction
@@ -1150,6 +1201,13 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
                             head_base, bs, voff);                                                  \
         issue_page<D, BITS>(SB, 2 * nx + 1 < wn, __builtin_amdgcn_readfirstlane(id2.y), head_base, bs, voff); \
         tdma = tdma || tl;                                                                         \
+        if constexpr (WS) {                                                                        \
+            split_left -= 2;                                 /* a split holds an even page count */ \
+            if (split_left == 0 && KW > 1) {                                                       \
+                split_left = pps;                                                                  \
+                if (wb + 2 * (P) + 2 < p1) folded.fold(o, vacc, m_run, l_run, vb_run, true);       \
+            }                                                                                      \
+        }                                                                                          \
         (P) = nx;                                                                                  \
     }
         for (;;) {
@@ -1234,6 +1292,13 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
                 const float b0[1] = {0.0f};
                 consume_pages<D, BITS, 1>(sp, o, vacc, x, 1.0f, b0, m_run, l_run, vb_run, lane);
             }
+        }
+    }
+
+    if constexpr (WS) {                                          // the wave's last split, folded in last
+        if (KW > 1) {
+            folded.fold(o, vacc, m_run, l_run, vb_run, false);
+            folded.restore(o, vacc, m_run, l_run, vb_run);
         }
     }
 
@@ -1530,7 +1595,7 @@ int launch_decode(dim3 grid, hipStream_t stream, const void* q, void* out, const
     kern<<<grid, dim3(NW * WAVE), 0, stream>>>(
         (const IN*)q, (IN*)out, (uint8_t*)cache, bs, hs, (IN*)tail_k, tail_idx, block_table, seq_lens, bt_stride,
         bt_cols, hkv, group, p2, rs, n_splits, part_ml, part_o, sync, seq_order, (const IN*)app_k, (const IN*)app_v,
-        app_ks, app_vs);
+        app_ks, app_vs, ws > 0 ? ws : 1);
     return kush_check_launch("kush_decode");
 }
 #endif

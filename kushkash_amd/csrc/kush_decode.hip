@@ -23,12 +23,26 @@ struct Append {
 // NS >= 8 and the workgroups still fill MI355X's 256 CUs. C4 (8 x 131,072 tokens) at 4 waves:
 // NS 32 / 64 / 128 / 256 232 / 243 / 280 / 373 us -> 222 / 226 / 234 / 242 us.
 // KUSHKASH_AMD_WAVE_SPLITS=0 / 1 turns it off / on wherever NS allows it.
-int wave_splits(int ns, int nw, int64_t chunks) {
+//
+// Returns 0 (no wave splits) or KW, the splits each wave takes: with the in-launch merge, as many
+// consecutive splits per wave as keep at least 256 workgroups (one per CU of MI355X), so a large NS
+// no longer multiplies the workgroups and their fixed costs (launch, q, window loads, the ramp of
+// the first pages, the merge in LDS) -- C4 at NS 64 / 128 / 256 runs 256 workgroups of 4 waves,
+// each wave streaming its 4 / 8 / 16 splits as one run of pages and folding each finished split
+// into its running state. KUSHKASH_AMD_SPLITS_PER_WAVE=k takes k splits per wave wherever NS allows
+// it (k = 1: one split per wave, as without the fold).
+int wave_splits(int ns, int nw, int64_t chunks, bool fused_merge) {
     if (nw != 4 || ns % nw != 0 || ns < 2 * nw) return 0;             // built for 4 waves
     const char* env = std::getenv("KUSHKASH_AMD_WAVE_SPLITS");
     if (env != nullptr && env[0] == '0') return 0;
-    if (env != nullptr && env[0] == '1') return 1;
-    return chunks * (ns / nw) >= 256 ? 1 : 0;
+    if (!(env != nullptr && env[0] == '1') && chunks * (ns / nw) < 256) return 0;
+    if (!fused_merge) return 1;                                      // the caller's combine reads NS partials
+    const char* per = std::getenv("KUSHKASH_AMD_SPLITS_PER_WAVE");
+    const int forced = per != nullptr ? std::atoi(per) : 0;
+    if (forced >= 1) return ns % (nw * forced) == 0 ? forced : 1;
+    int kw = 1;
+    while ((ns / nw) % (2 * kw) == 0 && chunks * (ns / (nw * 2 * kw)) >= 256) kw *= 2;
+    return kw;
 }
 
 int decode_impl(const char* what, int head_dim, int bits, int group, int dtype, const void* q, void* out,
@@ -72,8 +86,8 @@ int decode_impl(const char* what, int head_dim, int bits, int group, int dtype, 
         // the largest of the requested, 4 and 2 waves whose rings fit in LDS
         const auto launch = [&](auto nw) -> int {
             constexpr int NW = decltype(nw)::value;
-            const int ws = wave_splits(n_splits, NW, (int64_t)n_seqs * hkv * n_gc);
-            const dim3 g(n_seqs, hkv, (ws ? n_splits / NW : n_splits) * n_gc);
+            const int ws = wave_splits(n_splits, NW, (int64_t)n_seqs * hkv * n_gc, split_sync != nullptr);
+            const dim3 g(n_seqs, hkv, (ws ? n_splits / (NW * ws) : n_splits) * n_gc);
             return rot ? launch_decode<D, BITS, IN, NW, true>(g, KUSH_DECODE_ARGS, ws)
                        : launch_decode<D, BITS, IN, NW, false>(g, KUSH_DECODE_ARGS, ws);
         };

@@ -28,12 +28,18 @@ def _decode(c, q, ns, work, mode, monkeypatch):
 
 @pytest.mark.parametrize("bits,dtype,D,G", [(4, torch.bfloat16, 128, 7), (8, torch.float16, 64, 4),
                                             (4, torch.float16, 256, 2), (4, torch.bfloat16, 128, 20)])
-@pytest.mark.parametrize("ns", [8, 16, 64])
-def test_ragged_batch(ns, bits, dtype, D, G, monkeypatch):
+@pytest.mark.parametrize("ns,kw", [(8, ""), (16, ""), (64, ""), (8, "2"), (16, "4"), (64, "2"), (64, "8")])
+def test_ragged_batch(ns, kw, bits, dtype, D, G, monkeypatch):
     """Ragged lengths (empty, under one page, partial last pages, pages fewer than splits), G > 16
     (two head chunks) included, in the natural and the longest-first start order; two calls in a row
-    check that the split counters reset themselves."""
-    torch.manual_seed(ns * 100 + bits + D + G)
+    check that the split counters reset themselves. kw: splits per wave forced (a wave streams its kw
+    splits as one run of pages and folds each finished split into its running state; sequences whose
+    split length is odd keep one state over the run), else the library's choice."""
+    if kw:
+        monkeypatch.setenv("KUSHKASH_AMD_SPLITS_PER_WAVE", kw)
+    else:
+        monkeypatch.delenv("KUSHKASH_AMD_SPLITS_PER_WAVE", raising=False)
+    torch.manual_seed(ns * 100 + bits + D + G + len(kw))
     lens = [0, 5, PAGE, 3 * PAGE + 7, 40 * PAGE + 31, 97 * PAGE, 130 * PAGE + 1, 64 * PAGE + 16]
     S, H = len(lens), 2
     ops = kk.Ops(torch.device(DEV), D, bits, G, dtype)
@@ -75,12 +81,15 @@ def test_ragged_batch(ns, bits, dtype, D, G, monkeypatch):
     assert int(ops._sync.abs().sum()) == 0
 
 
-@pytest.mark.parametrize("bits", [4, 8])
-def test_two_windows_per_wave_then_partial_page(bits, monkeypatch):
-    """A wave's split over more than one 256-page window of its own (NS 8 over 2,100 pages: 263 pages
-    per split) ending in a 13-token partial page, taken by the last wave of the last workgroup."""
-    torch.manual_seed(bits)
-    B, H, G, D, N, ns = 1, 2, 4, 128, 32 * 2100 + 13, 8
+@pytest.mark.parametrize("bits,ns,kw", [(4, 8, "1"), (8, 8, "1"), (4, 16, "2"), (8, 32, "4")])
+def test_two_windows_per_wave_then_partial_page(bits, ns, kw, monkeypatch):
+    """A wave's pages over more than one 256-page window of its own (NS 8 over 2,100 pages: 263 pages
+    per split; NS 16 or 32 with 2 or 4 splits per wave: 264 pages per wave, split boundaries inside a
+    window and across the window edge) ending in a 13-token partial page, taken by the last wave of
+    the last workgroup."""
+    monkeypatch.setenv("KUSHKASH_AMD_SPLITS_PER_WAVE", kw)
+    torch.manual_seed(bits + ns)
+    B, H, G, D, N = 1, 2, 4, 128, 32 * 2100 + 13
     c = kk.KushCache(1, H, H * G, D, batch_size=B, bits=bits, device=DEV, dtype=torch.bfloat16, rotate=False)
     K = torch.randn(B, H, N, D, device=DEV, dtype=torch.bfloat16)
     c.write(0, K, K.flip(2))
@@ -91,14 +100,16 @@ def test_two_windows_per_wave_then_partial_page(bits, monkeypatch):
 
 
 @pytest.mark.parametrize("rot", [False, True])
-@pytest.mark.parametrize("ns", [8, 16])
+@pytest.mark.parametrize("ns,kw", [(8, "1"), (16, "1"), (16, "2"), (16, "4")])
 @pytest.mark.parametrize("D,bits,G,dtype", [(128, 4, 7, torch.bfloat16), (128, 8, 4, torch.float16),
                                             (256, 4, 2, torch.float32)])
-def test_fused_append_then_decode(D, bits, G, dtype, ns, rot, monkeypatch):
+def test_fused_append_then_decode(D, bits, G, dtype, ns, kw, rot, monkeypatch):
     """The fused append + decode with wave splits (the workgroup holding the split of the page a
-    token completes writes it), rotation folded in or not: the same records, K tails and outputs as
-    the append followed by the decode."""
+    token completes writes it; with kw splits per wave, the workgroup holding that split among its
+    4 kw), rotation folded in or not: the same records, K tails and outputs as the append followed
+    by the decode."""
     monkeypatch.setenv("KUSHKASH_AMD_WAVE_SPLITS", "1")
+    monkeypatch.setenv("KUSHKASH_AMD_SPLITS_PER_WAVE", kw)
     fused_append_case(D, bits, G, dtype, ns, 4, True, rot, monkeypatch)
 
 
