@@ -106,11 +106,13 @@ def parse_args(argv=None):
     ap.add_argument("--graph-replay", action="store_true",
                     help="time the steps as replays of one-step HIP graphs (the reference's method) instead of "
                          "recorded launches")
-    ap.add_argument("--floor", default="", metavar="MODE:WAVES:DEPTH[:Z],...",
+    ap.add_argument("--floor", default="", metavar="MODE:WAVES:DEPTH[:Z[:PW]],...",
                     help="c2: after the decode line, time the decode's streaming floor (libkushfloor.so: the same "
                          "records and block tables, no attention math) in each listed launch shape -- mode 0 the "
                          "decode's grid (sequence, kv head), mode 1 a grid (sequence, Z) over every kv head of a "
-                         "page range; WAVES per workgroup; DEPTH page pairs in flight per wave (2: the decode's ring)")
+                         "page range, mode 2 a persistent grid of Z workgroups claiming chunks of 2 WAVES PW pages "
+                         "of a (sequence, kv head) from a device counter (balanced across XCDs); WAVES per "
+                         "workgroup; DEPTH page pairs in flight per wave (2: the decode's ring)")
     ap.add_argument("--floor-timeline", type=int, default=0, metavar="N",
                     help="with --floor: also print N launches of each floor shape by XCD (per-workgroup wall clocks)")
     ap.add_argument("--traffic", default=str(ROOT / "profiles" / "decode_c2_traffic.md"),
@@ -855,58 +857,78 @@ def bench_timeline(a) -> None:
                       f"{pct(us[m, 3], 50):.2f} / {us[m, 3].max():.2f} | {pct(mhz[m], 50):.0f} |", flush=True)
 
 
-def _floor_fn():
-    """kush_floor_stream of the measurement library (kushkash_amd/csrc/kush_floor.hip)."""
+def _floor_fn(name: str = "kush_floor_stream"):
+    """kush_floor_stream / kush_floor_dynamic of the measurement library (kushkash_amd/csrc/kush_floor.hip)."""
     import ctypes
     import importlib
     kbuild = importlib.import_module("kushkash_amd.build")
     if not kbuild.FLOOR_LIB.exists():
         raise SystemExit(f"--floor: {kbuild.FLOOR_LIB.name} is not built; run `python -m kushkash_amd.build`")
-    fn = ctypes.CDLL(str(kbuild.FLOOR_LIB)).kush_floor_stream
-    P, I32, I64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
-    fn.argtypes = [I32, I32, P, I64, I64, P, P, I64, I32, I32, I32, I32, I32, I32, I32, P, P, P]
+    fn = getattr(ctypes.CDLL(str(kbuild.FLOOR_LIB)), name)
+    P, I32, I64, U32 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32
+    if name == "kush_floor_stream":
+        fn.argtypes = [I32, I32, P, I64, I64, P, P, I64, I32, I32, I32, I32, I32, I32, I32, P, P, P]
+    else:
+        fn.argtypes = [I32, I32, P, I64, I64, P, P, I64, I32, I32, I32, I32, I32, I32, I32, P, U32, P, P, P]
     fn.restype = I32
     return fn
 
 
 class FloorLaunches:
     """The decode's streaming floor over the workload's pools, step i on pool i % pools, in one launch
-    shape (mode, waves, depth, z); run() has the interface of Launches.run, so time_launches times it
-    the way it times the decode."""
+    shape (mode, waves, depth, z[, pw]); run() has the interface of Launches.run, so time_launches times
+    it the way it times the decode. Mode 2 (dynamic chunks) keeps one device counter, zeroed once; launch
+    k passes base k x n_chunks (each launch makes exactly n_chunks claims)."""
 
-    def __init__(self, w, mode: int, waves: int, depth: int, z: int, marks: bool = False):
-        self.fn = _floor_fn()
+    def __init__(self, w, mode: int, waves: int, depth: int, z: int, pw: int = 4, marks: bool = False):
         cache, B, Hkv, pages = w["cache"], w["B"], w["Hkv"], w["pages"]
-        self.wgs = B * (z if mode == 1 else Hkv)
+        self.mode = mode
+        self.wgs = B * (z if mode == 1 else Hkv) if mode != 2 else z
         self.sums = torch.empty(self.wgs * waves * 64, dtype=torch.int32, device=cache.device)
         self.marks = torch.zeros(self.wgs, 8, dtype=torch.int64, device=cache.device) if marks else None
         stream = torch.cuda.current_stream().cuda_stream
-        self.args = [(w["D"], w["bits"], cache.data_ptr(), cache.stride(0), cache.stride(1), t.data_ptr(),
-                      w["seq_lens"].data_ptr(), t.stride(0), Hkv, B, pages, mode, z, waves, depth,
-                      self.sums.data_ptr(), None if self.marks is None else self.marks.data_ptr(), stream)
-                     for t in w["tables"]]
-        if self.fn(*self.args[0]) != 0:
-            raise SystemExit(f"--floor: no floor kernel for mode {mode}, {waves} waves, depth {depth}, z {z}")
+        mk = None if self.marks is None else self.marks.data_ptr()
+        if mode == 2:
+            self.fn = _floor_fn("kush_floor_dynamic")
+            self.ctr = torch.zeros(1, dtype=torch.int32, device=cache.device)
+            cp = 2 * waves * pw
+            self.n_chunks = B * Hkv * ((pages + cp - 1) // cp)
+            self.launches = 0
+            self.args = [[w["D"], w["bits"], cache.data_ptr(), cache.stride(0), cache.stride(1), t.data_ptr(),
+                          w["seq_lens"].data_ptr(), t.stride(0), Hkv, B, pages, z, waves, depth, pw,
+                          self.ctr.data_ptr(), 0, self.sums.data_ptr(), mk, stream] for t in w["tables"]]
+        else:
+            self.fn = _floor_fn()
+            self.args = [[w["D"], w["bits"], cache.data_ptr(), cache.stride(0), cache.stride(1), t.data_ptr(),
+                          w["seq_lens"].data_ptr(), t.stride(0), Hkv, B, pages, mode, z, waves, depth,
+                          self.sums.data_ptr(), mk, stream] for t in w["tables"]]
+        self.run(0, 1)
+        torch.cuda.synchronize()
 
     def run(self, first: int, n: int) -> None:
         for i in range(first, first + n):
-            if self.fn(*self.args[i % len(self.args)]) != 0:
-                raise RuntimeError("bench: kush_floor_stream failed")
+            args = self.args[i % len(self.args)]
+            if self.mode == 2:
+                args[16] = (self.launches * self.n_chunks) & 0xFFFFFFFF
+                self.launches += 1
+            rc = self.fn(*args)
+            if rc != 0:
+                raise SystemExit(f"--floor: the floor kernel refused or failed ({rc}) for mode {self.mode}")
 
 
 def floor_shapes(spec: str):
     for item in [x for x in spec.split(",") if x.strip()]:
         v = [int(x) for x in item.split(":")]
-        if len(v) not in (3, 4):
-            raise SystemExit(f"--floor: '{item}' is not MODE:WAVES:DEPTH[:Z]")
-        yield v[0], v[1], v[2], (v[3] if len(v) == 4 else 1)
+        if len(v) not in (3, 4, 5):
+            raise SystemExit(f"--floor: '{item}' is not MODE:WAVES:DEPTH[:Z[:PW]]")
+        yield v[0], v[1], v[2], (v[3] if len(v) >= 4 else 1), (v[4] if len(v) == 5 else 4)
 
 
 def floor_timeline(w, shape, reps: int, warmup: int) -> None:
     """Per-workgroup wall clocks of one floor launch (after `warmup` untimed ones), by XCD, as markdown."""
     import numpy as np
-    mode, wv, depth, z = shape
-    fl = FloorLaunches(w, mode, wv, depth, z, marks=True)
+    mode, wv, depth, z, pw = shape
+    fl = FloorLaunches(w, mode, wv, depth, z, pw, marks=True)
     for rep in range(reps):
         fl.run(0, warmup)
         torch.cuda.synchronize()
@@ -919,17 +941,20 @@ def floor_timeline(w, shape, reps: int, warmup: int) -> None:
         loop = us[:, 3] - us[:, 2]
         pct = lambda x, p: float(np.percentile(x, p))
         print(f"\nfloor mode {mode}, {wv} waves, depth {depth}" + (f", z {z}" if mode == 1 else "")
+              + (f", {z} workgroups, chunks of {2 * wv * pw} pages" if mode == 2 else "")
               + f": launch {rep + 1} of {reps}, first workgroup start -> last pages done {us[:, 3].max():.2f} us\n\n"
               "| phase (us from the first start) | min | p10 | p50 | p90 | max |\n|---|---|---|---|---|---|")
         for name, k in (("start", 0), ("first page DMAs issued", 1), ("first page pair landed", 2), ("pages done", 3)):
             x = us[:, k]
             print(f"| {name} | {x.min():.2f} | {pct(x, 10):.2f} | {pct(x, 50):.2f} | {pct(x, 90):.2f} | {x.max():.2f} |")
-        print("\n| XCD | workgroups | page loop p10 / p50 / max (us) | pages done p50 / max (us) |\n|---|---|---|---|")
+        print("\n| XCD | workgroups | page loop p10 / p50 / max (us) | pages done p50 / max (us) |"
+              + (" chunks |\n|---|---|---|---|---|" if mode == 2 else "\n|---|---|---|---|"))
         for x in range(8):
             m = xcd == x
             if m.any():
                 print(f"| {x} | {int(m.sum())} | {pct(loop[m], 10):.2f} / {pct(loop[m], 50):.2f} / {loop[m].max():.2f} | "
-                      f"{pct(us[m, 3], 50):.2f} / {us[m, 3].max():.2f} |", flush=True)
+                      f"{pct(us[m, 3], 50):.2f} / {us[m, 3].max():.2f} |"
+                      + (f" {int(t[m, 5].sum())} |" if mode == 2 else ""), flush=True)
 
 
 def main(argv=None):
@@ -1007,16 +1032,19 @@ def main(argv=None):
         res["cpu_baseline"] = cpu_baseline(w, a.cpu_seconds)
     print(json.dumps(res), flush=True)
 
-    for mode, fwv, depth, z in floor_shapes(a.floor):              # the streaming floor, a line each
-        fms = time_launches(FloorLaunches(w, mode, fwv, depth, z), a.steps, a.warmup)
+    for mode, fwv, depth, z, pw in floor_shapes(a.floor):          # the streaming floor, a line each
+        fms = time_launches(FloorLaunches(w, mode, fwv, depth, z, pw), a.steps, a.warmup)
         rec = w["B"] * w["Hkv"] * (w["N"] // PAGE) * w["RB"]
-        print(json.dumps({"floor": {"mode": mode, "waves": fwv, "depth": depth, "z": z if mode == 1 else None},
-                          "kernel": f"kush_floor_stream (floor_kernel<{a.dim}, {a.bits}, {fwv}, {depth}>)",
+        kname = (f"kush_floor_stream (floor_kernel<{a.dim}, {a.bits}, {fwv}, {depth}>)" if mode != 2 else
+                 f"kush_floor_dynamic (floor_dyn_kernel<{a.dim}, {a.bits}, {fwv}, {depth}, {pw}>)")
+        print(json.dumps({"floor": {"mode": mode, "waves": fwv, "depth": depth, "z": z if mode else None,
+                                    "chunk_pages": 2 * fwv * pw if mode == 2 else None},
+                          "kernel": kname,
                           "us_per_step": round(fms * 1e3, 2), "records_GBps": round(rec / fms / 1e6, 1),
                           "pct_peak_hbm": round(100 * alg / fms / 1e6 / PEAK_HBM_GBS, 1),
                           "decode_us_per_step": round(ms * 1e3, 2)}), flush=True)
         if a.floor_timeline:
-            floor_timeline(w, (mode, fwv, depth, z), a.floor_timeline, min(a.warmup, 200))
+            floor_timeline(w, (mode, fwv, depth, z, pw), a.floor_timeline, min(a.warmup, 200))
 
     for item in [x for x in a.sweep.split(",") if x.strip()]:     # other launch shapes, a line each
         sns, swv = (int(v) for v in item.split(":"))

@@ -102,6 +102,146 @@ __global__ __launch_bounds__(NW * WAVE) void floor_kernel(const uint8_t* __restr
     }
 }
 
+// Dynamic chunks (mode 2): the same stream, balanced across the XCDs. Every (sequence, kv head) is cut
+// into fixed chunks of CP = 2 NW PW pages, numbered c = (s CPS + k) H + h (k: chunk k of the head's
+// CPS). A persistent grid of P workgroups takes chunk blockIdx.x first and then claims chunks from a
+// device counter one chunk ahead, so a workgroup on a fast XCD takes more of them; the waves' rings
+// run on from one chunk into the next without draining. Wave w streams pairs w, w + NW, .. of each
+// chunk (PW per chunk; past a sequence's full pages, empty issues). At pair PW - DEPTH - 1 of each
+// chunk, wave 0 publishes the chunk it claimed one chunk earlier in LDS (double-buffered by chunk
+// parity), one barrier, every wave loads that chunk's length and block ids (scalar loads through the
+// constant address space, which the compiler waits on by lgkmcnt, apart from the DMAs' vmcnt; in by
+// the lgkmcnt(0) after the next pair's LDS reads), and wave 0 claims the one after it. The two chunks in hand alternate between two register sets (the
+// loop body twice), so no id is copied while its load is in flight. Claim v returns P + v - base: a
+// launch makes exactly n_chunks claims (one past the end per workgroup), so the caller passes
+// base = launch index x n_chunks and never resets the counter; a claim outside [P, n_chunks) ends the
+// workgroup, and no workgroup takes more than n_chunks chunks.
+// The claim is a returning vector atomic in asm, outside the compiler's vmcnt accounting (a compiler
+// atomic would be waited on with vmcnt(0), draining the ring): it is complete once a DMA issued after
+// it has been waited on (vector memory returns in order), which the wait at the top of the next
+// chunk's publishing pair guarantees; its register is read only after that wait.
+template <int D, int BITS, int NW, int DEPTH, int PW>
+__global__ __launch_bounds__(NW * WAVE) void floor_dyn_kernel(const uint8_t* __restrict__ cache, int64_t bs, int64_t hs,
+                                                              const int32_t* __restrict__ block_table,
+                                                              const int32_t* __restrict__ seq_lens, int64_t bt_stride,
+                                                              int H, int CPS, int n_chunks, uint32_t* ctr, uint32_t base,
+                                                              uint32_t* __restrict__ sums, long long* __restrict__ marks) {
+    static_assert(PW > DEPTH && PW % DEPTH == 0, "a chunk holds whole rounds of the ring and one more pair");
+    using R = Ring<D, BITS>;
+    using cint = const __attribute__((address_space(4))) int32_t;
+    constexpr int CP = 2 * NW * PW, PUB = PW - DEPTH - 1;
+    constexpr int DSTRIDE = 2 * NW * R::SLOT;
+    __shared__ __align__(16) uint8_t ring[DEPTH * DSTRIDE];
+    __shared__ int next_chunk[2];
+    const long long t_start = wall_clock64();
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+    uint32_t voff[R::DMA];
+#pragma unroll
+    for (int i = 0; i < R::DMA; ++i) voff[i] = src_chunk<D, BITS>(R::chunk0(i) + lane) * 16u;
+    uint8_t* const mine = ring + 2 * w * R::SLOT;
+
+    // the wave's PW pairs of a chunk: the sequence's length, the wave's first page, block ids
+    struct Pairs {
+        int n, pg0, a[PW], b[PW];
+        const uint8_t* head;
+    };
+    const auto load_pairs = [&](int c, Pairs& p) {
+        const int h = c % H, k = (c / H) % CPS, s = c / (H * CPS);
+        cint* const bt = (cint*)(block_table + (int64_t)s * bt_stride + k * CP + 2 * w);
+        p.head = cache + (int64_t)h * hs;
+        p.pg0 = k * CP + 2 * w;
+        p.n = ((cint*)seq_lens)[s];
+#pragma unroll
+        for (int i = 0; i < PW; ++i) {
+            p.a[i] = bt[2 * NW * i];
+            p.b[i] = bt[2 * NW * i + 1];
+        }
+    };
+    const auto issue_pair = [&](uint8_t* dst, const Pairs& p, int i) {
+        const int pg = p.pg0 + 2 * NW * i;                 // page pg is full when (pg + 1) PAGE <= n
+        issue_page<D, BITS>(dst, (pg + 1) * PAGE <= p.n, p.a[i], p.head, bs, voff);
+        issue_page<D, BITS>(dst + R::SLOT, (pg + 2) * PAGE <= p.n, p.b[i], p.head, bs, voff);
+    };
+    const auto empty_pair = [&](uint8_t* dst) {
+        issue_page<D, BITS>(dst, false, 0, cache, bs, voff);
+        issue_page<D, BITS>(dst + R::SLOT, false, 0, cache, bs, voff);
+    };
+    uint32_t claim = 0;
+    const auto claim_next = [&]() {                  // wave 0, lane 0's returning atomic add
+        if (w == 0 && lane == 0) {
+            const uint32_t one = 1u;
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+            asm volatile("global_atomic_add %0, %1, %2, off sc0" : "=v"(claim) : "v"(ctr), "v"(one) : "memory");
+#pragma clang diagnostic pop
+        }
+    };
+
+    const int P = __builtin_amdgcn_readfirstlane((int)gridDim.x);
+    int chunks = 0;
+    uint32_t acc = 0;
+    long long t_first = 0;
+    // one chunk: consume its PW pairs, refilling the ring from `cur` and, past its end, from `nxt`
+    // (published and loaded at pair PUB); returns whether there is a next chunk
+    const auto run_chunk = [&](const Pairs& cur, Pairs& nxt, int parity) -> bool {
+        bool more = false;
+#pragma unroll
+        for (int i = 0; i < PW; ++i) {
+            KUSH_WAIT_VM((DEPTH - 1) * 2 * R::DMA);
+            if (chunks == 0 && i == 0) t_first = wall_clock64();
+            uint8_t* const sl = mine + (i % DEPTH) * DSTRIDE;
+            const u4 x = *reinterpret_cast<const u4*>(sl + 16 * lane);
+            const u4 y = *reinterpret_cast<const u4*>(sl + R::SLOT + 16 * lane);
+            acc ^= x[0] ^ x[1] ^ x[2] ^ x[3] ^ y[0] ^ y[1] ^ y[2] ^ y[3];
+            __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0): the slot's reads done
+            if (i == PUB) {                              // the next chunk: published, then claimed onward
+                if (w == 0 && lane == 0) {
+                    asm volatile("" : "+v"(claim));      // read only now, after the wait above
+                    next_chunk[parity] = (int)(claim - base) + P;
+                }
+                __syncthreads();
+                const int nx = __builtin_amdgcn_readfirstlane(next_chunk[parity]);
+                more = __builtin_amdgcn_readfirstlane(nx >= P && nx < n_chunks && chunks + 1 < n_chunks);
+                // loaded unconditionally (a valid chunk when there is none next), so no branch joins
+                // over the loads and nothing reads them before the next pair's lgkmcnt(0)
+                load_pairs(more ? nx : (int)blockIdx.x, nxt);
+                if (more) claim_next();
+            }
+            if (i + DEPTH < PW) issue_pair(sl, cur, i + DEPTH);
+            else if (more) issue_pair(sl, nxt, i + DEPTH - PW);
+            else empty_pair(sl);
+        }
+        ++chunks;
+        return more;
+    };
+
+    Pairs pa, pb;
+    load_pairs(blockIdx.x, pa);
+    claim_next();
+    const long long t_issue = wall_clock64();
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) issue_pair(mine + d * DSTRIDE, pa, d);
+    for (;;) {
+        if (!run_chunk(pa, pb, 0)) break;
+        if (!run_chunk(pb, pa, 1)) break;
+    }
+    KUSH_WAIT_VM(0);
+    const int wg = blockIdx.x;
+    sums[(int64_t)wg * NW * WAVE + threadIdx.x] = acc;
+    if (marks == nullptr) return;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        long long* const r = marks + (int64_t)wg * 8;
+        r[0] = t_start;
+        r[1] = t_issue;
+        r[2] = t_first;
+        r[3] = wall_clock64();
+        r[4] = __builtin_amdgcn_s_getreg((3 << 11) | 20);        // XCC_ID bits [3:0]
+        r[5] = chunks;
+    }
+}
+
 template <int D, int BITS, int NW, int DEPTH>
 constexpr bool floor_fits() {
     return DEPTH * 2 * NW * Ring<D, BITS>::SLOT + 4 * WIN + 8 * NW <= 160 * 1024 && 2 * DEPTH * Ring<D, BITS>::DMA <= 63;
@@ -134,7 +274,50 @@ int by_shape(int waves, int depth, dim3 grid, hipStream_t st, const void* cache,
     return -2;
 }
 
+template <int D, int BITS, int NW, int DEPTH, int PW>
+int launch_dyn(int P, hipStream_t st, const void* cache, int64_t bs, int64_t hs, const int32_t* bt, const int32_t* sl,
+               int64_t bt_stride, int H, int CPS, int n_chunks, uint32_t* ctr, uint32_t base, uint32_t* sums,
+               int64_t* marks) {
+    if constexpr (floor_fits<D, BITS, NW, DEPTH>()) {
+        floor_dyn_kernel<D, BITS, NW, DEPTH, PW><<<dim3(P), dim3(NW * WAVE), 0, st>>>(
+            (const uint8_t*)cache, bs, hs, bt, sl, bt_stride, H, CPS, n_chunks, ctr, base, sums, (long long*)marks);
+        return hipGetLastError() == hipSuccess ? 0 : -3;
+    } else {
+        return -2;
+    }
+}
+
 }  // namespace
+
+// Dynamic chunks of 2 waves pw pages (mode 2 above) on a persistent grid of P workgroups; ctr: one
+// uint32 the caller zeroes once, base = (launches so far) x n_chunks, n_chunks = n_seqs hkv
+// ceil(max_pages / chunk). Shapes: D 128, bits 4 or 8, waves 4 with depth 2 and pw 4 or 8, waves 8 with
+// depth 2 and pw 4; P <= n_chunks and the table's rows hold ceil(max_pages / chunk) chunks. Returns 0,
+// -2 for a shape or size it does not take, -3 for a launch error.
+extern "C" int kush_floor_dynamic(int head_dim, int bits, const void* cache, int64_t block_stride, int64_t head_stride,
+                                  const int32_t* block_table, const int32_t* seq_lens, int64_t bt_stride, int32_t hkv,
+                                  int32_t n_seqs, int32_t max_pages, int32_t P, int32_t waves, int32_t depth, int32_t pw,
+                                  uint32_t* ctr, uint32_t base, uint32_t* sums, int64_t* marks, void* stream) {
+    if (head_dim != 128 || (bits != 4 && bits != 8) || n_seqs <= 0 || hkv <= 0 || P <= 0 || depth != 2) return -2;
+    const int CP = 2 * waves * pw;
+    const int CPS = (max_pages + CP - 1) / CP;
+    const int64_t n_chunks = (int64_t)n_seqs * hkv * CPS;
+    if (CPS <= 0 || P > n_chunks || n_chunks >= (1 << 30) || (int64_t)CPS * CP > bt_stride) return -2;
+    if (((uintptr_t)cache | (uint64_t)block_stride | (uint64_t)head_stride) & 15) return -2;
+    hipStream_t st = (hipStream_t)stream;
+    const int nc = (int)n_chunks;
+#define KUSH_DYN(NW, PW)                                                                                      \
+    if (waves == NW && pw == PW)                                                                              \
+        return bits == 4 ? launch_dyn<128, 4, NW, 2, PW>(P, st, cache, block_stride, head_stride, block_table, \
+                                                         seq_lens, bt_stride, hkv, CPS, nc, ctr, base, sums, marks) \
+                         : launch_dyn<128, 8, NW, 2, PW>(P, st, cache, block_stride, head_stride, block_table, \
+                                                         seq_lens, bt_stride, hkv, CPS, nc, ctr, base, sums, marks);
+    KUSH_DYN(4, 4)
+    KUSH_DYN(4, 8)
+    KUSH_DYN(8, 4)
+#undef KUSH_DYN
+    return -2;
+}
 
 // sums: uint32 [workgroups][waves * 64]; marks: int64 [workgroups][8] or null. Returns 0, -2 for a
 // shape this library has no kernel for (D 128, bits 4 or 8, waves 4 with depth 2-4, waves 8 with
