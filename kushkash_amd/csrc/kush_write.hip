@@ -5,9 +5,8 @@
 //
 // Work split on CDNA4: a page task is one (page, kv head), of 256 threads for the append and of
 // 128 (D <= 128) or 256 threads for the chunk write, whose 256-thread workgroups take two
-// neighbouring kv heads of a page at D <= 128. A chunk's tasks start as fast as the dispatcher and
-// the CUs' registers allow (six such workgroups per CU at C4's 71 VGPRs), every task's row loads
-// issued before its first wait. The page quantizer itself (thread layout, K tile, rotation) is in
+// neighbouring kv heads of a page at D <= 128. A task's indices come in by scalar loads (two round
+// trips), and every task's row loads are issued before its first wait. The page quantizer itself (thread layout, K tile, rotation) is in
 // kush_page.h.
 #include "kush_page.h"
 
@@ -74,21 +73,26 @@ __global__ __launch_bounds__(256) void write_kernel(
     int64_t bs, int64_t hs, IN* __restrict__ tail_k, const int32_t* __restrict__ block_table, int64_t bt_stride, int H) {
     constexpr int TH = write_threads<D>(), TPB = write_tpb<D>();
     __shared__ __align__(16) uint8_t lds[TPB * tile_bytes<D, IN>()];
-    const int sub = (int)threadIdx.x / TH, tid = (int)threadIdx.x % TH;
-    const int64_t task = (int64_t)blockIdx.x * TPB + sub;
-    const bool live = task < (int64_t)n_jobs * H;      // a task past the end still passes the barriers
-    const int j = live ? (int)(task / H) : 0, h = live ? (int)(task % H) : 0;
-    const int s = job_seq[j];
-    const int ps = job_page[j] * PAGE;
-    const int q0 = qsl[s];
-    const int total = seq_lens[s];
-    const int ctx = total - (qsl[s + 1] - q0);
+    // the task's indices are wave-uniform (a task is whole waves): scalar loads, in two round trips --
+    // the job's sequence and page, then everything of the sequence at once (the empty asm statements
+    // take each group's values together, so no load waits for another of its group)
+    const int sub = __builtin_amdgcn_readfirstlane((int)threadIdx.x / TH), tid = (int)threadIdx.x % TH;
+    const int task = (int)blockIdx.x * TPB + sub;     // n_jobs H < 2^31 (checked by the entry point)
+    const bool live = task < n_jobs * H;              // a task past the end still passes the barriers
+    const int j = live ? task / H : 0, h = live ? task % H : 0;
+    int s = job_seq[j], pg = job_page[j];
+    asm volatile("" : "+s"(s), "+s"(pg));
+    int q0 = qsl[s], q1 = qsl[s + 1], total = seq_lens[s], ti = tail_idx[s];
+    int blk = block_table[(int64_t)s * bt_stride + pg];
+    asm volatile("" : "+s"(q0), "+s"(q1), "+s"(total), "+s"(ti), "+s"(blk));
+    const int ps = pg * PAGE;
+    const int ctx = total - (q1 - q0);
     const bool complete = ps + PAGE <= total;
-    IN* tail = tail_k + ((int64_t)tail_idx[s] * H + h) * PAGE * D;
+    IN* tail = tail_k + ((int64_t)ti * H + h) * PAGE * D;
     const int lo = ps > ctx ? ps : ctx;                     // first new position in the page
     const int64_t hoff = (int64_t)h * D;
     {
-        uint8_t* rec = cache + (int64_t)block_table[(int64_t)s * bt_stride + ps / PAGE] * bs + (int64_t)h * hs;
+        uint8_t* rec = cache + (int64_t)blk * bs + (int64_t)h * hs;
         const int hi = !live ? lo : (ps + PAGE < total ? ps + PAGE : total);
         int split = ctx - ps;                               // K rows before it come from the tail
         split = split < 0 ? 0 : (split > PAGE ? PAGE : split);
@@ -176,6 +180,8 @@ extern "C" int kush_write_ex(int head_dim, int bits, int dtype, const void* k, c
                              const int32_t* block_table, int64_t bt_stride, int32_t hkv, void* stream, int32_t rot) {
     if (n_jobs < 0 || hkv <= 0 || mode < 0 || mode > 2 || rot < 0 || rot > 1)
         return kush_fail(-2, "kush_write: bad n_jobs %d / hkv %d / mode %d / rot %d", n_jobs, hkv, mode, rot);
+    if ((int64_t)n_jobs * hkv >= (int64_t)1 << 31)
+        return kush_fail(-2, "kush_write: %d jobs x %d kv heads is 2^31 page tasks or more", n_jobs, hkv);
     return dispatch_shape(head_dim, bits, dtype, "kush_write", [&](auto dd, auto bb, auto in) -> int {
         constexpr int D = decltype(dd)::value, BITS = decltype(bb)::value;
         using IN = decltype(in);

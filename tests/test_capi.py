@@ -199,6 +199,8 @@ def test_combine_and_writes_reject_bad_arguments(lib):
     assert lib.kush_write_ex(*wr, -1) == -2
     wr[13] = 3
     assert lib.kush_write(*wr) == -2                                                     # mode 0, 1 or 2
+    wr[13], wr[12] = 2, 1 << 29
+    assert lib.kush_write(*wr) == -2                                 # 2^31 page tasks (jobs x kv heads) or more
 
 
 def test_ops_is_gpu_only():
