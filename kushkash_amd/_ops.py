@@ -1,9 +1,10 @@
 """Kernel launcher over the page-record layout, and the pure-torch helpers around it.
 
 Drop-in for the reference's ``kushkash/_ops.py``: ``Ops`` keeps its constructor, method names,
-argument meaning and error behaviour (``_ops.py:42-213``), but every method runs a hand-written
-gfx950 HIP kernel through the C ABI of ``libkushhip.so`` (include/kushkash_amd.h) on torch's
-current stream. The reference's torch helpers (record dequantization, attention with log-sum-exp,
+argument meaning and error behaviour (``_ops.py:42-213``). On a ROCm device every method runs a
+hand-written gfx950 HIP kernel through the C ABI of ``libkushhip.so`` (include/kushkash_amd.h) on
+torch's current stream; on device "cpu" it runs the host library ``libkushcpu.so`` (csrc/kush_cpu.cpp,
+the reference's CPU library's C ABI), fp32 tensors only, as the reference's CPU path. The reference's torch helpers (record dequantization, attention with log-sum-exp,
 rotation) are importable from here under their reference names; they live in _records, _attention
 and _rotation.
 
@@ -17,7 +18,6 @@ Tensor conventions (as the reference, ``_ops.py:6-15``)
   rotation    append / write / decode do not rotate: callers pass q H, k H, v H (rotate(), or
               Ops.fwht in the kernels' canonical order) and rotate back; unpack can rotate history back
 
-The CPU path of the reference (Mojo) is not part of this package: ``Ops`` runs on the GPU only.
 """
 from __future__ import annotations
 
@@ -97,33 +97,43 @@ def check_unpack_indices(page_blk: torch.Tensor, page_dst: torch.Tensor, tail_bl
 
 
 class Ops:
-    """Kernels for one (device, head_dim, bits, q heads per kv head, dtype); GPU only."""
+    """Kernels for one (device, head_dim, bits, q heads per kv head, dtype): the gfx950 library on a
+    ROCm device, the host library on device "cpu" (fp32; the reference's CPU path, _ops.py:49-57)."""
 
     def __init__(self, device: torch.device, head_dim: int, bits: int, group: int, dtype: torch.dtype,
                  *, validate: bool | None = None):
         device = torch.device(device)
-        if device.type != "cuda":
-            raise ValueError("kushkash_amd runs its kernels on the GPU (device 'cuda' under ROCm); the reference's "
-                             "CPU path is not part of this package")
+        if device.type not in ("cuda", "cpu"):
+            raise ValueError("kushkash_amd runs on the GPU (device 'cuda' under ROCm) or on the host (device 'cpu')")
+        where = "GPU" if device.type == "cuda" else "CPU"
         if head_dim not in (64, 128, 256):
-            raise ValueError("GPU head_dim must be 64, 128 or 256")
+            raise ValueError(f"{where} head_dim must be 64, 128 or 256")
         if bits not in (4, 8):
             raise ValueError("bits must be 4 or 8")
         if group < 1:
             raise ValueError("group must be >= 1")
         if dtype not in DTYPE_CODE:
             raise ValueError(f"dtype must be one of {tuple(DTYPE_CODE)}")
+        self.D, self.bits, self.G, self.dtype = head_dim, bits, group, dtype
+        self.validate = _validate_default() if validate is None else validate
+        self._dt = DTYPE_CODE[dtype]
+        if device.type == "cpu":
+            if dtype != torch.float32:
+                raise ValueError("the CPU path computes in fp32: its tensors (and dtype) are torch.float32")
+            from . import _cpu
+            self._cpu = _cpu
+            _cpu.lib()                                          # fail loudly now if it is not built
+            self.device, self.gpu, self.sms = torch.device("cpu"), False, 1
+            self.cfg = KernelConfig(head_dim, bits, group, "float32", arch="cpu", tensor_cores=False, warps=1)
+            return
         from . import _lib
         self._lib = _lib
         _lib.lib()                                              # fail loudly now if it is not built
         idx = device.index if device.index is not None else torch.cuda.current_device()
         self.device = torch.device("cuda", idx)
-        self.D, self.bits, self.G, self.dtype = head_dim, bits, group, dtype
         self.gpu = True
         self.sms = torch.cuda.get_device_properties(idx).multi_processor_count
         self.cfg = KernelConfig(head_dim, bits, group, str(dtype).split(".")[1])
-        self.validate = _validate_default() if validate is None else validate
-        self._dt = DTYPE_CODE[dtype]
         # counters of the fused split-K merge: zero at rest (the last workgroup of each (sequence, kv
         # head) resets its own), so one buffer serves every call of this Ops on one stream at a time
         self._sync = torch.zeros(SYNC_SLOTS, dtype=torch.int32, device=self.device)
@@ -132,7 +142,7 @@ class Ops:
     def _validating(self) -> bool:
         """Whether to check index values (validate on, and the stream not capturing a graph: the
         checks read values back to the host, which a capture does not allow)."""
-        return self.validate and not torch.cuda.is_current_stream_capturing()
+        return self.validate and (not self.gpu or not torch.cuda.is_current_stream_capturing())
 
     def _stream(self) -> int:
         return torch.cuda.current_stream(self.device).cuda_stream
@@ -206,6 +216,12 @@ class Ops:
             raise ValueError("seq_lens, tail_idx and block_table need one entry per sequence")
         self._check_values(cache, block_table, seq_lens, tail_idx, tail_k, S, extra=pos_offset + 1)
         bs, hs = _byte_strides(cache)
+        if not self.gpu:
+            _require(not rot, "append(rot=True) is a GPU extension; the CPU path takes rotated rows (fwht)")
+            self._cpu.call("kush_cpu_append", self.D, self.bits, k.data_ptr(), v.data_ptr(), k.stride(0), v.stride(0),
+                           seq_lens.data_ptr(), int(pos_offset), int(bool(advance)), cache.data_ptr(), bs, hs,
+                           tail_k.data_ptr(), tail_idx.data_ptr(), block_table.data_ptr(), block_table.stride(0), H, S)
+            return
         self._lib.call("kush_append_ex", self.D, self.bits, self._dt, k.data_ptr(), v.data_ptr(), k.stride(0),
                        v.stride(0), seq_lens.data_ptr(), int(pos_offset), int(bool(advance)), tail_idx.data_ptr(),
                        cache.data_ptr(), bs, hs, tail_k.data_ptr(), block_table.data_ptr(), block_table.stride(0),
@@ -248,6 +264,14 @@ class Ops:
                 _check_covers(query_start_loc, seq_lens, job_seq, job_page)
             self._check_values(cache, block_table, seq_lens, tail_idx, tail_k, S)
         bs, hs = _byte_strides(cache)
+        if not self.gpu:                                         # the two modes, in order, on the host
+            _require(not rot, "write(rot=True) is a GPU extension; the CPU path takes rotated rows (fwht)")
+            for mode in (0, 1):
+                self._cpu.call("kush_cpu_write", self.D, self.bits, k.data_ptr(), v.data_ptr(), k.stride(0),
+                               v.stride(0), query_start_loc.data_ptr(), seq_lens.data_ptr(), job_seq.data_ptr(),
+                               job_page.data_ptr(), n_jobs, mode, cache.data_ptr(), bs, hs, tail_k.data_ptr(),
+                               tail_idx.data_ptr(), block_table.data_ptr(), block_table.stride(0), H)
+            return
         for mode in ((2,) if fused else (0, 1)):
             self._lib.call("kush_write_ex", self.D, self.bits, self._dt, k.data_ptr(), v.data_ptr(), k.stride(0),
                            v.stride(0), query_start_loc.data_ptr(), seq_lens.data_ptr(), tail_idx.data_ptr(),
@@ -269,7 +293,11 @@ class Ops:
                  "fwht: out must be a contiguous tensor of x's shape and dtype")
         self._on_device(x=x, out=out)
         rows = x.numel() // D
-        if rows:
+        if rows and not self.gpu:                                # in place on the host
+            if out.data_ptr() != x.data_ptr():
+                out.copy_(x)
+            self._cpu.call("kush_cpu_fwht", D, out.data_ptr(), rows)
+        elif rows:
             self._lib.call("kush_fwht", D, self._dt, x.data_ptr(), out.data_ptr(), D, D, rows, self._stream())
         return out
 
@@ -311,6 +339,12 @@ class Ops:
         if self._validating():
             check_unpack_indices(page_blk, page_dst, tail_blk, tail_info, new_dst, kp.shape[0], cache.shape[0],
                                  tail_k.shape[0])
+        if not self.gpu:
+            self._cpu.call("kush_cpu_unpack", D, self.bits, cache.data_ptr(), bs, hs, H, page_blk.data_ptr(),
+                           page_dst.data_ptr(), n_pages, tail_blk.data_ptr(), tail_info.data_ptr(), n_tail,
+                           tail_k.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0), v_new.stride(0),
+                           new_dst.data_ptr(), n_new, kp.data_ptr(), vp.data_ptr(), int(bool(rot)))
+            return
         self._lib.call("kush_unpack", D, self.bits, self._dt, cache.data_ptr(), bs, hs, H, page_blk.data_ptr(),
                        page_dst.data_ptr(), n_pages, tail_blk.data_ptr(), tail_info.data_ptr(), n_tail,
                        tail_k.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0), v_new.stride(0),
@@ -323,6 +357,8 @@ class Ops:
         wave; at most 256. As in the reference (_ops.py:182-189) the grid stays small, so a work
         buffer of CUs * G * (D + 2) floats per (sequence, kv head) pair always suffices."""
         ns = 1
+        if not self.gpu:                                         # the host decode takes no splits (1 on CPU)
+            return ns
         while (ns < 256 and num_seqs * num_kv_heads * ns < self.sms
                and max_full_pages // (2 * ns) >= 2 * DECODE_WAVES):
             ns *= 2
@@ -379,7 +415,7 @@ class Ops:
             raise ValueError("k and v need one row per sequence")
         e = k.element_size()
         aligned = ((k.data_ptr() | v.data_ptr() | (k.stride(0) * e) | (v.stride(0) * e)) & 15) == 0
-        if self.G > 16 or not aligned:
+        if self.G > 16 or not aligned or not self.gpu:
             self.append(k, v, seq_lens, tail_idx, cache, block_table, tail_k, -1, False, rot=rot)
             self.decode(q, out, cache, block_table, seq_lens, tail_idx, tail_k, scale, n_splits, work, waves=waves,
                         order=order, rot=rot)
@@ -405,6 +441,13 @@ class Ops:
         if n_splits < 1:
             raise ValueError("n_splits must be >= 1")
         self._check_values(cache, block_table, seq_lens, tail_idx, tail_k, S)
+        if not self.gpu:                # one pass per (sequence, kv head): splits, work, waves, order unused
+            _require(not rot, "decode(rot=True) is a GPU extension; the CPU path takes a rotated q (fwht)")
+            bs, hs = _byte_strides(cache)
+            self._cpu.call("kush_cpu_decode", D, self.bits, q.data_ptr(), out.data_ptr(), cache.data_ptr(), bs, hs,
+                           tail_k.data_ptr(), tail_idx.data_ptr(), block_table.data_ptr(), seq_lens.data_ptr(),
+                           block_table.stride(0), H, G, float(scale), S)
+            return
         part_ml = part_o = None
         if n_splits > 1:
             nml = S * H * n_splits * G * 2

@@ -1,6 +1,7 @@
 """Ahead-of-time build of the gfx950 HIP library (replaces the reference's first-use Mojo build,
 kushkash/_build.py:215-254): csrc/*.hip compiled to objects in parallel (the decode instantiations
-once per input dtype and rot flag), then linked into kushkash_amd/libkushhip.so.
+once per input dtype and rot flag), then linked into kushkash_amd/libkushhip.so; beside it the CPU
+path's host library kushkash_amd/libkushcpu.so (csrc/kush_cpu.cpp, g++).
 
     python -m kushkash_amd.build
 """
@@ -27,6 +28,11 @@ TIMELINE_LIB = PKG / "libkushhip_timeline.so"
 # same records, launch shape and DMA ring as the decode without its math), loaded only by bench.py.
 FLOOR_LIB = PKG / "libkushfloor.so"
 FLOOR_SOURCE = "kush_floor.hip"
+# The host library of the package's CPU path (csrc/kush_cpu.cpp, g++ with OpenMP): Ops and KushCache on
+# device "cpu", the reference's CPU library's C ABI (kushkash/_cpu.py).
+CPU_LIB = PKG / "libkushcpu.so"
+CPU_SOURCE = "kush_cpu.cpp"
+CPU_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", "-fopenmp", "-ffp-contract=off"]
 SOURCES = ("kush_capi.hip", "kush_write.hip", "kush_decode.hip", "kush_rotate.hip",
            "kush_unpack.hip", "kush_decode_inst.hip")
 # the decode kernel instantiations: one object per (input dtype, rot)
@@ -118,7 +124,7 @@ def source_digest(unit: str | None = None) -> str:
         files = sorted(seen)
     for f in files:
         h.update(f.name.encode() + b"\0" + _code(f.read_text()).encode() + b"\0")
-    h.update(repr((FLAGS, units())).encode())
+    h.update(repr(CPU_FLAGS if unit == CPU_SOURCE else (FLAGS, units())).encode())
     return h.hexdigest()[:16]
 
 
@@ -146,15 +152,22 @@ def _run(cmd: list[str], verbose: bool) -> None:
     noise = "is not a recognized feature for this target"          # host pass: harmless
     err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{' '.join(cmd)}\n{err}")
+        raise RuntimeError(f"{Path(cmd[0]).name} failed ({res.returncode}):\n{' '.join(cmd)}\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
 
 
+def cxx() -> str:
+    for cand in (os.environ.get("CXX"), shutil.which("g++"), "/usr/bin/g++"):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("g++ not found (the CPU path's library is built with it)")
+
+
 def build(verbose: bool = False, jobs: int | None = None) -> Path:
     """Compile every HIP source for gfx950 into LIB, TIMELINE_LIB from the same objects with the
-    timeline unit instrumented, and the measurement library FLOOR_LIB (always recompiles; objects in
-    parallel, then the links); returns LIB."""
+    timeline unit instrumented, the measurement library FLOOR_LIB, and the CPU path's host library
+    CPU_LIB (always recompiles; objects in parallel, then the links); returns LIB."""
     todo = units() + [(FLOOR_SOURCE, {}), (TIMELINE_UNIT[0], dict(TIMELINE_UNIT[1], KUSH_TIMELINE=1))]
     jobs = jobs or max(1, min(len(todo), int(os.environ.get("MAX_JOBS", 0)) or os.cpu_count() or 1))
     compile_flags = [f for f in FLAGS if f != "-shared"]
@@ -165,8 +178,11 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
             objs.append(obj)
             cmds.append([hipcc(), *compile_flags, *(f"-D{k}={v}" for k, v in defs.items()), f"-I{ROOT / 'include'}",
                          "-c", str(PKG / "csrc" / src), "-o", obj])
+        cpu_tmp = CPU_LIB.with_suffix(".so.tmp")
+        cmds.append([cxx(), *CPU_FLAGS, "-o", str(cpu_tmp), str(PKG / "csrc" / CPU_SOURCE)])
         with ThreadPoolExecutor(jobs) as ex:
             list(ex.map(lambda c: _run(c, verbose), cmds))
+        os.replace(cpu_tmp, CPU_LIB)
         product = objs[:len(units())]
         swap = units().index(TIMELINE_UNIT)
         timeline = product[:swap] + objs[-1:] + product[swap + 1:]
@@ -175,7 +191,8 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
             _run([hipcc(), *FLAGS, "-o", str(tmp), *parts], verbose)
             os.replace(tmp, dst)
     import json
-    DIGEST.write_text(json.dumps({"all": source_digest(), **{u: source_digest(u) for u in SOURCES + (FLOOR_SOURCE,)}},
+    DIGEST.write_text(json.dumps({"all": source_digest(),
+                                  **{u: source_digest(u) for u in SOURCES + (FLOOR_SOURCE, CPU_SOURCE)}},
                                  indent=1) + "\n")
     return LIB
 

@@ -59,7 +59,8 @@ class KushCache:
         num_layers, num_kv_heads, num_q_heads, head_dim: the model's attention shape.
         batch_size: sequences per batch; they advance together.
         bits: 4 or 8.
-        device: the ROCm device ("cuda[:i]").
+        device: the ROCm device ("cuda[:i]"), or "cpu" for the host library (fp32 kernels and tails; q,
+            k, v in `dtype` are converted), as the reference's CPU path.
         dtype: dtype of q, k, v handed in and of the attention output.
         max_length: per-sequence capacity to reserve up front (the pool grows on demand otherwise).
         scale: softmax scale (default 1 / sqrt(head_dim)).
@@ -93,6 +94,8 @@ class KushCache:
         self.kdtype = dtype if self.gpu else torch.float32        # what the kernels and the tails hold
         self.ops = Ops(device, head_dim, bits, self.G, self.kdtype)
         self.rot = hadamard(head_dim, device) if rotation_enabled(bits, rotate) else None
+        if rotate_in_kernels and not self.gpu:
+            raise ValueError("rotate_in_kernels is for the GPU kernels; on the CPU the cache rotates with torch")
         self.krot = self.rot is not None and bool(rotate_in_kernels)
         self.profile: list | None = None                          # a list: attend_chunk records event pairs
         self.tail_k = torch.zeros(num_layers, batch_size, num_kv_heads, PAGE, head_dim, dtype=self.kdtype,

@@ -203,12 +203,15 @@ def test_combine_and_writes_reject_bad_arguments(lib):
     assert lib.kush_write(*wr) == -2                                 # 2^31 page tasks (jobs x kv heads) or more
 
 
-def test_ops_is_gpu_only():
-    """No CPU fallback: the product's Ops refuses a CPU device (the oracle lives under tests' reach only)."""
-    with pytest.raises(ValueError, match="GPU"):
+def test_ops_devices():
+    """Ops runs on a ROCm device or on the host (its own CPU library, fp32 as the reference's CPU path;
+    never the oracle, which lives under the tests' reach only); any other device is refused."""
+    with pytest.raises(ValueError, match="GPU .* or on the host"):
+        kushkash_amd.Ops(torch.device("meta"), 128, 4, 7, torch.float32)
+    with pytest.raises(ValueError, match="fp32"):
         kushkash_amd.Ops(torch.device("cpu"), 128, 4, 7, torch.bfloat16)
-    with pytest.raises(ValueError):
-        kushkash_amd.KushCache(1, 4, 28, 128, device="cpu", dtype=torch.float32)
+    ops = kushkash_amd.Ops(torch.device("cpu"), 128, 4, 7, torch.float32)
+    assert ops._cpu.LIB.name == "libkushcpu.so" and ops._cpu.LIB.parent == Path(kushkash_amd.__file__).parent
 
 
 def test_package_does_not_import_the_oracle():
@@ -217,4 +220,9 @@ def test_package_does_not_import_the_oracle():
     for f in list(pkg.rglob("*.py")) + list(pkg.rglob("*.hip")) + list(pkg.rglob("*.h")):
         src = f.read_text()
         assert not re.search(r"^\s*(from|import)\s+oracle\b", src, re.M), f
-        assert "libkush_oracle" not in src and "kush_cpu_" not in src, f
+        assert "libkush_oracle" not in src and "kush_oracle" not in src, f
+    # the CPU path's entry points keep the reference's CPU names (kush_cpu_*): the package binds them
+    # from its own host library, built from csrc/kush_cpu.cpp, never from the oracle's
+    from kushkash_amd import _cpu
+    assert Path(_cpu.lib()._name).resolve() == pkg / "libkushcpu.so"
+    assert _cpu.LIB == pkg / "libkushcpu.so"

@@ -3,6 +3,7 @@ errors, and the reference's CPU tests of the transformers integration (tests/tes
 with the KushCache running on the CPU oracle (the C restatement of the reference's CPU kernels) in
 place of the GPU kernels, so what is tested here is hf.py's host logic. The same tests on the GPU
 kernels are in test_gpu_hf.py."""
+import contextlib
 from types import SimpleNamespace
 
 import pytest
@@ -104,11 +105,29 @@ def test_cache_layer_surface():
             call()
 
 
-def test_gpu_only_outside_tests():
-    """Without the oracle stand-in the cache runs on the GPU only: a CPU model fails loudly."""
+def test_cpu_model_runs_on_the_package_cpu_path():
+    """Without the oracle stand-in a CPU model runs on the package's own CPU library (libkushcpu.so):
+    prefill and 12 decode steps give the logits of the oracle-backed run (kushkash/cache.py:72-78: the
+    reference's CPU path), within fp32 summation order."""
     model = kk.enable(_tiny("llama"))
-    with pytest.raises(ValueError, match="GPU"):
-        model(torch.randint(0, 256, (1, 8)), past_key_values=kk.KushHFCache(model.config), use_cache=True)
+    ids = torch.randint(0, 256, (2, 40))
+    runs = []
+    with torch.no_grad():
+        for backend in (None, oracle_backend):
+            out = []
+            with (backend() if backend else contextlib.nullcontext()):
+                cache = kk.KushHFCache(model.config, bits=4)
+                logits = model(ids, past_key_values=cache, use_cache=True).logits
+                out.append(logits)
+                nxt = logits[:, -1:].argmax(-1)
+                for _ in range(12):
+                    logits = model(nxt, past_key_values=cache, use_cache=True).logits
+                    out.append(logits)
+                    nxt = logits.argmax(-1)
+            runs.append(torch.cat(out, 1))
+            if backend is None:
+                assert type(cache.kv.ops) is kk.Ops and not cache.kv.ops.gpu     # the package's own CPU path
+    assert torch.allclose(runs[0], runs[1], rtol=1e-4, atol=1e-4)
 
 
 @pytest.mark.parametrize("kind", ["llama", "qwen2"])
