@@ -11,25 +11,22 @@ from pathlib import Path
 
 LIB = Path(__file__).resolve().parent / "libkushcpu.so"
 
-_I, _F = ctypes.c_int64, ctypes.c_float
-SIGNATURES = {
-    # d, bits, k, v, k_stride, v_stride, seq_lens, pos_offset, advance, cache, block_stride, head_stride,
-    # tail_k, tail_idx, block_table, bt_row_stride, hkv, n_seqs
-    "kush_cpu_append": [_I] * 18,
-    # d, bits, k, v, k_stride, v_stride, query_start_loc, seq_lens, job_seq, job_page, n_jobs, mode, cache,
-    # block_stride, head_stride, tail_k, tail_idx, block_table, bt_row_stride, hkv
-    "kush_cpu_write": [_I] * 20,
-    # d, bits, q, out, cache, block_stride, head_stride, tail_k, tail_idx, block_table, seq_lens,
-    # bt_row_stride, hkv, group, scale, n_seqs
-    "kush_cpu_decode": [_I] * 14 + [_F, _I],
-    # d, x, rows
-    "kush_cpu_fwht": [_I] * 3,
-    # d, bits, cache, block_stride, head_stride, hkv, page_blk, page_dst, n_pages, tail_blk, tail_info, n_tail,
-    # tail_k, k_new, v_new, k_stride, v_stride, new_dst, n_new, kp, vp, rot
-    "kush_cpu_unpack": [_I] * 22,
-    # x, out, n: fp32 -> fp16 bits with the library's rounding (tests)
-    "kush_cpu_half_bits": [_I] * 3,
+# Each entry point's parameters by name, in order, as include/kushkash_amd_cpu.h declares them: int64
+# (an address, stride or count) except the float softmax scale.
+PARAMS = {
+    "kush_cpu_append": "head_dim bits k v k_row_stride v_row_stride seq_lens pos_offset advance cache "
+                       "block_stride head_stride tail_k tail_idx block_table bt_row_stride hkv n_seqs",
+    "kush_cpu_write": "head_dim bits k v k_row_stride v_row_stride query_start_loc seq_lens job_seq job_page "
+                      "n_jobs mode cache block_stride head_stride tail_k tail_idx block_table bt_row_stride hkv",
+    "kush_cpu_decode": "head_dim bits q out cache block_stride head_stride tail_k tail_idx block_table seq_lens "
+                       "bt_row_stride hkv group scale n_seqs",
+    "kush_cpu_fwht": "head_dim x rows",
+    "kush_cpu_unpack": "head_dim bits cache block_stride head_stride hkv page_blk page_dst n_pages tail_blk "
+                       "tail_info n_tail tail_k k_new v_new k_row_stride v_row_stride new_dst n_new kp vp rot",
+    "kush_cpu_half_bits": "x out n",          # fp32 -> fp16 bits with the library's rounding (tests)
 }
+SIGNATURES = {name: [ctypes.c_float if p == "scale" else ctypes.c_int64 for p in params.split()]
+              for name, params in PARAMS.items()}
 
 
 @lru_cache(None)

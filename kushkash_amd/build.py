@@ -179,7 +179,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
             cmds.append([hipcc(), *compile_flags, *(f"-D{k}={v}" for k, v in defs.items()), f"-I{ROOT / 'include'}",
                          "-c", str(PKG / "csrc" / src), "-o", obj])
         cpu_tmp = CPU_LIB.with_suffix(".so.tmp")
-        cmds.append([cxx(), *CPU_FLAGS, "-o", str(cpu_tmp), str(PKG / "csrc" / CPU_SOURCE)])
+        cmds.append([cxx(), *CPU_FLAGS, f"-I{ROOT / 'include'}", "-o", str(cpu_tmp), str(PKG / "csrc" / CPU_SOURCE)])
         with ThreadPoolExecutor(jobs) as ex:
             list(ex.map(lambda c: _run(c, verbose), cmds))
         os.replace(cpu_tmp, CPU_LIB)

@@ -21,6 +21,8 @@
 #include <type_traits>
 #include <vector>
 
+#include "kushkash_amd_cpu.h"
+
 namespace {
 
 using i64 = int64_t;
@@ -437,7 +439,7 @@ Cache make_cache(i64 cache, i64 bs, i64 hs, i64 tail_k, i64 tail_idx, i64 table,
 
 }  // namespace
 
-// ------------------------------------------------------------------ C ABI (kushkash/_cpu.py:10-25)
+// ------------------------------------------------------------------ C ABI (kushkash_amd_cpu.h; kushkash/_cpu.py:10-25)
 extern "C" {
 
 // d, bits, k, v, k_stride, v_stride, seq_lens, pos_offset, advance, cache, block_stride, head_stride,

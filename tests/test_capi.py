@@ -22,11 +22,11 @@ def lib():
     return _lib.lib()
 
 
-def header_params() -> dict[str, list[str]]:
+def header_params(header: Path = HEADER) -> dict[str, list[str]]:
     """name -> parameter declarations (type and name) of every function declared in the header."""
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
     out = {}
-    for m in re.finditer(r"\b(?:int|const char\s*\*)\s*(kush_\w+)\s*\(([^)]*)\)\s*;", text):
+    for m in re.finditer(r"\b(?:int|int32_t|const char\s*\*)\s*(kush_\w+)\s*\(([^)]*)\)\s*;", text):
         params = m.group(2).strip()
         out[m.group(1)] = [] if params in ("", "void") else [" ".join(x.split()) for x in params.split(",")]
     return out
@@ -86,6 +86,27 @@ def test_library_exports_every_header_symbol(lib):
         assert hasattr(raw, name), name
         assert len(_lib.SIGNATURES[name]) == n, (name, n, len(_lib.SIGNATURES[name]))
     assert set(_lib.SIGNATURES) == set(header_functions())
+
+
+def test_cpu_library_exports_every_cpu_header_symbol():
+    """libkushcpu.so (the CPU path) exports what include/kushkash_amd_cpu.h declares, with the parameter
+    names and types its binding uses: the reference's CPU ABI (kush/cpu.mojo:476-562) plus one
+    test hook, every argument int64 except the decode's float scale, int32 results."""
+    from kushkash_amd import _cpu
+    if not _cpu.LIB.exists():
+        kushkash_amd.build()
+    params = header_params(HEADER.parent / "kushkash_amd_cpu.h")
+    assert set(params) == set(_cpu.PARAMS) == {"kush_cpu_append", "kush_cpu_write", "kush_cpu_decode",
+                                               "kush_cpu_fwht", "kush_cpu_unpack", "kush_cpu_half_bits"}
+    raw = ctypes.CDLL(str(_cpu.LIB))
+    for name, decl in params.items():
+        assert _names(decl) == _cpu.PARAMS[name].split(), name
+        assert [p.split()[0] for p in decl] == ["float" if p.endswith(" scale") else "int64_t" for p in decl], name
+        assert hasattr(raw, name), name
+    # the reference's argument counts (kushkash/_cpu.py:10-25): 18, 20, 16, 3, 22
+    assert [len(_cpu.SIGNATURES[n]) for n in ("kush_cpu_append", "kush_cpu_write", "kush_cpu_decode",
+                                               "kush_cpu_fwht", "kush_cpu_unpack")] == [18, 20, 16, 3, 22]
+    assert _cpu.SIGNATURES["kush_cpu_decode"][14] is ctypes.c_float
 
 
 def test_timeline_build_is_the_library_plus_its_reader(lib):

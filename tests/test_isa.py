@@ -70,3 +70,18 @@ def test_every_lds_load_is_ours(asm):
             if ins.endswith(" lds") or "_lds_" in ins:
                 prev = [l for l in lines[:i] if l][-1]
                 assert prev.startswith("s_mov_b32 m0,"), (name, prev, ins)
+
+
+def test_split_merge_is_device_scope_accesses_without_cache_maintenance(asm):
+    """The fused split-K merge communicates only through device-scope accesses: partials stored
+    write-through (`global_store ... sc1`), one returning atomic add per workgroup on the split
+    counter, partials read back past the local L2 (`global_load ... sc1`), and no L2 write-back or
+    invalidate anywhere (no `buffer_wbl2` / `buffer_inv`, which a release / acquire would add)."""
+    for name, lines in kernels(asm).items():
+        assert not [l for l in lines if re.match(r"(buffer_wbl2|buffer_inv|buffer_wbinvl1)", l)], name
+        atomics = [l for l in lines if l.startswith("global_atomic")]
+        assert atomics, name                                        # every variant carries the merge
+        for a in atomics:
+            assert re.match(r"global_atomic_add v\d+, v\d+, v\d+, s\[\d+:\d+\] sc0$", a), (name, a)
+        assert any(l.startswith("global_store") and l.endswith(" sc1") for l in lines), name
+        assert any(l.startswith("global_load") and l.endswith(" sc1") for l in lines), name
