@@ -164,6 +164,23 @@ void read_codes(const uint8_t* rec, bool v, int n, float* out) {
     }
 }
 
+// A full page's K codes by dimension: out[d * PAGE + t] (the scores then run over 32 tokens at a time)
+template <int D, int BITS>
+void read_k_codes_by_dim(const uint8_t* rec, float* out) {
+    using R = Rec<D, BITS>;
+    const int8_t* c = reinterpret_cast<const int8_t*>(rec);
+    for (int t = 0; t < PAGE; ++t, c += R::DC) {
+        if constexpr (BITS == 8) {
+            for (int d = 0; d < D; ++d) out[d * PAGE + t] = (float)c[d];
+        } else {
+            for (int j = 0; j < D / 2; ++j) {
+                out[j * PAGE + t] = (float)(int8_t)(c[j] << 4) / 16.0f;
+                out[(j + D / 2) * PAGE + t] = (float)(c[j] >> 4);
+            }
+        }
+    }
+}
+
 struct Cache {
     uint8_t* base;
     i64 bs, hs;
@@ -251,14 +268,14 @@ void decode(const float* q, float* out, const Cache& c, const int32_t* seq_lens,
             const i64 row0 = ((i64)s * c.hkv + h) * G;                    // first q / out row of this kv head
             std::vector<float> codes((size_t)PAGE * D), o((size_t)G * D, 0.0f), p((size_t)G * PAGE);
             std::vector<float> m(G, -INFINITY), l(G, 0.0f), vbs(G, 0.0f);
-            float qs[D], ksv[D], kbv[D], vsv[PAGE], vbv[PAGE];
+            float ksv[D], kbv[D], vsv[PAGE], vbv[PAGE];
             const float* tail = c.tail(s, h, D);
             for (int pg = 0; pg < full + (tn > 0 ? 1 : 0); ++pg) {
                 const bool part = pg == full;
                 const int cnt = part ? tn : PAGE;
                 const uint8_t* rec = c.rec(s, pg, h);
                 if (!part) {
-                    read_codes<D, BITS>(rec, false, PAGE, codes.data());
+                    read_k_codes_by_dim<D, BITS>(rec, codes.data());
                     for (int d = 0; d < D; ++d) {
                         ksv[d] = get_half(rec + R::KS + 2 * d);
                         kbv[d] = get_half(rec + R::KB + 2 * d);
@@ -268,17 +285,14 @@ void decode(const float* q, float* out, const Cache& c, const int32_t* seq_lens,
                     const float* qg = q + (row0 + g) * D;
                     float* pg_ = p.data() + (size_t)g * PAGE;
                     if (!part) {                                       // K scales folded into q
-                        float bias = 0.0f;
-                        for (int d = 0; d < D; ++d) {
-                            qs[d] = qg[d] * ksv[d];
+                        float bias = 0.0f, acc[PAGE] = {};
+                        for (int d = 0; d < D; ++d) {                  // each token's sum over d in order,
+                            const float w = qg[d] * ksv[d];            // 32 tokens side by side
+                            const float* col = codes.data() + (size_t)d * PAGE;
+                            for (int t = 0; t < PAGE; ++t) acc[t] += w * col[t];
                             bias += qg[d] * kbv[d];
                         }
-                        for (int t = 0; t < PAGE; ++t) {
-                            const float* ct = codes.data() + (size_t)t * D;
-                            float acc = 0.0f;
-                            for (int d = 0; d < D; ++d) acc += qs[d] * ct[d];
-                            pg_[t] = (acc + bias) * scale;
-                        }
+                        for (int t = 0; t < PAGE; ++t) pg_[t] = (acc[t] + bias) * scale;
                     } else {                                           // exact K rows from the tail
                         for (int t = 0; t < cnt; ++t) {
                             const float* kt = tail + (i64)t * D;
