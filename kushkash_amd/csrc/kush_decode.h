@@ -1112,13 +1112,15 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
         __syncthreads();
         KUSH_MARK(1);
         KUSH_ISSUE_PAIR(sl0, sl1, pa)
-        if constexpr (!ROT) KUSH_ISSUE_PAIR(sl2, sl3, pb)
-        if constexpr (DEP == 3) KUSH_ISSUE_PAIR(sl4, sl5, pc)
+        // the tail's slices between the first pair and the rest: the first step's wait (the later
+        // pairs outstanding) then completes exactly the first pair and the slices, as with ROT
         if (!ROT && TPRE && has_tail) {
             kpk.load(ktail);
             qpk.load(qg + qbase + (int64_t)min(r16, Gc - 1) * D + sdim);
             tpre = true;
         }
+        if constexpr (!ROT) KUSH_ISSUE_PAIR(sl2, sl3, pb)
+        if constexpr (DEP == 3) KUSH_ISSUE_PAIR(sl4, sl5, pc)
         if constexpr (ROT) {                                             // rotate, round to IN, regather
             float* const qst = reinterpret_cast<float*>(ringB);          // [16][D]
 #pragma unroll
