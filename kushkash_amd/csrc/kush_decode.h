@@ -369,12 +369,15 @@ __device__ __forceinline__ void issue_page(uint8_t* dst, bool valid, int blk, co
     const u4 rsrc = u4{(uint32_t)rec, (uint32_t)(rec >> 32) & 0xFFFFu, valid ? (uint32_t)F::REC : 0u, 0x00020000u};
     const uint32_t lds = (uint32_t)(uintptr_t)(lds_void*)dst;
     // m0 is reserved by the compiler; nothing else in the decode kernels uses it (checked on their
-    // assembly by tests/test_isa.py), so setting it here is safe
+    // assembly by tests/test_isa.py), so setting it here is safe. An LDS DMA reads m0 one wait state
+    // after a scalar write of it at the earliest (the compiler puts one between its own m0 writes and
+    // LDS DMAs, and cannot see inside this asm), hence the s_nop: without it the load can take the
+    // previous m0, the previous chunk's LDS address, depending on how the two instructions issue.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 #pragma unroll
     for (int i = 0; i < R::DMA; ++i)
-        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                      :: "s"(lds + R::chunk0(i) * 16), "v"(voff[i]), "s"(rsrc) : "memory", "m0");
 #pragma clang diagnostic pop
 }
@@ -631,7 +634,9 @@ template <typename IN, int N>
 struct Packed {
     static constexpr int BYTES = N * (int)sizeof(IN), WORDS = BYTES / 4;
     static_assert(BYTES % 16 == 0 || BYTES == 8, "16-byte pieces, or one 8-byte piece");
-    uint32_t wd[WORDS];
+    // zero at first: set() of a half-width element keeps the other half of its word, which must
+    // then be a defined value (an uninitialized one lets the optimizer fold the word away)
+    uint32_t wd[WORDS] = {};
     __device__ __forceinline__ void load(const IN* p) {          // p aligned to min(16, BYTES)
         if constexpr (BYTES % 16 == 0) {
 #pragma unroll

@@ -3,7 +3,9 @@
 The page loop issues its buffer-to-LDS loads in asm, out of the compiler's sight, and waits for
 them with explicit vmcnt counts; the asm sets m0, which the compiler reserves. That is sound only
 while (1) nothing else in these kernels reads m0 (no movrel / gpr-index instructions, every write
-of m0 is the one our load sequence makes) and (2) the compiler inserts no LDS-DMA of its own."""
+of m0 is the one our load sequence makes), (2) each m0 write is separated from the LDS DMA that
+reads it by one wait state (the compiler's own LDS DMAs keep that distance; it cannot add it inside
+the asm) and (3) the compiler inserts no LDS-DMA of its own."""
 import re
 import shutil
 import subprocess
@@ -60,16 +62,18 @@ def test_m0_is_only_the_lds_load_base(asm):
             assert not re.match(r"(v_movrel|s_movrel|s_set_gpr_idx|v_interp|ds_gws|s_sendmsg)", ins), (name, ins)
             if "m0" in ins:
                 assert re.match(r"s_mov_b32 m0, s\d+$", ins), (name, ins)
-                nxt = next(l for l in lines[i + 1:] if l)
-                assert re.match(r"buffer_load_dwordx4 v\d+, s\[\d+:\d+\], 0 offen lds$", nxt), (name, nxt)
+                # one wait state between the m0 write and the LDS DMA that reads it, then the DMA
+                nxt = [l for l in lines[i + 1:i + 4] if l]
+                assert nxt[0] == "s_nop 0", (name, nxt[0])
+                assert re.match(r"buffer_load_dwordx4 v\d+, s\[\d+:\d+\], 0 offen lds$", nxt[1]), (name, nxt[1])
 
 
 def test_every_lds_load_is_ours(asm):
     for name, lines in kernels(asm).items():
         for i, ins in enumerate(lines):
             if ins.endswith(" lds") or "_lds_" in ins:
-                prev = [l for l in lines[:i] if l][-1]
-                assert prev.startswith("s_mov_b32 m0,"), (name, prev, ins)
+                prev = [l for l in lines[:i] if l][-2:]
+                assert prev[0].startswith("s_mov_b32 m0,") and prev[1] == "s_nop 0", (name, prev, ins)
 
 
 def test_split_merge_is_device_scope_accesses_without_cache_maintenance(asm):
