@@ -1196,9 +1196,12 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
             const uint8_t* const sp[2] = {SA, SB};                                                 \
             float sv[2][8], kx[2];                                                                 \
             pair_scores<D, BITS, QLO>(SA, qa, qla, qh, ql, sv, kx, rs, lane);                      \
-            if (2 * (P) + 1 >= wn) {                                                               \
-                _Pragma("unroll") for (int jj = 0; jj < 8; ++jj) sv[1][jj] = -__builtin_inff();    \
-            }                                                                                      \
+            /* page B masked without a branch: a uniform branch here put the reads of the last  */ \
+            /* bias MFMA's results (kx) 3 wait states after it on the taken path (8 needed), a  */ \
+            /* join the compiler's hazard check does not cover (tests/test_isa.py checks every  */ \
+            /* path)                                                                            */ \
+            const float pbm = 2 * (P) + 1 >= wn ? -__builtin_inff() : 0.0f;                        \
+            _Pragma("unroll") for (int jj = 0; jj < 8; ++jj) sv[1][jj] += pbm;                     \
             id2 = *reinterpret_cast<const int2*>(tb + min(2 * nx, TW - 2));                        \
             consume_pages<D, BITS, 2>(sp, o, vacc, sv, sa, kx, m_run, l_run, vb_run, lane);        \
         }                                                                                          \
@@ -1303,6 +1306,11 @@ __global__ __launch_bounds__(NW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) 
     }
 
     if constexpr (WS) {                                          // the wave's last split, folded in last
+        // The fold reuses registers the partial page's last MFMAs still write, behind a uniform branch:
+        // on its taken path the compiler kept 7 wait states after them (8 needed), a join its hazard
+        // check does not cover. Nothing sinks below this point, and 8 wait states follow it.
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_nop 7");
         if (KW > 1) {
             folded.fold(o, vacc, m_run, l_run, vb_run, false);
             folded.restore(o, vacc, m_run, l_run, vb_run);
