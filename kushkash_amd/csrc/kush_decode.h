@@ -460,9 +460,10 @@ __device__ __forceinline__ void pair_scores(const uint8_t* s0, const h8 (&qa)[D 
 // Scores of a staged pair (page A at s0, page B in the next slot) for this lane's column: sv[j] for
 // token tok(q, j) of its page, x = a sv[j] + kx. The Q' operand is built once for both pages (each
 // column from its own page's scales); K of page A and of page B each meet it in their own MFMAs,
-// and a column keeps the product with its page. Q' = fp16(q' ks), one rounding of the product, as
-// the reference's tensor-core path (G <= 8) forms its operand (gpu.mojo:660-675); fp32 q adds the
-// residual of that product (plus its low part ql times ks) as a second operand.
+// and a column keeps the product with its page. Q' enters as the fp16 pair qp + qr: qp = fp16(q' ks),
+// the operand the reference's tensor-core path (G <= 8) forms (gpu.mojo:660-675, rounded twice
+// there), and qr the residual of that product (plus q's low part ql times ks for fp32 q), in a
+// second MFMA, so the scores are fp32-grade here as in the one-stream form.
 template <int D, int BITS, bool QLO>
 __device__ __forceinline__ void pair_scores2(const uint8_t* s0, const h8 (&qa)[D / 32], const h8 (&qla)[D / 32],
                                              const h8 (&qh)[D / 32], const h8 (&ql)[D / 32], float (&sv)[8],
@@ -484,10 +485,13 @@ __device__ __forceinline__ void pair_scores2(const uint8_t* s0, const h8 (&qa)[D
     for (int kk = 0; kk < KSTEPS; ++kk) {
         const int d0 = kdim<D, BITS>(kk, q, 0);
         const h8 ks8 = *reinterpret_cast<const h8*>(mine + F::OFF_KS + 2 * d0);
-        // Q' = fp16(q' ks), rounded once (the reference's tensor-core form); fp32 q adds a residual operand
+        // Q' as an fp16 pair: qp = fp16(q' ks) and qr, the residual of that product (plus ql ks for
+        // fp32 q), so the scores carry no fp16 rounding of Q'. With qp alone (the reference's
+        // tensor-core operand, which it rounds twice) a few outputs in a thousand exceeded 2e-3
+        // plus their own rounding; the residual's MFMAs cost C2 ~0.5 us of 31.7.
         const h8 qp = qa[kk] * ks8;
-        h8 qr{};
-        if constexpr (QLO) qr = __builtin_elementwise_fma(qla[kk], ks8, __builtin_elementwise_fma(qa[kk], ks8, -qp));
+        h8 qr = __builtin_elementwise_fma(qa[kk], ks8, -qp);
+        if constexpr (QLO) qr = __builtin_elementwise_fma(qla[kk], ks8, qr);
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
             h8 a[2];
@@ -506,10 +510,8 @@ __device__ __forceinline__ void pair_scores2(const uint8_t* s0, const h8 (&qa)[D
             }
             sacc[p][0] = mfma16(a[0], qp, sacc[p][0]);
             sacc[p][1] = mfma16(a[1], qp, sacc[p][1]);
-            if constexpr (QLO) {
-                sacc[p][0] = mfma16(a[0], qr, sacc[p][0]);
-                sacc[p][1] = mfma16(a[1], qr, sacc[p][1]);
-            }
+            sacc[p][0] = mfma16(a[0], qr, sacc[p][0]);
+            sacc[p][1] = mfma16(a[1], qr, sacc[p][1]);
         }
         const h8 b8 = *reinterpret_cast<const h8*>(brow + 2 * d0);
         bacc = mfma16(b8, qh[kk], bacc);
